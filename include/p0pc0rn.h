@@ -1,0 +1,181 @@
+/*
+ * p0pc0rn.h - C ABI of the MI355X (gfx950) int4 quantized-matmul library.
+ *
+ * This is the boundary the Node.js host (p0pc0rn_amd/js) binds through its N-API addon, and that Python binds
+ * through ctypes. Every entry point takes plain pointers, sizes and enums; no torch or HIP types appear in the
+ * signatures (streams are passed as opaque `void*`).
+ *
+ * The entry points replace the WebGPU dispatch underneath these reference functions (paths are relative to the
+ * reference repository ArtistJoshHughes/p0pc0rn):
+ *   p0_open / p0_close / p0_device_info  <- createGpu / Gpu.init / Gpu.describe   engine/core/gpu.js:18-78
+ *   p0_buffer / p0_free                  <- Gpu.buffer / Gpu.free                 engine/core/gpu.js:81-95
+ *   p0_upload / p0_read                  <- Gpu.upload / Gpu.read / readInto      engine/core/gpu.js:98-140
+ *   p0_done                              <- Gpu.done                              engine/core/gpu.js:141-147
+ *   p0_q4_gemv                           <- gemv(g, a)                            engine/llm/lops.js:108-141
+ *   p0_q4_gemvM                          <- gemvM(g, a)                           engine/llm/lops_spec.js:159-191
+ *   p0_q4_gemm                           <- gemm(gpu, a)                          engine/ops/gemm.js:255-322
+ *   p0_q4_dequant                        <- the q4g32a.t64 unpacking of            engine/kcheck.js:22-38 (packQ4 deq),
+ *                                           engine/ops/gemm.js:139-149 (fp16 tile) and engine/core/store.js:276-301
+ *
+ * Error behaviour: every function returns P0_OK (0) or a nonzero status. On failure, p0_last_error() returns the
+ * message of the calling thread's last failure. Argument errors carry the reference's own text (for example
+ * "gemv: N % 64" or "gemm: K must be a multiple of 32"), so a host shim can rethrow them as `new Error(msg)`
+ * exactly where the reference throws. Argument validation runs before any device work, so it needs no GPU.
+ *
+ * Threading and streams: one library context per process, on the device given to p0_open. Ops are enqueued on the
+ * library's current stream (p0_set_stream, default: a stream created by p0_open) and return immediately; p0_done
+ * waits for them. The split-K workspace is shared by all ops of the context, so ops must not run concurrently on two
+ * streams of one context.
+ */
+#ifndef P0PC0RN_H
+#define P0PC0RN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------------------------------------------------- */
+enum {
+  P0_OK = 0,
+  P0_EINVAL = 1,   /* argument validation failed (the reference throws Error) */
+  P0_EHIP = 2,     /* the HIP runtime reported an error */
+  P0_ENODEV = 3,   /* no context (p0_open not called) or no gfx950 device */
+  P0_ENOMEM = 4    /* device allocation failed */
+};
+
+/* ---- enums mirroring the reference's string options ------------------------------------------------------------ */
+enum { P0_ENC_Q4G32A_T64 = 1, P0_ENC_Q8G64S_T64 = 2, P0_ENC_F16 = 3 };             /* a.w.enc */
+enum { P0_PRO_RAW = 0, P0_PRO_RMS = 1, P0_PRO_SUM = 2, P0_PRO_PLEG = 3 };           /* gemv / gemvM a.pro */
+enum { P0_EPI_STORE = 0, P0_EPI_GEGLU = 1, P0_EPI_SOFTCAP = 2 };                    /* gemv / gemvM a.epi */
+enum { P0_XMODE_F16 = 0, P0_XMODE_LNMOD = 1, P0_XMODE_RMS = 2, P0_XMODE_BF16 = 3 }; /* gemm a.x.mode */
+enum { P0_GEPI_F16 = 0, P0_GEPI_F32 = 1, P0_GEPI_RESADD = 2, P0_GEPI_SWIGLU = 3, P0_GEPI_BIAS = 4 }; /* gemm a.epi */
+enum { P0_ACT_SILU = 0, P0_ACT_GELU = 1 };                                          /* gemm a.act (swiglu) */
+
+/* ---- device / buffers ------------------------------------------------------------------------------------------ */
+const char* p0_last_error(void);
+int p0_version(void);                          /* library ABI version (P0_ABI_VERSION) */
+#define P0_ABI_VERSION 1
+
+typedef struct {
+  char name[64];          /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  int device;
+  int cu_count;
+  int xcd_count;          /* 8 on MI355X (derived: cu_count / 32) */
+  int64_t hbm_bytes;
+  int64_t lds_bytes_per_cu;
+  int clock_khz;
+  int64_t workspace_bytes;
+} p0_device_info_t;
+
+int p0_open(int device);                       /* selects the device, checks gfx950, creates the stream + workspace */
+int p0_close(void);
+int p0_device_info(p0_device_info_t* out);
+int p0_set_stream(void* stream);               /* hipStream_t as void*; NULL = the library's own stream */
+void* p0_get_stream(void);
+
+int p0_buffer(size_t bytes, void** out);       /* device allocation, size rounded up to 16 B (Gpu.buffer) */
+int p0_free(void* buf);
+int p0_upload(void* dst, size_t dst_off, const void* src, size_t bytes);   /* host -> device, ordered on the stream */
+int p0_read(void* host_dst, const void* src, size_t src_off, size_t bytes); /* device -> host; waits for the stream */
+int p0_fill(void* dst, size_t dst_off, uint32_t value, size_t words);       /* 32-bit pattern fill (NaN-fill checks) */
+int p0_done(void);                             /* wait for every op enqueued on the stream */
+
+/* Event timing on the current stream (for benchmarks): p0_timer_start records a start event, p0_timer_stop records a
+ * stop event, waits for it and returns the elapsed milliseconds. */
+int p0_timer_start(void);
+int p0_timer_stop(float* ms);
+
+/* ---- q4g32a.t64 GEMV: y = x W^T for ONE row (engine/llm/lops.js:108-141) ---------------------------------------- */
+/* Buffers are base pointers; offsets use the reference's units (w_off bytes, the rest in floats). */
+typedef struct {
+  const void* w;       /* a.w.buf */
+  int64_t w_off;       /* a.w.off, bytes (multiple of 4; 16 on this build's fast path) */
+  int32_t w_enc;       /* a.w.enc */
+  int64_t w_rows;      /* a.w.rows */
+  int64_t w_cols;      /* a.w.cols: groups per weight row = w_cols / 32 */
+  const float* x;      /* a.x.buf */
+  int64_t x_rowB;      /* a.x.rowB (floats) */
+  int64_t N, K;        /* a.N (output rows; for geglu the gate rows), a.K */
+  int64_t kPer;        /* a.kPer (0 = none) */
+  int32_t pro, epi;    /* a.pro, a.epi */
+  float* y;            /* a.y.buf */
+  int64_t ldy;         /* a.ldy (0 = N) */
+  const float* stat;   /* a.stat.buf (rms) */
+  int64_t stat_off;    /* a.stat.off (floats) */
+  const float* norm;   /* a.norm.buf (rms) */
+  int64_t norm_off;    /* a.norm.off (floats) */
+  int64_t src_n;       /* a.src.n (sum / pleg: number of producer partials) */
+  int64_t src_ld;      /* a.src.ld (floats between partials) */
+  const float* ev;     /* a.ev.buf (pleg) */
+  int64_t ev_off;      /* a.ev.off (floats) */
+  float* mx;           /* a.mx.buf (softcap: [N/64][2] max, bitcast index) */
+  float cap;           /* a.cap (0 = 30) */
+} p0_gemv_args_t;
+int p0_q4_gemv(const p0_gemv_args_t* a, int32_t* nsplit_out);
+
+/* ---- q4g32a.t64 GEMV-M: y[m] = x[m] W^T for M rows, weights read once (engine/llm/lops_spec.js:159-191) ---------- */
+typedef struct {
+  const void* w; int64_t w_off; int32_t w_enc; int64_t w_rows, w_cols;
+  const float* x;      /* a.x.buf */
+  int64_t x_ldx;       /* a.x.ldx (0 = K) */
+  int64_t x_rowB;      /* a.x.rowB */
+  int64_t M, N, K, kPer;
+  int32_t pro, epi;    /* raw | rms | pleg ; store | geglu | softcap */
+  float* y;
+  int64_t y_ldy;       /* a.y.ldy (0 = M * ldm): floats between splits */
+  int64_t y_ldm;       /* a.y.ldm (0 = N): floats between rows */
+  const float* stat; int64_t stat_off, stat_ld;   /* rms: rstd of row m at stat[stat_off + m * stat_ld] (ld 0 = 2) */
+  const float* norm; int64_t norm_off;
+  int64_t src_n, src_ld;                          /* pleg partials (src_n 0 = 1) */
+  const float* ev; int64_t ev_off, ev_ld;         /* pleg: ev row m at ev_off + m * ev_ld */
+  float* mx;                                      /* softcap: [M][N/64][2] */
+  float cap;
+} p0_gemvm_args_t;
+int p0_q4_gemvM(const p0_gemvm_args_t* a, int32_t* nsplit_out);
+
+/* ---- q4g32a.t64 dequant-GEMM on MFMA: Y[m,n] = sum_k X'[m,k] * fl16(deq(W[n,k])) (engine/ops/gemm.js:255-322) --- */
+typedef struct {
+  const void* w; int64_t w_off; int32_t w_enc; int64_t w_rows, w_cols;
+  const void* x;       /* a.x.buf */
+  int64_t x_off;       /* a.x.off (bytes) */
+  int64_t x_ld;        /* a.x.ld (elements; 0 = K) */
+  int64_t x_k0;        /* a.x.k0 */
+  int32_t x_mode;      /* a.x.mode: f16 | lnmod | rms (| bf16: this build's bf16 activations, converted to fp16) */
+  int64_t M, N, K;
+  int64_t wr0, wr1, wk0;   /* first weight row, swiglu 'up' first row, first weight k column */
+  int32_t epi;
+  void* y; int64_t y_off /* bytes */, y_ld /* elements, 0 = N */, y_n0;
+  const float* ev; int64_t ev_off;            /* resadd gate / bias vector (floats) */
+  const float* stats; int64_t stats_off;      /* lnmod / rms: (mean, rstd) pairs per row, off in rows */
+  const float* pv; int64_t pv_off, pv_stride; /* lnmod: scale at pv_off, shift at pv_off + pv_stride (u32 wrap); rms: weight */
+  const float* bv; int64_t bv_off, bv_up;     /* bias vector (resadd / swiglu: gate at bv_off, up at bv_off + bv_up) */
+  int32_t act;         /* swiglu activation */
+  int32_t store;       /* resadd: 1 = Y = gate * (acc + bias) instead of += */
+  int32_t res;         /* bias: 1 = add the previous Y in place */
+} p0_gemm_args_t;
+int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out);
+
+/* ---- bit-exact dequant of whole q4g32a.t64 weights --------------------------------------------------------------- */
+/* out32 (may be NULL): fl32(q * scale + min), row-major [N][K]; out16 (may be NULL): fl16 of that, the GEMM tile value. */
+int p0_q4_dequant(const void* w, int64_t w_off, int64_t N, int64_t K, float* out32, uint16_t* out16);
+
+/* ---- tuning knobs (the analogue of the reference's per-device kernel picks, engine/llm/lopsx.js:317-321) ---------- */
+/* knob 0: workgroups a GEMV call aims for before it splits K across workgroups (default 2048);
+ * knob 1: output tiles from which a GEMV wave streams two tiles (default 1024). value <= 0 only queries.
+ * Returns the previous value, or -1 for an unknown knob. */
+int p0_gemv_tune(int knob, int value);
+
+/* ---- synthetic weights on the device (the reference's GPU filler, engine/tune/autotune.js:73-87) ----------------- */
+/* Symmetric BASELINE records: codes uniform in [0,16) (= q + 8 for q uniform in [-8, 8)), scale = fl16(|N(0, sigma)|),
+ * min = -8 * scale; counter-based hash of (seed, index), so any sub-range is reproducible. */
+int p0_fill_q4_sym(void* w, int64_t w_off, int64_t N, int64_t K, uint32_t seed, float sigma);
+/* fp16 N(0,1)-shaped activations (hash-based Box-Muller), fp32 or fp16 output */
+int p0_fill_randn(void* dst, int64_t off_bytes, int64_t n, uint32_t seed, float sigma, int32_t as_f16);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* P0PC0RN_H */

@@ -1,0 +1,60 @@
+// common.hpp - shared state and helpers of the gfx950 q4 matmul library (see include/p0pc0rn.h for the C ABI).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/p0pc0rn.h"
+
+namespace p0 {
+
+// The per-process library context: one device, one current stream, one split-K workspace.
+struct Ctx {
+  int device = -1;
+  hipStream_t own = nullptr;   // created by p0_open
+  hipStream_t cur = nullptr;   // where ops are enqueued (own unless p0_set_stream)
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  // split-K workspace: partial sums of the K-slices of a call, and one arrival counter per (split, tile block).
+  // Counters start at zero (cleared once by p0_open) and the last workgroup to arrive resets its counter, so every
+  // call leaves them at zero again: no memset per call, which also keeps calls capturable into HIP graphs.
+  float* part = nullptr;
+  size_t part_floats = 0;
+  unsigned* counters = nullptr;
+  size_t n_counters = 0;
+  int cu_count = 0;
+  hipDeviceProp_t prop{};
+};
+Ctx& ctx();
+
+// Thread-local message of the last failure (p0_last_error).
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
+inline int fail_hip(hipError_t e, const char* what) {
+  set_error("%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+  return P0_EHIP;
+}
+inline int require_open(const char* op) {
+  if (ctx().device < 0) {
+    set_error("%s: no device (p0_open was not called)", op);
+    return P0_ENODEV;
+  }
+  return P0_OK;
+}
+
+#define P0_HIP(call, what)                         \
+  do {                                             \
+    hipError_t e_ = (call);                        \
+    if (e_ != hipSuccess) return fail_hip(e_, what); \
+  } while (0)
+
+// Kernel launches report configuration errors through hipGetLastError; asynchronous faults surface at p0_done.
+#define P0_LAUNCHED(what)                          \
+  do {                                             \
+    hipError_t e_ = hipGetLastError();             \
+    if (e_ != hipSuccess) return fail_hip(e_, what); \
+  } while (0)
+
+}  // namespace p0

@@ -1,0 +1,184 @@
+// runtime.hip - device context, buffers, stream and timing: the part of the reference's Gpu object
+// (engine/core/gpu.js:18-147) that the q4 ops need, on one gfx950 device.
+#include "common.hpp"
+
+#include <cstring>
+
+namespace p0 {
+
+Ctx& ctx() {
+  static Ctx c;
+  return c;
+}
+
+static thread_local std::string g_err;
+
+void set_error(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+}
+
+// 32-bit pattern fill (the NaN-fill that proves a kernel wrote its output, engine/tune/autotune.js:1-7)
+__global__ void fill_u32_kernel(uint32_t* __restrict__ p, uint32_t v, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x, stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) p[i] = v;
+}
+
+}  // namespace p0
+
+using namespace p0;
+
+// Split-K workspace held by the context: 64 MiB of partial sums and 1 Mi arrival counters.
+static constexpr size_t kPartBytes = 64ull << 20;
+static constexpr size_t kCounters = 1ull << 20;
+
+extern "C" {
+
+const char* p0_last_error(void) { return g_err.c_str(); }
+int p0_version(void) { return P0_ABI_VERSION; }
+
+int p0_open(int device) {
+  Ctx& c = ctx();
+  if (c.device >= 0) {
+    if (c.device == device) return P0_OK;
+    set_error("p0_open: already open on device %d", c.device);
+    return P0_EINVAL;
+  }
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= device || device < 0) {
+    set_error("p0_open: no HIP device %d (%d visible)", device, e == hipSuccess ? n : 0);
+    return P0_ENODEV;
+  }
+  P0_HIP(hipSetDevice(device), "p0_open");
+  P0_HIP(hipGetDeviceProperties(&c.prop, device), "p0_open");
+  if (std::strncmp(c.prop.gcnArchName, "gfx950", 6) != 0) {
+    set_error("p0_open: device %d is %s; this library is built for gfx950 (MI355X) only", device, c.prop.gcnArchName);
+    return P0_ENODEV;
+  }
+  P0_HIP(hipStreamCreate(&c.own), "p0_open");   // default priority
+  P0_HIP(hipEventCreate(&c.ev0), "p0_open");
+  P0_HIP(hipEventCreate(&c.ev1), "p0_open");
+  P0_HIP(hipMalloc((void**)&c.part, kPartBytes), "p0_open: workspace");
+  P0_HIP(hipMalloc((void**)&c.counters, kCounters * sizeof(unsigned)), "p0_open: workspace");
+  P0_HIP(hipMemset(c.counters, 0, kCounters * sizeof(unsigned)), "p0_open: workspace");
+  P0_HIP(hipDeviceSynchronize(), "p0_open");
+  c.part_floats = kPartBytes / sizeof(float);
+  c.n_counters = kCounters;
+  c.cur = c.own;
+  c.cu_count = c.prop.multiProcessorCount;
+  c.device = device;
+  return P0_OK;
+}
+
+int p0_close(void) {
+  Ctx& c = ctx();
+  if (c.device < 0) return P0_OK;
+  hipStreamSynchronize(c.own);
+  hipFree(c.part);
+  hipFree(c.counters);
+  hipEventDestroy(c.ev0);
+  hipEventDestroy(c.ev1);
+  hipStreamDestroy(c.own);
+  c = Ctx{};
+  return P0_OK;
+}
+
+int p0_device_info(p0_device_info_t* out) {
+  if (int r = require_open("p0_device_info")) return r;
+  Ctx& c = ctx();
+  std::memset(out, 0, sizeof *out);
+  std::strncpy(out->name, c.prop.gcnArchName, sizeof out->name - 1);
+  out->device = c.device;
+  out->cu_count = c.cu_count;
+  out->xcd_count = c.cu_count / 32;
+  out->hbm_bytes = (int64_t)c.prop.totalGlobalMem;
+  out->lds_bytes_per_cu = (int64_t)c.prop.maxSharedMemoryPerMultiProcessor;
+  out->clock_khz = c.prop.clockRate;
+  out->workspace_bytes = (int64_t)(kPartBytes + kCounters * sizeof(unsigned));
+  return P0_OK;
+}
+
+int p0_set_stream(void* stream) {
+  if (int r = require_open("p0_set_stream")) return r;
+  ctx().cur = stream ? (hipStream_t)stream : ctx().own;
+  return P0_OK;
+}
+void* p0_get_stream(void) { return (void*)ctx().cur; }
+
+int p0_buffer(size_t bytes, void** out) {   // Gpu.buffer: at least 16 B, rounded up to 16 B
+  if (int r = require_open("p0_buffer")) return r;
+  size_t size = bytes < 16 ? 16 : (bytes + 15) / 16 * 16;
+  hipError_t e = hipMalloc(out, size);
+  if (e != hipSuccess) {
+    *out = nullptr;
+    set_error("buffer %zu B: %s", size, hipGetErrorString(e));
+    return P0_ENOMEM;
+  }
+  return P0_OK;
+}
+
+int p0_free(void* buf) {
+  if (int r = require_open("p0_free")) return r;
+  if (!buf) return P0_OK;
+  P0_HIP(hipStreamSynchronize(ctx().cur), "p0_free");   // never free under a running op
+  P0_HIP(hipFree(buf), "p0_free");
+  return P0_OK;
+}
+
+int p0_upload(void* dst, size_t dst_off, const void* src, size_t bytes) {
+  if (int r = require_open("p0_upload")) return r;
+  if (!bytes) return P0_OK;
+  P0_HIP(hipMemcpyAsync((char*)dst + dst_off, src, bytes, hipMemcpyHostToDevice, ctx().cur), "p0_upload");
+  P0_HIP(hipStreamSynchronize(ctx().cur), "p0_upload");   // the host copy may be reused when this returns
+  return P0_OK;
+}
+
+int p0_read(void* host_dst, const void* src, size_t src_off, size_t bytes) {
+  if (int r = require_open("p0_read")) return r;
+  if (!bytes) return P0_OK;
+  P0_HIP(hipMemcpyAsync(host_dst, (const char*)src + src_off, bytes, hipMemcpyDeviceToHost, ctx().cur), "p0_read");
+  P0_HIP(hipStreamSynchronize(ctx().cur), "p0_read");
+  return P0_OK;
+}
+
+int p0_fill(void* dst, size_t dst_off, uint32_t value, size_t words) {
+  if (int r = require_open("p0_fill")) return r;
+  if ((dst_off & 3) || ((uintptr_t)dst & 3)) {
+    set_error("p0_fill: destination must be 4-byte aligned");
+    return P0_EINVAL;
+  }
+  if (!words) return P0_OK;
+  size_t blocks = (words + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx().cur,
+                     (uint32_t*)((char*)dst + dst_off), value, words);
+  P0_LAUNCHED("p0_fill");
+  return P0_OK;
+}
+
+int p0_done(void) {   // Gpu.done: wait for everything enqueued; faults of earlier ops surface here
+  if (int r = require_open("p0_done")) return r;
+  P0_HIP(hipStreamSynchronize(ctx().cur), "p0_done");
+  return P0_OK;
+}
+
+int p0_timer_start(void) {
+  if (int r = require_open("p0_timer_start")) return r;
+  P0_HIP(hipEventRecord(ctx().ev0, ctx().cur), "p0_timer_start");
+  return P0_OK;
+}
+
+int p0_timer_stop(float* ms) {
+  if (int r = require_open("p0_timer_stop")) return r;
+  P0_HIP(hipEventRecord(ctx().ev1, ctx().cur), "p0_timer_stop");
+  P0_HIP(hipEventSynchronize(ctx().ev1), "p0_timer_stop");
+  P0_HIP(hipEventElapsedTime(ms, ctx().ev0, ctx().ev1), "p0_timer_stop");
+  return P0_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,111 @@
+// util.hip - bit-exact q4g32a.t64 dequant and the synthetic-data fillers.
+#include "common.hpp"
+
+namespace p0 {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+// One thread per (row, code word): the 8 weights k = 32 g + 8 w .. + 7 of row n.
+// fl32(q * s + m) as engine/kcheck.js:32 / engine/core/store.js:291 compute it (q * s is exact in f32, so the fused and
+// unfused forms round the same), and fl16 of that as the GEMM tile (engine/ops/gemm.js:147-148).
+__global__ void q4_dequant_kernel(const uint8_t* __restrict__ w, int64_t wG, int64_t N, int64_t K, float* __restrict__ o32,
+                                  uint16_t* __restrict__ o16) {
+  const int64_t words = N * (K / 8);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t n = i / (K / 8), kw = i - n * (K / 8), g = kw >> 2, wd = kw & 3;
+    const uint8_t* rec = w + ((n >> 6) * wG + g) * 1280;
+    const int r = (int)(n & 63);
+    const uint32_t q = *(const uint32_t*)(rec + r * 16 + wd * 4);
+    const h2_t sm = __builtin_bit_cast(h2_t, *(const uint32_t*)(rec + 1024 + r * 4));
+    const float s = (float)sm.x, m = (float)sm.y;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float v = (float)((q >> (4 * j)) & 15u) * s + m;
+      const int64_t o = n * K + kw * 8 + j;
+      if (o32) o32[o] = v;
+      if (o16) o16[o] = __builtin_bit_cast(uint16_t, (_Float16)v);
+    }
+  }
+}
+
+// The PCG RXS-M-XS hash (Jarzynski & Olano, JCGT 2020), as the reference's GPU filler (engine/tune/autotune.js:76).
+__device__ __forceinline__ uint32_t hash32(uint32_t x) {
+  uint32_t v = x * 747796405u + 2891336453u;
+  uint32_t w = ((v >> ((v >> 28) + 4u)) ^ v) * 277803737u;
+  return (w >> 22) ^ w;
+}
+__device__ __forceinline__ double u01(uint32_t h) { return ((double)(h >> 8) + 0.5) * (1.0 / 16777216.0); }
+__device__ __forceinline__ double hnorm(uint32_t idx, uint32_t seed) {   // Box-Muller in float64
+  const double a = u01(hash32((2u * idx) ^ seed)), b = u01(hash32((2u * idx + 1u) ^ seed ^ 0x9E3779B9u));
+  return sqrt(-2.0 * log(a)) * cos(6.283185307179586 * b);
+}
+
+// One thread per u32 of a record: words 0..255 = codes (uniform nibbles), 256..319 = f16(|z| sigma) | f16(-8 s) << 16
+__global__ void fill_q4_sym_kernel(uint32_t* __restrict__ w, int64_t nrec, uint32_t seed, float sigma) {
+  const int64_t words = nrec * 320;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t rc = i / 320;
+    const int j = (int)(i - rc * 320);
+    uint32_t v;
+    if (j < 256) {
+      v = hash32((uint32_t)(rc * 256 + j) ^ seed);
+    } else {
+      const double z = hnorm((uint32_t)(rc * 64 + (j - 256)), seed ^ 0x5bd1e995u);
+      const _Float16 sh = (_Float16)(float)(fabs(z) * (double)sigma);
+      const _Float16 mh = (_Float16)(-8.0f * (float)sh);
+      v = (uint32_t)__builtin_bit_cast(uint16_t, sh) | ((uint32_t)__builtin_bit_cast(uint16_t, mh) << 16);
+    }
+    w[i] = v;
+  }
+}
+
+__global__ void fill_randn_kernel(void* __restrict__ dst, int64_t n, uint32_t seed, float sigma, int as_f16) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const _Float16 h = (_Float16)(float)(hnorm((uint32_t)i, seed) * (double)sigma);
+    if (as_f16) ((uint16_t*)dst)[i] = __builtin_bit_cast(uint16_t, h);
+    else ((float*)dst)[i] = (float)h;
+  }
+}
+
+static unsigned grid_for(int64_t work) {
+  int64_t b = (work + 255) / 256;
+  return (unsigned)(b > 16384 ? 16384 : (b < 1 ? 1 : b));
+}
+
+}  // namespace p0
+
+using namespace p0;
+
+extern "C" int p0_q4_dequant(const void* w, int64_t w_off, int64_t N, int64_t K, float* out32, uint16_t* out16) {
+  if (N <= 0 || N % 64) { set_error("dequant: N %% 64"); return P0_EINVAL; }
+  if (K <= 0 || K % 32) { set_error("dequant: K must be a multiple of 32"); return P0_EINVAL; }
+  if (w_off % 4) { set_error("dequant: weight offset"); return P0_EINVAL; }
+  if (!w || (!out32 && !out16)) { set_error("dequant: missing buffer"); return P0_EINVAL; }
+  if (int r = require_open("dequant")) return r;
+  hipLaunchKernelGGL(q4_dequant_kernel, dim3(grid_for(N * K / 8)), dim3(256), 0, ctx().cur, (const uint8_t*)w + w_off, K / 32,
+                     N, K, out32, out16);
+  P0_LAUNCHED("dequant");
+  return P0_OK;
+}
+
+extern "C" int p0_fill_q4_sym(void* w, int64_t w_off, int64_t N, int64_t K, uint32_t seed, float sigma) {
+  if (N <= 0 || N % 64 || K <= 0 || K % 32) { set_error("fill_q4_sym: N %% 64 and K %% 32 required"); return P0_EINVAL; }
+  if (w_off % 4) { set_error("fill_q4_sym: weight offset"); return P0_EINVAL; }
+  if (!w) { set_error("fill_q4_sym: missing buffer"); return P0_EINVAL; }
+  if (int r = require_open("fill_q4_sym")) return r;
+  const int64_t nrec = (N / 64) * (K / 32);
+  hipLaunchKernelGGL(fill_q4_sym_kernel, dim3(grid_for(nrec * 320)), dim3(256), 0, ctx().cur,
+                     (uint32_t*)((uint8_t*)w + w_off), nrec, seed, sigma);
+  P0_LAUNCHED("fill_q4_sym");
+  return P0_OK;
+}
+
+extern "C" int p0_fill_randn(void* dst, int64_t off_bytes, int64_t n, uint32_t seed, float sigma, int32_t as_f16) {
+  if (!dst || n < 0 || off_bytes % (as_f16 ? 2 : 4)) { set_error("fill_randn: bad destination"); return P0_EINVAL; }
+  if (int r = require_open("fill_randn")) return r;
+  if (!n) return P0_OK;
+  hipLaunchKernelGGL(fill_randn_kernel, dim3(grid_for(n)), dim3(256), 0, ctx().cur, (void*)((uint8_t*)dst + off_bytes), n, seed,
+                     sigma, as_f16);
+  P0_LAUNCHED("fill_randn");
+  return P0_OK;
+}

@@ -1,0 +1,56 @@
+"""GPU checks of the bit-exact dequant (p0_q4_dequant) and the synthetic-data fillers, against the oracle."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from p0pc0rn_amd import capi
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("N,K,w_off", [(128, 256, 0), (192, 96, 4), (64, 2048, 16)])
+def test_dequant_bit_exact(dev, N, K, w_off):
+    """fl32(q s + m) and its fp16 tile value, bit for bit (engine/kcheck.js:32, engine/ops/gemm.js:147-148)"""
+    W = O.randn(N * K, 5 + N, 0.05)
+    W[:K] *= 1e4                      # a row with large values next to tiny ones: wide exponent spreads in one tile
+    b, deq = O.pack_q4(W, N, K)
+    buf = np.zeros(w_off + b.nbytes, np.uint8)
+    buf[w_off:] = b
+    wb = capi.to_device(buf)
+    o32 = capi.Buffer(N * K * 4).fill_u32(0x7FC00000)
+    o16 = capi.Buffer(N * K * 2).fill_u32(0x7E007E00)
+    capi.q4_dequant(wb, N, K, out32=o32, out16=o16, w_off=w_off)
+    g32, g16 = o32.read(np.uint32), o16.read(np.uint16)
+    w32, w16 = O.dequant_q4(b, N, K)
+    assert np.array_equal(g32, w32.view(np.uint32).ravel())
+    assert np.array_equal(g32, deq.view(np.uint32).ravel())
+    assert np.array_equal(g16, w16.ravel())
+    for x in (wb, o32, o16):
+        x.free()
+
+
+def test_fill_q4_sym_matches_oracle(dev):
+    N, K = 256, 512
+    wb = capi.Buffer(N // 64 * K // 32 * 1280)
+    capi.fill_q4_sym(wb, N, K, 1234, 0.02)
+    got = wb.read(np.uint8).reshape(-1, 1280)
+    want = O.fill_q4_sym(N, K, 1234, 0.02).reshape(-1, 1280)
+    assert np.array_equal(got[:, :1024], want[:, :1024])                 # code words: integer hash, exact
+    gs = got[:, 1024:].copy().view(np.uint32).ravel()
+    ws = want[:, 1024:].copy().view(np.uint32).ravel()
+    mismatch = np.count_nonzero(gs != ws)
+    # scales go through float64 log / cos on both sides: libm last-ulp differences may move a rare fp16 rounding
+    assert mismatch <= max(1, gs.size // 10000), mismatch
+    wb.free()
+
+
+def test_fill_randn_matches_oracle(dev):
+    n = 100_000
+    b32, b16 = capi.Buffer(n * 4), capi.Buffer(n * 2)
+    capi.fill_randn(b32, n, 77)
+    capi.fill_randn(b16, n, 77, as_f16=True)
+    w32, w16 = O.fill_randn(n, 77)
+    g32, g16 = b32.read(np.float32), b16.read(np.uint16)
+    assert np.count_nonzero(g16 != w16) <= 10
+    assert np.array_equal(g32.view(np.uint32) == w32.view(np.uint32), g16 == w16)
+    b32.free(); b16.free()
