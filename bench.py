@@ -1,0 +1,347 @@
+#!/usr/bin/env python3
+"""Benchmark of the q4g32a.t64 matmul hot path on one MI355X (BASELINE.json's metric and configs).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemm] [--json-only]
+
+Headline (`value`): tokens/s of the Gemma-4-E2B-shaped decode step at M=1 (config B): 30 layers x {qkv 3072x2048 rms,
+o 2048x2048 raw kPer 2048, gate_up 2x8192x2048 rms+geglu, down 2048x8192 raw kPer 2048} + lm_head 262144x2048
+rms+softcap (tile max/argmax) = 121 GEMV launches, recorded once and replayed per token (the DecodeRunner analogue).
+Attention, norms and the PLE projections are not part of the step.
+
+Also reported: the step's weight-streaming GB/s, config A (one 8192x2048 GEMV, weight ring of 32 copies), the
+verify pass at M = 5 and the M sweep {1, 2, 4, 8, 16} (config C), and the FLUX.2-klein (M=4608, config D) and
+SANA-Video (M=32760, config E) dequant-GEMM TFLOP/s. All weights are synthetic symmetric int4 (codes uniform,
+scale |N(0, 0.02)| fp16, min = -8 scale) filled on the device; activations fp16-valued N(0, 1).
+
+Timing: HIP events on the library's stream around back-to-back replays, inputs already resident in HBM.
+CPU baseline: the oracle's fp32 port of the reference's lgemv kernel (engine/llm/lops.js:60-88) on the host cores,
+over a bounded sample of the same step (one layer + 1/16 of the head), scaled to tokens/s.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBPS = 8000.0        # MI355X HBM3E
+FP16_PEAK_TFLOPS = 2500.0     # MI355X dense fp16 MFMA
+Q4_BYTES_PER_W = 0.625        # 1280 B per 64 rows x 32 k (engine/kcheck.js:23)
+
+D, LAYERS, QKV, MLP, VOCAB = 2048, 30, 3072, 8192, 262144
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Step:
+    """The decode step's weights and buffers (device), and its op sequence for M rows."""
+
+    def __init__(self, capi, seed=0):
+        self.c = capi
+        c = capi
+        self.layers = []
+        for l in range(LAYERS):
+            t = {}
+            for name, (n, k) in (("qkv", (QKV, D)), ("o", (D, D)), ("gu", (2 * MLP, D)), ("down", (D, MLP))):
+                b = c.Buffer(n // 64 * k // 32 * 1280)
+                c.fill_q4_sym(b, n, k, seed * 7919 + l * 16 + len(t), 0.02)
+                t[name] = (b, n, k)
+            self.layers.append(t)
+        self.head = c.Buffer(VOCAB // 64 * D // 32 * 1280)
+        c.fill_q4_sym(self.head, VOCAB, D, seed * 7919 + 999, 0.02)
+        self.weight_bytes = sum(b.nbytes for t in self.layers for (b, n, k) in t.values()) + self.head.nbytes
+        self.nw = c.to_device(np.linspace(0.8, 1.2, D).astype(np.float32))
+        self.M = 0
+
+    def alloc(self, M):
+        """activation buffers for M rows (fp16-valued N(0,1) inputs, rstd slots)"""
+        c = self.c
+        self.M = M
+        self.x = c.Buffer(M * D * 4)
+        c.fill_randn(self.x, M * D, 12345)
+        st = np.zeros(2 * M + 4, np.float32)
+        st[1::2] = 1.0 / np.sqrt(1.0 + 1e-6)
+        self.st = c.to_device(st)
+        self.qkvp = c.Buffer(M * QKV * 4)
+        self.tpart = c.Buffer(4 * M * D * 4)
+        self.mbuf = c.Buffer(M * MLP * 4)
+        self.logits = c.Buffer(M * VOCAB * 4)
+        mx = np.zeros(M * (VOCAB // 64) * 2 + 2 * M + 4, np.float32)
+        mx[M * (VOCAB // 64) * 2 + 1::2] = 1.0
+        self.mx = c.to_device(mx)
+        self.mx_stat_off = M * (VOCAB // 64) * 2 + 1
+
+    def free_acts(self):
+        for b in (self.x, self.st, self.qkvp, self.tpart, self.mbuf, self.logits, self.mx):
+            b.free()
+
+    # one projection, M = 1 through gemv, M > 1 through gemvM (the reference's decode / verify call pairs)
+    def proj(self, w, n, k, x, y, pro="raw", epi="store", kPer=0, stat=None, stat_off=0, mx=None):
+        c, M = self.c, self.M
+        if M == 1:
+            a = c.gemv_args(w=w, w_rows=n if epi != "geglu" else n, w_cols=k, x=x, N=n if epi != "geglu" else n // 2,
+                            K=k, kPer=kPer, pro=c.PRO[pro], epi=c.EPI[epi], y=y, stat=stat, stat_off=stat_off,
+                            norm=self.nw, mx=mx)
+            return c.q4_gemv(a)
+        a = c.gemvm_args(w=w, w_rows=n, w_cols=k, x=x, x_ldx=k, M=M, N=n if epi != "geglu" else n // 2, K=k,
+                         kPer=kPer, pro=c.PRO[pro], epi=c.EPI[epi], y=y, stat=stat, stat_off=stat_off, stat_ld=2,
+                         norm=self.nw, mx=mx)
+        return c.q4_gemvM(a)
+
+    def ops(self, only=None):
+        """enqueue the step (or only one projection kind over all layers)"""
+        for t in self.layers:
+            if only in (None, "qkv"):
+                b, n, k = t["qkv"]
+                self.proj(b, n, k, self.x, self.qkvp, "rms", stat=self.st, stat_off=1)
+            if only in (None, "o"):
+                b, n, k = t["o"]
+                self.proj(b, n, k, self.qkvp, self.tpart, "raw", kPer=2048)
+            if only in (None, "gu"):
+                b, n, k = t["gu"]
+                self.proj(b, n, k, self.x, self.mbuf, "rms", "geglu", stat=self.st, stat_off=1)
+            if only in (None, "down"):
+                b, n, k = t["down"]
+                self.proj(b, n, k, self.mbuf, self.tpart, "raw", kPer=2048)
+        if only in (None, "head"):
+            # the head's rms slot lives in the mx buffer past the tile maxima (engine/llm/gemma4.js:505-508)
+            self.proj(self.head, VOCAB, D, self.x, self.logits, "rms", "softcap", stat=self.mx,
+                      stat_off=self.mx_stat_off, mx=self.mx)
+
+    def step_bytes(self, only=None):
+        M = self.M
+        tot = 0
+        shapes = {"qkv": (QKV, D), "o": (D, D), "gu": (2 * MLP, D), "down": (D, MLP)}
+        for kind, (n, k) in shapes.items():
+            if only in (None, kind):
+                out = (n // 2 if kind == "gu" else n) * (4 if kind == "down" else 1)
+                tot += LAYERS * (n * k * Q4_BYTES_PER_W + M * k * 4 + M * out * 4)
+        if only in (None, "head"):
+            tot += VOCAB * D * Q4_BYTES_PER_W + M * D * 4 + M * VOCAB * 4 + M * (VOCAB // 64) * 8
+        return tot
+
+
+def time_replays(c, rec, warmup, reps):
+    for _ in range(warmup):
+        rec.replay()
+    c.done()
+    c.timer_start()
+    for _ in range(reps):
+        rec.replay()
+    return c.timer_stop() / reps
+
+
+def bench_decode(c, step, steps, warmup):
+    step.alloc(1)
+    rec = c.record(step.ops)
+    ms = time_replays(c, rec, warmup, steps)
+    rec.free()
+    by_kind = {}
+    for kind in ("qkv", "o", "gu", "down", "head"):
+        r = c.record(lambda: step.ops(kind))
+        kms = time_replays(c, r, 3, 20)
+        r.free()
+        launches = 1 if kind == "head" else LAYERS
+        by_kind[kind] = {"ms_total": round(kms, 4), "us_per_launch": round(kms * 1e3 / launches, 2),
+                         "GBps": round(step.step_bytes(kind) / (kms * 1e-3) / 1e9, 1)}
+    out = {"ms": ms, "bytes": step.step_bytes(), "by_kind": by_kind}
+    step.free_acts()
+    return out
+
+
+def bench_verify(c, step, Ms=(1, 2, 4, 5, 8, 16)):
+    res = {}
+    for M in Ms:
+        step.alloc(M)
+        rec = c.record(step.ops)
+        ms = time_replays(c, rec, 3, 10)
+        rec.free()
+        res[str(M)] = {"ms_per_pass": round(ms, 4), "tok_per_s": round(M / (ms * 1e-3), 1),
+                       "GBps": round(step.step_bytes() / (ms * 1e-3) / 1e9, 1)}
+        step.free_acts()
+    return res
+
+
+def bench_config_a(c, reps=8):
+    """one M=1 GEMV N=8192 K=2048 over a ring of 32 weight copies (336 MB > the 256 MB last-level cache)"""
+    N, K, R = 8192, 2048, 32
+    ws = []
+    for i in range(R):
+        b = c.Buffer(N // 64 * K // 32 * 1280)
+        c.fill_q4_sym(b, N, K, i, 0.02)
+        ws.append(b)
+    x = c.Buffer(K * 4)
+    c.fill_randn(x, K, 0)
+    y = c.Buffer(N * 4)
+
+    def ops():
+        for b in ws:
+            c.q4_gemv(c.gemv_args(w=b, w_rows=N, w_cols=K, x=x, N=N, K=K, y=y))
+
+    rec = c.record(ops)
+    ms = time_replays(c, rec, 2, reps) / R
+    rec.free()
+    for b in ws + [x, y]:
+        b.free()
+    byts = N * K * Q4_BYTES_PER_W + K * 4 + N * 4
+    return {"us_per_launch": round(ms * 1e3, 2), "GBps": round(byts / (ms * 1e-3) / 1e9, 1), "bytes": int(byts)}
+
+
+def bench_gemm(c, M, shapes, reps=5):
+    """the dequant-GEMMs of one DiT block at M tokens: bf16 N(0,1) activations (converted to fp16 in-kernel, exact
+    for |x| >= 2^-17), fp16 output"""
+    Kmax = max(k for (_, n, k) in shapes)
+    Nmax = max(n for (_, n, k) in shapes)
+    xf = np.random.default_rng(3).standard_normal(M * Kmax, dtype=np.float32)
+    x = c.to_device((xf.view(np.uint32) >> 16).astype(np.uint16))
+    del xf
+    y = c.Buffer(M * Nmax * 2)
+    ws = []
+    for i, (name, n, k) in enumerate(shapes):
+        b = c.Buffer(n // 64 * k // 32 * 1280)
+        c.fill_q4_sym(b, n, k, 100 + i, 0.02)
+        ws.append((name, b, n, k))
+    res, tot_fl, tot_ms = {}, 0.0, 0.0
+    for name, b, n, k in ws:
+        args = c.gemm_args(w=b, w_rows=n, w_cols=k, x=x, x_ld=k, x_mode=c.XMODE["bf16"], M=M, N=n, K=k,
+                           epi=c.GEPI["f16"], y=y)
+        rec = c.record(lambda: c.q4_gemm(args))
+        ms = time_replays(c, rec, 2, reps)
+        rec.free()
+        fl = 2.0 * M * n * k
+        res[name] = {"ms": round(ms, 4), "TFLOPS": round(fl / (ms * 1e-3) / 1e12, 1)}
+        tot_fl += fl
+        tot_ms += ms
+    for (_, b, _, _) in ws:
+        b.free()
+    x.free()
+    y.free()
+    return {"M": M, "GFLOP": round(tot_fl / 1e9, 2), "ms": round(tot_ms, 4),
+            "TFLOPS": round(tot_fl / (tot_ms * 1e-3) / 1e12, 1),
+            "frac_fp16_peak": round(tot_fl / (tot_ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4), "per_gemm": res}
+
+
+def cpu_baseline(min_seconds=10.0):
+    """the oracle's fp32 port of lgemv (engine/llm/lops.js:60-88) over one layer + 1/16 of the head"""
+    from oracle import oracle as O
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+    shapes = [(QKV, D), (D, D), (2 * MLP, D), (D, MLP)]
+    ws = [(O.fill_q4_sym(n, k, 1 + i, 0.02), n, k) for i, (n, k) in enumerate(shapes)]
+    head_rows = VOCAB // 16
+    hw = O.fill_q4_sym(head_rows, D, 9, 0.02)
+    x = {k: O.fill_randn(k, 5)[0] for k in (D, MLP)}
+    for w, n, k in ws:   # warm-up
+        O.lgemv_f32(w, x[k], n, k, threads)
+    t_layer, t_head, reps, t0 = 0.0, 0.0, 0, time.time()
+    while time.time() - t0 < min_seconds or reps < 2:
+        a = time.perf_counter()
+        for w, n, k in ws:
+            O.lgemv_f32(w, x[k], n, k, threads)
+        b = time.perf_counter()
+        O.lgemv_f32(hw, x[D], head_rows, D, threads)
+        t_layer += b - a
+        t_head += time.perf_counter() - b
+        reps += 1
+    per_token = (t_layer / reps) * LAYERS + (t_head / reps) * 16
+    return {"value": round(1.0 / per_token, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": "oracle lgemv_f32 (the reference lgemv's fp32 order) over one decoder layer's 4 GEMVs + "
+                      "1/16 of the lm_head (16384x2048), %d repetitions in %.1f s; tokens/s = 1 / (30 x layer + "
+                      "16 x head slice)" % (reps, time.time() - t0),
+            "ms_per_token": round(per_token * 1e3, 2)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="decode step only")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU; --gpus %d is not supported (the hot path runs on one MI355X, "
+              "see DESIGN.md for how it would shard)" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    from p0pc0rn_amd import capi as c
+    c.open_device(0)
+    info = c.device_info()
+    log("device", info)
+
+    t0 = time.time()
+    step = Step(c)
+    c.done()
+    log("weights filled: %.2f GB in %.1f s" % (step.weight_bytes / 1e9, time.time() - t0))
+    dec = bench_decode(c, step, args.steps, args.warmup)
+    ms = dec["ms"]
+    tok_s = 1e3 / ms
+    step_gbps = dec["bytes"] / (ms * 1e-3) / 1e9
+    log("decode step: %.4f ms -> %.1f tok/s, %.1f GB/s" % (ms, tok_s, step_gbps), dec["by_kind"])
+
+    extra = {"decode_step": {"ms": round(ms, 4), "algorithmic_bytes": int(dec["bytes"]),
+                             "GBps": round(step_gbps, 1), "frac_hbm_peak": round(step_gbps / HBM_PEAK_GBPS, 4),
+                             "by_projection": dec["by_kind"]}}
+    if not args.no_extra:
+        extra["config_a_gemv"] = bench_config_a(c)
+        log("config A", extra["config_a_gemv"])
+        extra["verify_sweep"] = bench_verify(c, step)
+        log("verify sweep", extra["verify_sweep"])
+    for t in step.layers:
+        for (b, n, k) in t.values():
+            b.free()
+    step.head.free()
+    if not args.no_gemm:
+        extra["gemm_flux2_klein_M4608"] = bench_gemm(
+            c, 4608, [("qkv", 9216, 3072), ("out", 3072, 3072), ("mlp_up", 9216, 3072), ("mlp_down", 3072, 9216)])
+        log("gemm FLUX", extra["gemm_flux2_klein_M4608"])
+        if not args.no_extra:
+            extra["gemm_sana_video_M32760"] = bench_gemm(
+                c, 32760, [("qkv", 9216, 3072), ("glu_up", 16384, 3072), ("down", 3072, 8192)], reps=2)
+            log("gemm SANA", extra["gemm_sana_video_M32760"])
+
+    # the dominant kernel: the gate_up GEMV (mode-2 q4_gemv_kernel, 43% of the step's bytes), back-to-back over the
+    # 30 layers' distinct weights (629 MB > the last-level cache)
+    gu = dec["by_kind"]["gu"]
+    gu_bytes_per_launch = 2 * MLP * D * Q4_BYTES_PER_W + D * 4 + MLP * 4
+    achieved = gu_bytes_per_launch / (gu["us_per_launch"] * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                "kernel": "q4_gemv_kernel<1,2> (gate_up 16384x2048 rms+geglu)",
+                "bytes_per_launch": int(gu_bytes_per_launch), "us_per_launch": gu["us_per_launch"]}
+    prof = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(prof):
+        try:
+            roofline["traffic"] = json.load(open(prof)).get("gate_up_gemv_bytes_per_launch")
+        except Exception:
+            pass
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline()
+        log("cpu baseline", cpu)
+
+    line = {
+        "metric": "int4 GEMV HBM GB/s + decode tok/s (M=1); dequant-GEMM TFLOPS at M=4608",
+        "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "gemma4-e2b-shaped decode step, M=1: 30 x {qkv 3072x2048 rms, o 2048x2048, "
+                               "gate_up 2x8192x2048 rms+geglu, down 2048x8192 kPer 2048} + lm_head 262144x2048 "
+                               "rms+softcap; q4g32a.t64 int4 weights (0.625 B/weight), fp32 accumulate",
+                   "weights_GB": round(step.weight_bytes / 1e9, 3), "launches_per_step": 121,
+                   "gemv_GBps": round(step_gbps, 1),
+                   "gemm_TFLOPS_M4608": extra.get("gemm_flux2_klein_M4608", {}).get("TFLOPS")},
+        "roofline": roofline, "cpu_baseline": cpu, "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

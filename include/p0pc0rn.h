@@ -88,6 +88,15 @@ int p0_done(void);                             /* wait for every op enqueued on 
 int p0_timer_start(void);
 int p0_timer_stop(float* ms);
 
+/* ---- recorded op sequences: the decode-step recorder (engine/llm/drunner.js:1-8, 83-101 DecodeRunner) ------------ */
+/* Between p0_record_begin and p0_record_end the ops called on this thread are recorded (HIP stream capture of the
+ * current stream) instead of run; p0_replay enqueues the whole recorded sequence with one launch. The library's ops
+ * clear nothing with memset and leave their split-K counters at zero, so a recording replays any number of times. */
+int p0_record_begin(void);
+int p0_record_end(void** rec_out);
+int p0_replay(void* rec);
+int p0_record_free(void* rec);
+
 /* ---- q4g32a.t64 GEMV: y = x W^T for ONE row (engine/llm/lops.js:108-141) ---------------------------------------- */
 /* Buffers are base pointers; offsets use the reference's units (w_off bytes, the rest in floats). */
 typedef struct {
@@ -163,9 +172,11 @@ int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out);
 int p0_q4_dequant(const void* w, int64_t w_off, int64_t N, int64_t K, float* out32, uint16_t* out16);
 
 /* ---- tuning knobs (the analogue of the reference's per-device kernel picks, engine/llm/lopsx.js:317-321) ---------- */
-/* knob 0: workgroups a GEMV call aims for before it splits K across workgroups (default 2048);
- * knob 1: output tiles from which a GEMV wave streams two tiles (default 1024). value <= 0 only queries.
- * Returns the previous value, or -1 for an unknown knob. */
+/* knob 0: waves a GEMV call aims for before it splits K (default 2048);
+ * knob 1: output tiles from which a GEMV wave streams two tiles (default 1024);
+ * knob 2: fewest q4 groups a wave streams when K is split (default 2);
+ * knob 3: most waves sharing one tile slot's K range inside a workgroup (default 4, at most 8).
+ * value <= 0 only queries. Returns the previous value, or -1 for an unknown knob. */
 int p0_gemv_tune(int knob, int value);
 
 /* ---- synthetic weights on the device (the reference's GPU filler, engine/tune/autotune.js:73-87) ----------------- */

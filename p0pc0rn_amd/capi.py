@@ -25,6 +25,7 @@ HEADER_SYMBOLS = [
     "p0_last_error", "p0_version", "p0_open", "p0_close", "p0_device_info", "p0_set_stream", "p0_get_stream",
     "p0_buffer", "p0_free", "p0_upload", "p0_read", "p0_fill", "p0_done", "p0_timer_start", "p0_timer_stop",
     "p0_q4_gemv", "p0_q4_gemvM", "p0_q4_gemm", "p0_q4_dequant", "p0_fill_q4_sym", "p0_fill_randn", "p0_gemv_tune",
+    "p0_record_begin", "p0_record_end", "p0_replay", "p0_record_free",
 ]
 
 i64, i32, f32, vp = C.c_int64, C.c_int32, C.c_float, C.c_void_p
@@ -87,6 +88,7 @@ def lib():
             "p0_q4_gemm": [C.POINTER(GemmArgs), C.POINTER(C.c_double)],
             "p0_q4_dequant": [vp, i64, i64, i64, vp, vp], "p0_fill_q4_sym": [vp, i64, i64, i64, C.c_uint32, f32],
             "p0_fill_randn": [vp, i64, i64, C.c_uint32, f32, i32], "p0_gemv_tune": [C.c_int, C.c_int],
+            "p0_record_begin": [], "p0_record_end": [C.POINTER(vp)], "p0_replay": [vp], "p0_record_free": [vp],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -174,6 +176,33 @@ def timer_stop():
     ms = f32()
     check(lib().p0_timer_stop(C.byref(ms)))
     return ms.value
+
+
+class Recording:
+    """A recorded op sequence (p0_record_begin ... p0_record_end), replayed with one launch."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    def replay(self):
+        check(lib().p0_replay(self.handle))
+
+    def free(self):
+        if self.handle:
+            lib().p0_record_free(self.handle)
+            self.handle = None
+
+
+def record(fn):
+    """Record the ops fn() enqueues into a Recording (they do not run now)."""
+    check(lib().p0_record_begin())
+    try:
+        fn()
+    finally:
+        h = vp()
+        rc = lib().p0_record_end(C.byref(h))
+    check(rc)
+    return Recording(h.value)
 
 
 def gemv_tune(knob, value=0):

@@ -42,8 +42,10 @@ struct GemvP {
   const float* EV; int64_t evOff, evLd;
   float* Y; int64_t ldy, ldm;
   float* MX; float cap;
-  int gps;            // groups per K-slice
-  int nks;            // K-slices per split
+  int gps;            // groups per workgroup K-slice
+  int nks;            // workgroup K-slices per split (> 1: cross-workgroup reduction through the workspace)
+  int kw;             // waves per tile slot inside a workgroup (each takes a contiguous share of the K-slice)
+  int tgw;            // tile slots per workgroup (waves = tgw * kw)
   int ntb;            // tile blocks (grid.x)
   int rowsTot;        // rows that carry partials: N, or 2N for a geglu
   float* part; unsigned* cnt;
@@ -71,7 +73,7 @@ struct Rec {
 };
 
 __device__ __forceinline__ Rec load_rec(const GemvP& p, int64_t tile, int g, int lane) {
-  const uint8_t* rec = p.w + (tile * p.wG + g) * 1280;
+  const uint8_t* rec = p.w + (int64_t)__builtin_amdgcn_readfirstlane((int)((tile * p.wG + g) >> 0)) * 1280;
   Rec r;
   r.q = __builtin_nontemporal_load((const u32x4*)(rec + lane * 16));
   r.sm = __builtin_nontemporal_load((const uint32_t*)(rec + 1024 + lane * 4));
@@ -136,58 +138,52 @@ __device__ __forceinline__ void epilogue(const GemvP& p, int split, int m, int t
   }
 }
 
-// MODE 0: one tile per wave; MODE 1: two tiles per wave; MODE 2: geglu (gate tile + its up tile N/64 tiles later)
+// MODE 0: one tile per wave; MODE 1: two tiles per wave; MODE 2: geglu (gate tile + its up tile N/64 tiles later).
+// A workgroup = tgw tile slots x kw waves per slot; it owns the K-slice [g0, g1) of one split, and the kw waves of a
+// slot take contiguous shares of it, reduced through LDS in wave order.
 template <int M, int MODE>
-__global__ __launch_bounds__(256) void q4_gemv_kernel(GemvP p) {
+__global__ __launch_bounds__(512) void q4_gemv_kernel(GemvP p) {
   constexpr int T = MODE == 0 ? 1 : 2;
   constexpr int TPW = MODE == 1 ? 2 : 1;   // distinct output tiles per wave
-  extern __shared__ float smem[];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  extern __shared__ __attribute__((aligned(16))) float smem[];   // 16-byte aligned: ds_read_b128 of x
+  const int tid = threadIdx.x, lane = tid & 63;
+  // wave-uniform indices live in SGPRs: record addresses become a scalar base plus the lane's constant 16-byte offset
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kwv = wv % p.kw, tw = wv / p.kw;
   const int KL = p.gps * 32;
-  float* xs = smem;                  // [M][KL]
-  float* xsum = smem + M * KL;       // [M][gps]
+  float* xs = smem;                    // [M][KL]   x' of the slice, odd k scaled 1/16
+  float* xsum = smem + M * KL;         // [M][gps]  group sums of x'
+  float* red = xsum + M * p.gps;       // [waves][T][64] in-workgroup reduction
   __shared__ int s_last;
 
   const int split = blockIdx.y / p.nks, ks = blockIdx.y - split * p.nks;
   const int k0s = split * p.kPer, k1s = min(p.K, k0s + p.kPer);
   const int gs0 = k0s >> 5, gs1 = k1s >> 5;
   const int g0 = min(gs1, gs0 + ks * p.gps), g1 = min(gs1, g0 + p.gps);
+  const int sub = (g1 - g0 + p.kw - 1) / p.kw;
+  const int wg0 = min(g1, g0 + kwv * sub), wg1 = min(g1, wg0 + sub);   // this wave's share
 
   // tiles of this wave
+  const int slot = blockIdx.x * p.tgw + tw;
   int tile[T];
   if (MODE == 2) {
-    tile[0] = blockIdx.x * 4 + wv;
-    tile[T - 1] = tile[0] + p.NT;
+    tile[0] = slot;
+    tile[T - 1] = slot + p.NT;
   } else {
 #pragma unroll
-    for (int t = 0; t < T; ++t) tile[t] = (blockIdx.x * 4 + wv) * TPW + t;
+    for (int t = 0; t < T; ++t) tile[t] = slot * TPW + t;
   }
   const bool active = tile[0] < p.NT;
 
-  // ---- issue the first three records before staging x (their latency overlaps the prologue)
-  auto tl = [&](int t) -> int64_t { return (MODE == 1 && tile[t] >= p.NT) ? tile[0] : tile[t]; };
-  Rec ra[T], rb[T], rc[T];
-  // refills past the slice's last group re-read that group (an in-bounds load whose value is never used), so every
-  // load is unconditional and the pipeline keeps its registers without merges
-  const int glast = g1 - 1;
-  if (active && g0 < g1) {
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-      ra[t] = load_rec(p, tl(t), g0, lane);
-      rb[t] = load_rec(p, tl(t), min(g0 + 1, glast), lane);
-      rc[t] = load_rec(p, tl(t), min(g0 + 2, glast), lane);
-    }
-  }
-
-  // ---- prologue: x'[m][k] for this K-slice -> LDS (odd k scaled 1/16), then per-group sums of x'
+  // ---- prologue: x'[m][k] for the workgroup's K-slice -> LDS (odd k scaled 1/16), then per-group sums of x'
   const int kb = g0 * 32, ke = g1 * 32;
-  for (int idx = tid; idx < M * KL; idx += 256) {
+  for (int idx = tid; idx < M * KL; idx += blockDim.x) {
     const int m = idx / KL, kl = idx - m * KL, k = kb + kl;
     float v = k < ke ? prologue(p, m, k) : 0.0f;
     xs[idx] = (k & 1) ? v * 0.0625f : v;
   }
   __syncthreads();
-  for (int idx = tid; idx < M * p.gps; idx += 256) {
+  for (int idx = tid; idx < M * p.gps; idx += blockDim.x) {
     const int m = idx / p.gps, gl = idx - m * p.gps;
     const float* xp = xs + m * KL + gl * 32;
     float s = 0.0f;
@@ -197,7 +193,7 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvP p) {
   }
   __syncthreads();
 
-  // ---- stream the records of the slice
+  // ---- stream the records of the wave's share
   float acc[T][M];
 #pragma unroll
   for (int t = 0; t < T; ++t)
@@ -224,28 +220,50 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvP p) {
       }
     }
   };
-  // three records in flight per tile: each buffer is refilled right after it is consumed, so the wait before a
-  // buffer's use covers only its own (oldest) load
+  // Chunks of D groups: all D (x T) records of a chunk are issued, then consumed in order. No load is carried across
+  // the loop's back edge, so the compiler's wait counts stay exact (each consume waits for its own record only; a
+  // rotating pipeline carried across the back edge made the counts collapse to near-full drains). The latency at
+  // the start of each chunk is hidden by the other resident waves. Loads past the share's end re-read its last group
+  // (in bounds, value unused), so every load is unconditional.
+  constexpr int D = MODE == 0 ? 8 : 4;
+  // a wave's second tile past N (odd tile count, MODE 1) re-reads its first tile; its results are never stored
+  auto tl = [&](int t) -> int64_t { return (MODE == 1 && tile[t] >= p.NT) ? tile[0] : tile[t]; };
   if (active) {
-    int g = g0;
-    for (; g + 2 < g1; g += 3) {   // branch-free body: the refills stay where they are issued
-      consume(ra, g);
+    const int glast = wg1 - 1;
+    for (int c0 = wg0; c0 < wg1; c0 += D) {
+      Rec r[D][T];
 #pragma unroll
-      for (int t = 0; t < T; ++t) ra[t] = load_rec(p, tl(t), min(g + 3, glast), lane);
-      consume(rb, g + 1);
+      for (int i = 0; i < D; ++i)
 #pragma unroll
-      for (int t = 0; t < T; ++t) rb[t] = load_rec(p, tl(t), min(g + 4, glast), lane);
-      consume(rc, g + 2);
+        for (int t = 0; t < T; ++t) r[i][t] = load_rec(p, tl(t), min(c0 + i, glast), lane);
 #pragma unroll
-      for (int t = 0; t < T; ++t) rc[t] = load_rec(p, tl(t), min(g + 5, glast), lane);
+      for (int i = 0; i < D; ++i)
+        if (c0 + i < wg1) consume(r[i], c0 + i);
     }
-    if (g < g1) consume(ra, g);
-    if (g + 1 < g1) consume(rb, g + 1);
   }
 
-  // ---- single K-slice: the epilogue straight from registers
+  // ---- the kw waves of a slot: sum their shares in wave order into wave kwv == 0
+  if (p.kw > 1) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < T; ++t) red[(wv * T + t) * 64 + lane] = acc[t][m];
+      __syncthreads();
+      if (kwv == 0) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          float s = 0.0f;
+          for (int j = 0; j < p.kw; ++j) s += red[((wv + j) * T + t) * 64 + lane];
+          acc[t][m] = s;
+        }
+      }
+    }
+  }
+
+  // ---- one workgroup per split: the epilogue straight from registers
   if (p.nks == 1) {
-    if (!active) return;
+    if (!active || kwv != 0) return;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       if (MODE == 2) {
@@ -259,9 +277,12 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvP p) {
     return;
   }
 
-  // ---- several K-slices: partials -> workspace; the last workgroup of (split, tile block) reduces them in order
+  // ---- several workgroups per split: partials -> workspace; the last workgroup of (split, tile block) to arrive
+  // reduces them in K-slice order. One thread fences for the workgroup (a device-scope release / acquire writes back
+  // / invalidates the whole L2 of the XCD, so it is done once, after the barrier that orders every wave's stores).
   const size_t sliceBase = (size_t)(split * p.nks) * M * p.rowsTot;
-  if (active) {
+  const bool owner = active && kwv == 0;
+  if (owner) {
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       const int row = (MODE == 2 && t == 1) ? p.N + tile[0] * 64 + lane : tile[t] * 64 + lane;
@@ -271,18 +292,20 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvP p) {
       }
     }
   }
-  __threadfence();   // release: this thread's partials are visible device-wide (all XCDs) before the arrival count
   __syncthreads();
   if (tid == 0) {
+    __threadfence();   // release: the workgroup's partials reach memory before the arrival count
     unsigned* c = p.cnt + (size_t)split * p.ntb + blockIdx.x;
     const unsigned prev = atomicAdd(c, 1u);
     const int last = prev == (unsigned)(p.nks - 1);
-    if (last) atomicExch(c, 0u);   // leave the counter at zero for the next call
+    if (last) {
+      atomicExch(c, 0u);   // leave the counter at zero for the next call
+      __threadfence();     // acquire: every other workgroup's partials
+    }
     s_last = last;
   }
   __syncthreads();
-  if (!s_last || !active) return;
-  __threadfence();   // acquire: see every other workgroup's partials
+  if (!s_last || !owner) return;
 
 #pragma unroll
   for (int m = 0; m < M; ++m) {
@@ -292,7 +315,7 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(GemvP p) {
       tot[t] = 0.0f;
       const int row = (MODE == 2 && t == 1) ? p.N + tile[0] * 64 + lane : tile[t] * 64 + lane;
       if (MODE != 1 || tile[t] < p.NT) {
-        for (int s = 0; s < p.nks; ++s) tot[t] += __builtin_nontemporal_load(&p.part[sliceBase + ((size_t)s * M + m) * p.rowsTot + row]);
+        for (int s = 0; s < p.nks; ++s) tot[t] += p.part[sliceBase + ((size_t)s * M + m) * p.rowsTot + row];
       }
     }
     if (MODE == 2) {
@@ -338,28 +361,38 @@ static gemv_kernel_t pick(int M, int mode) {
 }
 
 // tuning knobs (the analogue of the reference's per-device picks, engine/llm/lopsx.js:317-321)
-static int g_target_wgs = 2048;   // workgroups a call aims for before it splits K
-static int g_two_tiles_min_nt = 1024;   // output tiles at which a wave takes two tiles
+static int g_target_waves = 2048;       // waves a call aims for before it splits K
+static int g_two_tiles_min_nt = 1024;   // output tiles from which a wave streams two tiles
+static int g_min_gpw = 2;               // fewest q4 groups a wave streams when K is split
+static int g_max_kw = 4;                // most waves that share one tile slot's K-slice inside a workgroup
 
 struct Plan {
-  int mode, gps, nks, ntb, rowsTot;
+  int mode, gps, nks, kw, tgw, ntb, rowsTot, waves;
   size_t lds;
 };
 
 static Plan plan(int M, int NT, int epi, int nsplit, int kPer) {
   Plan pl{};
   pl.mode = epi == P0_EPI_GEGLU ? 2 : (NT >= g_two_tiles_min_nt ? 1 : 0);
-  const int tilesPerWG = pl.mode == 1 ? 8 : 4;
-  pl.ntb = (NT + tilesPerWG - 1) / tilesPerWG;
+  const int T = pl.mode == 0 ? 1 : 2;
+  const int slots = pl.mode == 1 ? (NT + 1) / 2 : NT;
   pl.rowsTot = (epi == P0_EPI_GEGLU ? 2 : 1) * NT * 64;
   const int Gs = kPer / 32;
-  int maxGps = (48 * 1024) / (M * 33 * 4);   // x' + group sums within 48 KB of LDS
-  if (maxGps > 64) maxGps = 64;
-  if (maxGps < 1) maxGps = 1;
-  int nks = (g_target_wgs + pl.ntb * nsplit - 1) / (pl.ntb * nsplit);
-  if (nks < 1) nks = 1;
-  if (nks > Gs) nks = Gs;
+  // K shares per slot and split: enough waves for the chip, but at least g_min_gpw groups each
+  int kws = (g_target_waves + slots * nsplit - 1) / (slots * nsplit);
+  const int kws_max = Gs / g_min_gpw > 1 ? Gs / g_min_gpw : 1;
+  if (kws > kws_max) kws = kws_max;
+  if (kws < 1) kws = 1;
+  pl.kw = kws < g_max_kw ? kws : g_max_kw;
+  pl.tgw = pl.kw >= 4 ? 1 : 4 / pl.kw;                 // 4 waves per workgroup unless kw is larger
+  if (pl.tgw > slots) pl.tgw = slots;
+  pl.waves = pl.tgw * pl.kw;
+  int nks = (kws + pl.kw - 1) / pl.kw;
   int gps = (Gs + nks - 1) / nks;
+  // LDS: x' and its group sums for the slice, plus the reduction rows
+  const size_t red = (size_t)pl.waves * T * 64 * sizeof(float);
+  int maxGps = (int)((48 * 1024 - red) / ((size_t)M * 33 * sizeof(float)));
+  if (maxGps < 1) maxGps = 1;
   if (gps > maxGps) gps = maxGps;
   for (;;) {   // the partials must fit the workspace: coarser slices until they do
     nks = (Gs + gps - 1) / gps;
@@ -368,7 +401,8 @@ static Plan plan(int M, int NT, int epi, int nsplit, int kPer) {
   }
   pl.gps = gps;
   pl.nks = nks;
-  pl.lds = (size_t)M * gps * 33 * sizeof(float);
+  pl.ntb = (slots + pl.tgw - 1) / pl.tgw;
+  pl.lds = (size_t)M * gps * 33 * sizeof(float) + red;
   return pl;
 }
 
@@ -384,13 +418,15 @@ static int launch(GemvP& p, int M, const char* op) {
   }
   p.gps = pl.gps;
   p.nks = pl.nks;
+  p.kw = pl.kw;
+  p.tgw = pl.tgw;
   p.ntb = pl.ntb;
   p.rowsTot = pl.rowsTot;
   p.part = ctx().part;
   p.cnt = ctx().counters;
   gemv_kernel_t k = pick(M, pl.mode);
   dim3 grid((unsigned)pl.ntb, (unsigned)(p.nsplit * pl.nks));
-  hipLaunchKernelGGL(k, grid, dim3(256), pl.lds, ctx().cur, p);
+  hipLaunchKernelGGL(k, grid, dim3(64 * pl.waves), pl.lds, ctx().cur, p);
   P0_LAUNCHED(op);
   return P0_OK;
 }
@@ -496,12 +532,13 @@ extern "C" int p0_q4_gemvM(const p0_gemvm_args_t* a, int32_t* nsplit_out) {
   return P0_OK;
 }
 
-// tuning knobs (benchmark sweeps): 0 = target workgroups before K is split, 1 = tile count from which a wave takes
-// two tiles. Returns the previous value.
+// tuning knobs (benchmark sweeps): 0 = target waves before K is split, 1 = tile count from which a wave takes two
+// tiles, 2 = fewest groups per wave, 3 = most waves per tile slot in a workgroup. Returns the previous value.
 extern "C" int p0_gemv_tune(int knob, int value) {
-  int* t = knob == 0 ? &g_target_wgs : knob == 1 ? &g_two_tiles_min_nt : nullptr;
+  int* t = knob == 0 ? &g_target_waves : knob == 1 ? &g_two_tiles_min_nt : knob == 2 ? &g_min_gpw
+         : knob == 3 ? &g_max_kw : nullptr;
   if (!t) return -1;
   const int old = *t;
-  if (value > 0) *t = value;
+  if (value > 0) *t = knob == 3 && value > 8 ? 8 : value;
   return old;
 }

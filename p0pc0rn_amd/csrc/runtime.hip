@@ -167,6 +167,38 @@ int p0_done(void) {   // Gpu.done: wait for everything enqueued; faults of earli
   return P0_OK;
 }
 
+// ---- recorded op sequences (engine/llm/drunner.js:1-8, 83-101: one decode token recorded once, submitted per token)
+int p0_record_begin(void) {
+  if (int r = require_open("p0_record_begin")) return r;
+  P0_HIP(hipStreamBeginCapture(ctx().cur, hipStreamCaptureModeThreadLocal), "p0_record_begin");
+  return P0_OK;
+}
+
+int p0_record_end(void** out) {
+  if (int r = require_open("p0_record_end")) return r;
+  hipGraph_t graph = nullptr;
+  P0_HIP(hipStreamEndCapture(ctx().cur, &graph), "p0_record_end");
+  hipGraphExec_t exec = nullptr;
+  hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  hipGraphDestroy(graph);
+  if (e != hipSuccess) return fail_hip(e, "p0_record_end: instantiate");
+  *out = (void*)exec;
+  return P0_OK;
+}
+
+int p0_replay(void* rec) {
+  if (int r = require_open("p0_replay")) return r;
+  if (!rec) { set_error("p0_replay: no recording"); return P0_EINVAL; }
+  P0_HIP(hipGraphLaunch((hipGraphExec_t)rec, ctx().cur), "p0_replay");
+  return P0_OK;
+}
+
+int p0_record_free(void* rec) {
+  if (!rec) return P0_OK;
+  P0_HIP(hipGraphExecDestroy((hipGraphExec_t)rec), "p0_record_free");
+  return P0_OK;
+}
+
 int p0_timer_start(void) {
   if (int r = require_open("p0_timer_start")) return r;
   P0_HIP(hipEventRecord(ctx().ev0, ctx().cur), "p0_timer_start");

@@ -168,15 +168,16 @@ def test_gemv_decompositions_agree(dev):
     c = Case(1, 1024, 4096, "raw", "store", kPer=2048, seed=17)
     want = c.run_oracle()[0]
     idx = c.rows_written()
-    old0, old1 = capi.gemv_tune(0), capi.gemv_tune(1)
+    old = [capi.gemv_tune(k) for k in range(4)]
     try:
-        for target, two in [(1, 100000), (64, 8), (100000, 1), (512, 100000)]:
-            capi.gemv_tune(0, target)
-            capi.gemv_tune(1, two)
-            _check(c.run_gpu()[0][idx], want[idx], f"decomposition target {target} two-tiles {two}")
+        for knobs in [(1, 100000, 1, 1), (64, 8, 1, 8), (100000, 1, 1, 2), (512, 100000, 4, 4), (8192, 2, 2, 8),
+                      (4096, 100000, 1, 3)]:
+            for k, v in enumerate(knobs):
+                capi.gemv_tune(k, v)
+            _check(c.run_gpu()[0][idx], want[idx], f"decomposition knobs {knobs}")
     finally:
-        capi.gemv_tune(0, old0)
-        capi.gemv_tune(1, old1)
+        for k, v in enumerate(old):
+            capi.gemv_tune(k, v)
 
 
 def test_gemv_head_shape_softcap(dev):
