@@ -175,9 +175,34 @@ int p0_q4_dequant(const void* w, int64_t w_off, int64_t N, int64_t K, float* out
 /* knob 0: waves a GEMV call aims for before it splits K (default 2048);
  * knob 1: output tiles from which a GEMV wave streams two tiles (default 1024);
  * knob 2: fewest q4 groups a wave streams when K is split (default 2);
- * knob 3: most waves sharing one tile slot's K range inside a workgroup (default 4, at most 8).
+ * knob 3: most waves sharing one tile slot's K range inside a workgroup (default 16, at most 16; 8 when M > 2).
  * value <= 0 only queries. Returns the previous value, or -1 for an unknown knob. */
 int p0_gemv_tune(int knob, int value);
+
+/* ---- GEMV chains: a decode step's GEMVs in ONE persistent launch (engine/llm/drunner.js:1-8, 83-101) ------------- */
+/* Between p0_chain_begin and p0_chain_end, p0_q4_gemv / p0_q4_gemvM calls are validated and planned as usual but
+ * appended to the chain instead of launched (all ops of a chain have the same M). p0_chain_run enqueues the whole
+ * chain as one kernel: op i starts its arithmetic once op i - 1 has written all of its outputs (so op i may read
+ * anything earlier ops wrote), and each workgroup streams op i's first weights while it waits. Buffers are bound at
+ * p0_chain_end; a chain runs any number of times, also inside p0_record_begin / p0_record_end. Every wait is bounded:
+ * a wait that gives up (which needs another kernel holding the GPU's CUs meanwhile) marks the chain, and
+ * p0_chain_status (which waits for the stream) returns 1 once in *timed_out and resets the chain and the split-K
+ * counters; the results of that run are invalid.
+ * Runs of one chain, or of chains sharing the context's workspace, must not overlap (one stream). */
+typedef struct {
+  int32_t n_ops, m, workgroups, waves_per_workgroup;
+  int64_t lds_bytes;
+} p0_chain_info_t;
+int p0_chain_begin(void);
+int p0_chain_end(void** chain_out);
+int p0_chain_run(void* chain);
+int p0_chain_status(void* chain, int32_t* timed_out);
+int p0_chain_info(void* chain, p0_chain_info_t* out);
+int p0_chain_free(void* chain);
+/* knob 0: waves per chain workgroup for M = 1 (8 or 16, default 16); knob 1: largest wave share in q4 groups before
+ * a chain op splits K across workgroups (default 16); knob 2: polls before a chain wait gives up (default 2^22).
+ * Applies to chains begun afterwards (knob 2: to runs). value <= 0 only queries; returns the previous value. */
+int p0_chain_tune(int knob, int value);
 
 /* ---- synthetic weights on the device (the reference's GPU filler, engine/tune/autotune.js:73-87) ----------------- */
 /* Symmetric BASELINE records: codes uniform in [0,16) (= q + 8 for q uniform in [-8, 8)), scale = fl16(|N(0, sigma)|),

@@ -26,6 +26,8 @@ HEADER_SYMBOLS = [
     "p0_buffer", "p0_free", "p0_upload", "p0_read", "p0_fill", "p0_done", "p0_timer_start", "p0_timer_stop",
     "p0_q4_gemv", "p0_q4_gemvM", "p0_q4_gemm", "p0_q4_dequant", "p0_fill_q4_sym", "p0_fill_randn", "p0_gemv_tune",
     "p0_record_begin", "p0_record_end", "p0_replay", "p0_record_free",
+    "p0_chain_begin", "p0_chain_end", "p0_chain_run", "p0_chain_status", "p0_chain_info", "p0_chain_free",
+    "p0_chain_tune",
 ]
 
 i64, i32, f32, vp = C.c_int64, C.c_int32, C.c_float, C.c_void_p
@@ -34,6 +36,10 @@ i64, i32, f32, vp = C.c_int64, C.c_int32, C.c_float, C.c_void_p
 class DeviceInfo(C.Structure):
     _fields_ = [("name", C.c_char * 64), ("device", C.c_int), ("cu_count", C.c_int), ("xcd_count", C.c_int),
                 ("hbm_bytes", i64), ("lds_bytes_per_cu", i64), ("clock_khz", C.c_int), ("workspace_bytes", i64)]
+
+
+class ChainInfo(C.Structure):
+    _fields_ = [("n_ops", i32), ("m", i32), ("workgroups", i32), ("waves_per_workgroup", i32), ("lds_bytes", i64)]
 
 
 class GemvArgs(C.Structure):
@@ -89,6 +95,9 @@ def lib():
             "p0_q4_dequant": [vp, i64, i64, i64, vp, vp], "p0_fill_q4_sym": [vp, i64, i64, i64, C.c_uint32, f32],
             "p0_fill_randn": [vp, i64, i64, C.c_uint32, f32, i32], "p0_gemv_tune": [C.c_int, C.c_int],
             "p0_record_begin": [], "p0_record_end": [C.POINTER(vp)], "p0_replay": [vp], "p0_record_free": [vp],
+            "p0_chain_begin": [], "p0_chain_end": [C.POINTER(vp)], "p0_chain_run": [vp],
+            "p0_chain_status": [vp, C.POINTER(i32)], "p0_chain_info": [vp, C.POINTER(ChainInfo)], "p0_chain_free": [vp],
+            "p0_chain_tune": [C.c_int, C.c_int],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -207,6 +216,48 @@ def record(fn):
 
 def gemv_tune(knob, value=0):
     return lib().p0_gemv_tune(knob, value)
+
+
+class Chain:
+    """A GEMV chain (p0_chain_begin ... p0_chain_end): the recorded ops run as one persistent launch."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    def run(self):
+        check(lib().p0_chain_run(self.handle))
+
+    def status(self):
+        """waits for the stream; True if a wait of an earlier run gave up (that run's results are invalid)"""
+        t = i32()
+        check(lib().p0_chain_status(self.handle, C.byref(t)))
+        return bool(t.value)
+
+    def info(self):
+        d = ChainInfo()
+        check(lib().p0_chain_info(self.handle, C.byref(d)))
+        return {f: getattr(d, f) for f, _ in ChainInfo._fields_}
+
+    def free(self):
+        if self.handle:
+            lib().p0_chain_free(self.handle)
+            self.handle = None
+
+
+def chain(fn):
+    """Plan the gemv / gemvM calls fn() makes into a Chain (they do not run now)."""
+    check(lib().p0_chain_begin())
+    try:
+        fn()
+    finally:
+        h = vp()
+        rc = lib().p0_chain_end(C.byref(h))
+    check(rc)
+    return Chain(h.value)
+
+
+def chain_tune(knob, value=0):
+    return lib().p0_chain_tune(knob, value)
 
 
 # ------------------------------------------------------------------------------------------------ ops

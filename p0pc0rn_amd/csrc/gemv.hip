@@ -1,343 +1,17 @@
-// gemv.hip - q4g32a.t64 GEMV (M = 1) and GEMV-M (M <= 16) for gfx950.
+// gemv.hip - host side of the q4g32a.t64 GEMV (M = 1), GEMV-M (M <= 16) and GEMV chains: validation, planning,
+// launch and the C entry points.
 //
 // Replaces the WebGPU dispatch of gemv (engine/llm/lops.js:108-141) and gemvM (engine/llm/lops_spec.js:159-191) with
 // the same arguments, the same split semantics (nsplit partial rows Y[split * ldy + m * ldm + n]) and the same errors.
-//
-// Data layout (q4g32a.t64, engine/kcheck.js:22-38): a weight W[N][K] is a sequence of 1280-byte records, record
-// (tile, g) = rows 64 tile .. 64 tile + 63, k = 32 g .. 32 g + 31, tile-major. Bytes [16 r, 16 r + 16) hold row r's 32
-// codes (u32 word w, nibble i = k 8 w + i); u32 256 + r = fp16 scale | fp16 min << 16.
-//
-// Kernel mapping (MI355X: 64-lane waves, 160 KB LDS per CU, 256 CUs in 8 XCDs):
-//  * one wave owns one 64-row tile (lane = row; T = 2 tiles per wave on large N, or the gate/up pair of a geglu);
-//  * per record, a lane issues ONE 16-byte load of its row's codes and one 4-byte load of its scale/min: the wave reads
-//    the record's 1024 + 256 bytes as two fully coalesced requests;
-//  * a code word is split with masks into fp16 bit patterns that ARE the codes as subnormals (q * 2^-24; the odd
-//    nibbles land as 16 q * 2^-24), which v_fma_mix_f32 multiplies into fp32 accumulators exactly: 13 VALU ops per
-//    8 weights, no int->float conversion;
-//  * x' = prologue(x) is staged once per workgroup in LDS for the workgroup's K-slice, the odd-k entries pre-scaled by
-//    1/16 (exact) to undo the odd nibbles' factor 16, plus the per-group sums of x' for the min term:
-//    y = sum_g (s_g 2^24) * (2^-24 sum q x') + m_g * sum x'   (the reference's s * sum q x + m * sum x split,
-//    engine/llm/lops.js:71);
-//  * when N alone gives too few waves for 256 CUs, K is split across workgroups; each writes its partial sums to the
-//    context workspace and the LAST workgroup to arrive at a (split, tile block) adds them in K-slice order (so the
-//    result does not depend on arrival order) and runs the epilogue.
-#include "common.hpp"
+// The kernels and their mapping onto MI355X are described in gemv_kernels.hpp.
+#include "gemv_kernels.hpp"
+
+#include <memory>
+#include <string>
+#include <vector>
 
 namespace p0 {
-
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-// 4-byte alignment is all a record base guarantees (weight offsets are multiples of 4, engine/llm/lops.js:124);
-// global_load_dwordx4 needs only dword alignment, so one 16-byte load per lane serves both cases
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
-
-struct GemvP {
-  const uint8_t* w;   // weight base (buf + w_off)
-  int64_t wG;         // groups per weight row (w_cols / 32)
-  int N, K, kPer, nsplit, NT;
-  int pro, epi;
-  const float* X; int64_t ldx, rowB;
-  const float* ST; int64_t statOff, statLd;
-  const float* NW; int64_t nOff;
-  int nsrc; int64_t ldp;
-  const float* EV; int64_t evOff, evLd;
-  float* Y; int64_t ldy, ldm;
-  float* MX; float cap;
-  int gps;            // groups per workgroup K-slice
-  int nks;            // workgroup K-slices per split (> 1: cross-workgroup reduction through the workspace)
-  int kw;             // waves per tile slot inside a workgroup (each takes a contiguous share of the K-slice)
-  int tgw;            // tile slots per workgroup (waves = tgw * kw)
-  int ntb;            // tile blocks (grid.x)
-  int rowsTot;        // rows that carry partials: N, or 2N for a geglu
-  float* part; unsigned* cnt;
-};
-
-__device__ __forceinline__ float gelu_tanh(float v) {   // engine/llm/lops.js:26
-  float t = 0.7978845608028654f * (v + 0.044715f * v * v * v);
-  t = fminf(15.0f, fmaxf(-15.0f, t));
-  return v * 0.5f * (1.0f + tanhf(t));
-}
-
-// prologue value x'[m][k] (engine/llm/lops.js:50-57, engine/llm/lops_spec.js:61-64)
-__device__ __forceinline__ float prologue(const GemvP& p, int m, int k) {
-  if (p.pro == P0_PRO_RAW) return p.X[m * p.ldx + p.rowB + k];
-  if (p.pro == P0_PRO_RMS) return p.X[m * p.ldx + p.rowB + k] * p.ST[p.statOff + m * p.statLd] * p.NW[p.nOff + k];
-  float s = 0.0f;
-  for (int j = 0; j < p.nsrc; ++j) s += p.X[j * p.ldp + m * p.ldx + k];
-  if (p.pro == P0_PRO_SUM) return s;
-  return gelu_tanh(s) * p.EV[p.evOff + m * p.evLd + k];
-}
-
-struct Rec {
-  u32x4 q;
-  uint32_t sm;
-};
-
-__device__ __forceinline__ Rec load_rec(const GemvP& p, int64_t tile, int g, int lane) {
-  const uint8_t* rec = p.w + (int64_t)__builtin_amdgcn_readfirstlane((int)((tile * p.wG + g) >> 0)) * 1280;
-  Rec r;
-  r.q = __builtin_nontemporal_load((const u32x4*)(rec + lane * 16));
-  r.sm = __builtin_nontemporal_load((const uint32_t*)(rec + 1024 + lane * 4));
-  return r;
-}
-
-// 2^-24 * sum_k q_k x'_k over one row's 32 codes; x points at the group's 32 staged values (odd k pre-scaled 1/16)
-__device__ __forceinline__ float dot32(const u32x4 q, const float* __restrict__ x) {
-  const float4* x4 = (const float4*)x;
-  const uint32_t u[4] = {q.x, q.y, q.z, q.w};
-  float da = 0.0f, db = 0.0f;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const float4 xa = x4[2 * w], xb = x4[2 * w + 1];   // k = 8w .. 8w+3, 8w+4 .. 8w+7
-    const uint32_t v = u[w], v8 = v >> 8;
-    const h2_t a = __builtin_bit_cast(h2_t, v & 0x000F000Fu);    // nibbles 0 | 4      (k 8w, 8w+4)
-    const h2_t b = __builtin_bit_cast(h2_t, v & 0x00F000F0u);    // nibbles 1 | 5 x16  (k 8w+1, 8w+5)
-    const h2_t c = __builtin_bit_cast(h2_t, v8 & 0x000F000Fu);   // nibbles 2 | 6      (k 8w+2, 8w+6)
-    const h2_t e = __builtin_bit_cast(h2_t, v8 & 0x00F000F0u);   // nibbles 3 | 7 x16  (k 8w+3, 8w+7)
-    da = __builtin_fmaf((float)a.x, xa.x, da);
-    db = __builtin_fmaf((float)a.y, xb.x, db);
-    da = __builtin_fmaf((float)b.x, xa.y, da);
-    db = __builtin_fmaf((float)b.y, xb.y, db);
-    da = __builtin_fmaf((float)c.x, xa.z, da);
-    db = __builtin_fmaf((float)c.y, xb.z, db);
-    da = __builtin_fmaf((float)e.x, xa.w, da);
-    db = __builtin_fmaf((float)e.y, xb.w, db);
-  }
-  return da + db;
-}
-
-__device__ __forceinline__ float h2f_lo(uint32_t v) { return (float)__builtin_bit_cast(h2_t, v).x; }
-__device__ __forceinline__ float h2f_hi(uint32_t v) { return (float)__builtin_bit_cast(h2_t, v).y; }
-
-// wave-wide (max, lowest index) of the softcapped row values: engine/llm/lops.js:96-102
-__device__ __forceinline__ void wave_argmax(float& v, int& r) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    float ov = __shfl_xor(v, off, 64);
-    int orr = __shfl_xor(r, off, 64);
-    if (ov > v || (ov == v && orr < r)) { v = ov; r = orr; }
-  }
-}
-
-// the epilogue of one wave for x row m: tot0 = row sums of tile0 (gate tile for a geglu), tot1 = the up tile's
-__device__ __forceinline__ void epilogue(const GemvP& p, int split, int m, int tile0, int lane, float tot0, float tot1) {
-  const int n = tile0 * 64 + lane;
-  if (p.epi == P0_EPI_STORE) {
-    p.Y[split * p.ldy + m * p.ldm + n] = tot0;
-  } else if (p.epi == P0_EPI_GEGLU) {
-    p.Y[m * p.ldm + n] = gelu_tanh(tot0) * tot1;
-  } else {
-    float v = p.cap * tanhf(fminf(15.0f, fmaxf(-15.0f, tot0 / p.cap)));
-    p.Y[m * p.ldm + n] = v;
-    int r = lane;
-    wave_argmax(v, r);
-    if (lane == 0) {
-      const int o = (m * p.NT + tile0) * 2;
-      p.MX[o] = v;
-      p.MX[o + 1] = __int_as_float(tile0 * 64 + r);
-    }
-  }
-}
-
-// MODE 0: one tile per wave; MODE 1: two tiles per wave; MODE 2: geglu (gate tile + its up tile N/64 tiles later).
-// A workgroup = tgw tile slots x kw waves per slot; it owns the K-slice [g0, g1) of one split, and the kw waves of a
-// slot take contiguous shares of it, reduced through LDS in wave order.
-template <int M, int MODE>
-__global__ __launch_bounds__(512) void q4_gemv_kernel(GemvP p) {
-  constexpr int T = MODE == 0 ? 1 : 2;
-  constexpr int TPW = MODE == 1 ? 2 : 1;   // distinct output tiles per wave
-  extern __shared__ __attribute__((aligned(16))) float smem[];   // 16-byte aligned: ds_read_b128 of x
-  const int tid = threadIdx.x, lane = tid & 63;
-  // wave-uniform indices live in SGPRs: record addresses become a scalar base plus the lane's constant 16-byte offset
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kwv = wv % p.kw, tw = wv / p.kw;
-  const int KL = p.gps * 32;
-  float* xs = smem;                    // [M][KL]   x' of the slice, odd k scaled 1/16
-  float* xsum = smem + M * KL;         // [M][gps]  group sums of x'
-  float* red = xsum + M * p.gps;       // [waves][T][64] in-workgroup reduction
-  __shared__ int s_last;
-
-  const int split = blockIdx.y / p.nks, ks = blockIdx.y - split * p.nks;
-  const int k0s = split * p.kPer, k1s = min(p.K, k0s + p.kPer);
-  const int gs0 = k0s >> 5, gs1 = k1s >> 5;
-  const int g0 = min(gs1, gs0 + ks * p.gps), g1 = min(gs1, g0 + p.gps);
-  const int sub = (g1 - g0 + p.kw - 1) / p.kw;
-  const int wg0 = min(g1, g0 + kwv * sub), wg1 = min(g1, wg0 + sub);   // this wave's share
-
-  // tiles of this wave
-  const int slot = blockIdx.x * p.tgw + tw;
-  int tile[T];
-  if (MODE == 2) {
-    tile[0] = slot;
-    tile[T - 1] = slot + p.NT;
-  } else {
-#pragma unroll
-    for (int t = 0; t < T; ++t) tile[t] = slot * TPW + t;
-  }
-  const bool active = tile[0] < p.NT;
-
-  // ---- prologue: x'[m][k] for the workgroup's K-slice -> LDS (odd k scaled 1/16), then per-group sums of x'
-  const int kb = g0 * 32, ke = g1 * 32;
-  for (int idx = tid; idx < M * KL; idx += blockDim.x) {
-    const int m = idx / KL, kl = idx - m * KL, k = kb + kl;
-    float v = k < ke ? prologue(p, m, k) : 0.0f;
-    xs[idx] = (k & 1) ? v * 0.0625f : v;
-  }
-  __syncthreads();
-  for (int idx = tid; idx < M * p.gps; idx += blockDim.x) {
-    const int m = idx / p.gps, gl = idx - m * p.gps;
-    const float* xp = xs + m * KL + gl * 32;
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; i += 2) s += xp[i] + xp[i + 1] * 16.0f;
-    xsum[idx] = s;
-  }
-  __syncthreads();
-
-  // ---- stream the records of the wave's share
-  float acc[T][M];
-#pragma unroll
-  for (int t = 0; t < T; ++t)
-#pragma unroll
-    for (int m = 0; m < M; ++m) acc[t][m] = 0.0f;
-
-  // one group's records: scale/min unpack, then the M x-rows against each tile's codes
-  auto consume = [&](const Rec (&cur)[T], int g) {
-    const int gl = g - g0;
-    float s24[T], mn[T];
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-      s24[t] = h2f_lo(cur[t].sm) * 16777216.0f;   // scale * 2^24 (exact)
-      mn[t] = h2f_hi(cur[t].sm);
-    }
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const float* xg = xs + m * KL + gl * 32;
-      const float sx = xsum[m * p.gps + gl];
-#pragma unroll
-      for (int t = 0; t < T; ++t) {
-        const float d = dot32(cur[t].q, xg);
-        acc[t][m] = __builtin_fmaf(s24[t], d, __builtin_fmaf(mn[t], sx, acc[t][m]));
-      }
-    }
-  };
-  // Chunks of D groups: all D (x T) records of a chunk are issued, then consumed in order. No load is carried across
-  // the loop's back edge, so the compiler's wait counts stay exact (each consume waits for its own record only; a
-  // rotating pipeline carried across the back edge made the counts collapse to near-full drains). The latency at
-  // the start of each chunk is hidden by the other resident waves. Loads past the share's end re-read its last group
-  // (in bounds, value unused), so every load is unconditional.
-  constexpr int D = MODE == 0 ? 8 : 4;
-  // a wave's second tile past N (odd tile count, MODE 1) re-reads its first tile; its results are never stored
-  auto tl = [&](int t) -> int64_t { return (MODE == 1 && tile[t] >= p.NT) ? tile[0] : tile[t]; };
-  if (active) {
-    const int glast = wg1 - 1;
-    for (int c0 = wg0; c0 < wg1; c0 += D) {
-      Rec r[D][T];
-#pragma unroll
-      for (int i = 0; i < D; ++i)
-#pragma unroll
-        for (int t = 0; t < T; ++t) r[i][t] = load_rec(p, tl(t), min(c0 + i, glast), lane);
-#pragma unroll
-      for (int i = 0; i < D; ++i)
-        if (c0 + i < wg1) consume(r[i], c0 + i);
-    }
-  }
-
-  // ---- the kw waves of a slot: sum their shares in wave order into wave kwv == 0
-  if (p.kw > 1) {
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      __syncthreads();
-#pragma unroll
-      for (int t = 0; t < T; ++t) red[(wv * T + t) * 64 + lane] = acc[t][m];
-      __syncthreads();
-      if (kwv == 0) {
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-          float s = 0.0f;
-          for (int j = 0; j < p.kw; ++j) s += red[((wv + j) * T + t) * 64 + lane];
-          acc[t][m] = s;
-        }
-      }
-    }
-  }
-
-  // ---- one workgroup per split: the epilogue straight from registers
-  if (p.nks == 1) {
-    if (!active || kwv != 0) return;
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      if (MODE == 2) {
-        epilogue(p, split, m, tile[0], lane, acc[0][m], acc[T - 1][m]);
-      } else {
-#pragma unroll
-        for (int t = 0; t < T; ++t)
-          if (tile[t] < p.NT) epilogue(p, split, m, tile[t], lane, acc[t][m], 0.0f);
-      }
-    }
-    return;
-  }
-
-  // ---- several workgroups per split: partials -> workspace; the last workgroup of (split, tile block) to arrive
-  // reduces them in K-slice order. One thread fences for the workgroup (a device-scope release / acquire writes back
-  // / invalidates the whole L2 of the XCD, so it is done once, after the barrier that orders every wave's stores).
-  const size_t sliceBase = (size_t)(split * p.nks) * M * p.rowsTot;
-  const bool owner = active && kwv == 0;
-  if (owner) {
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-      const int row = (MODE == 2 && t == 1) ? p.N + tile[0] * 64 + lane : tile[t] * 64 + lane;
-      if (MODE != 1 || tile[t] < p.NT) {
-#pragma unroll
-        for (int m = 0; m < M; ++m) p.part[sliceBase + ((size_t)ks * M + m) * p.rowsTot + row] = acc[t][m];
-      }
-    }
-  }
-  __syncthreads();
-  if (tid == 0) {
-    __threadfence();   // release: the workgroup's partials reach memory before the arrival count
-    unsigned* c = p.cnt + (size_t)split * p.ntb + blockIdx.x;
-    const unsigned prev = atomicAdd(c, 1u);
-    const int last = prev == (unsigned)(p.nks - 1);
-    if (last) {
-      atomicExch(c, 0u);   // leave the counter at zero for the next call
-      __threadfence();     // acquire: every other workgroup's partials
-    }
-    s_last = last;
-  }
-  __syncthreads();
-  if (!s_last || !owner) return;
-
-#pragma unroll
-  for (int m = 0; m < M; ++m) {
-    float tot[T];
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-      tot[t] = 0.0f;
-      const int row = (MODE == 2 && t == 1) ? p.N + tile[0] * 64 + lane : tile[t] * 64 + lane;
-      if (MODE != 1 || tile[t] < p.NT) {
-        for (int s = 0; s < p.nks; ++s) tot[t] += p.part[sliceBase + ((size_t)s * M + m) * p.rowsTot + row];
-      }
-    }
-    if (MODE == 2) {
-      epilogue(p, split, m, tile[0], lane, tot[0], tot[T - 1]);
-    } else {
-#pragma unroll
-      for (int t = 0; t < T; ++t)
-        if (tile[t] < p.NT) epilogue(p, split, m, tile[t], lane, tot[t], 0.0f);
-    }
-  }
-}
-
 // ------------------------------------------------------------------------------------------------ launch
-typedef void (*gemv_kernel_t)(GemvP);
-
-template <int M>
-static gemv_kernel_t pick_m(int mode) {
-  if (mode == 0) return q4_gemv_kernel<M, 0>;
-  if (mode == 1) return q4_gemv_kernel<M, 1>;
-  return q4_gemv_kernel<M, 2>;
-}
-
 static gemv_kernel_t pick(int M, int mode) {
   switch (M) {
     case 1: return pick_m<1>(mode);
@@ -364,7 +38,7 @@ static gemv_kernel_t pick(int M, int mode) {
 static int g_target_waves = 2048;       // waves a call aims for before it splits K
 static int g_two_tiles_min_nt = 1024;   // output tiles from which a wave streams two tiles
 static int g_min_gpw = 2;               // fewest q4 groups a wave streams when K is split
-static int g_max_kw = 4;                // most waves that share one tile slot's K-slice inside a workgroup
+static int g_max_kw = 16;               // most waves that share one tile slot's K-slice inside a workgroup
 
 struct Plan {
   int mode, gps, nks, kw, tgw, ntb, rowsTot, waves;
@@ -383,7 +57,8 @@ static Plan plan(int M, int NT, int epi, int nsplit, int kPer) {
   const int kws_max = Gs / g_min_gpw > 1 ? Gs / g_min_gpw : 1;
   if (kws > kws_max) kws = kws_max;
   if (kws < 1) kws = 1;
-  pl.kw = kws < g_max_kw ? kws : g_max_kw;
+  const int max_kw = M <= 2 ? g_max_kw : (g_max_kw < 8 ? g_max_kw : 8);   // the kernel's launch bound
+  pl.kw = kws < max_kw ? kws : max_kw;
   pl.tgw = pl.kw >= 4 ? 1 : 4 / pl.kw;                 // 4 waves per workgroup unless kw is larger
   if (pl.tgw > slots) pl.tgw = slots;
   pl.waves = pl.tgw * pl.kw;
@@ -406,14 +81,102 @@ static Plan plan(int M, int NT, int epi, int nsplit, int kPer) {
   return pl;
 }
 
+// ---- chain building: between p0_chain_begin and p0_chain_end, gemv / gemvM calls append planned ops instead of
+// launching. A chain runs with W waves per workgroup (16 for M = 1, else 8) and G = CUs x (1 or 2) workgroups.
+static chain_kernel_t pick_chain(int M, int W) {
+  switch (M) {
+    case 1: return pick_chain_m<1>(W);
+    case 2: return pick_chain_m<2>(W);
+    case 3: return pick_chain_m<3>(W);
+    case 4: return pick_chain_m<4>(W);
+    case 5: return pick_chain_m<5>(W);
+    case 6: return pick_chain_m<6>(W);
+    case 7: return pick_chain_m<7>(W);
+    case 8: return pick_chain_m<8>(W);
+    case 9: return pick_chain_m<9>(W);
+    case 10: return pick_chain_m<10>(W);
+    case 11: return pick_chain_m<11>(W);
+    case 12: return pick_chain_m<12>(W);
+    case 13: return pick_chain_m<13>(W);
+    case 14: return pick_chain_m<14>(W);
+    case 15: return pick_chain_m<15>(W);
+    case 16: return pick_chain_m<16>(W);
+  }
+  return nullptr;
+}
+
+static int g_chain_waves = 16;          // waves per chain workgroup for M = 1 (8 or 16)
+static int g_chain_split_gpw = 16;      // a wave share above this many groups splits K across workgroups
+static int g_chain_spin = 1 << 22;      // polls before a chain wait gives up (about 0.3 s)
+static constexpr size_t kChainLds = 64 * 1024;
+
+struct ChainBuild {
+  int M = 0, W = 0, G = 0;
+  size_t lds = 0;
+  std::vector<GemvP> ops;
+  std::string error;   // the first failed append (reported again by p0_chain_end)
+};
+struct ChainExec {
+  GemvP* ops;
+  unsigned* st;
+  int n_ops, M, W, grid;
+  size_t lds;
+  chain_kernel_t kernel;
+};
+static ChainBuild* g_chain = nullptr;
+
+// plan of one op inside a chain: all W waves of a workgroup busy (tgw = W / kw), one K-slice per split unless the op
+// leaves half the grid idle AND a wave's share would exceed g_chain_split_gpw groups
+static Plan plan_chain(int M, int NT, int epi, int nsplit, int kPer, int W, int G) {
+  Plan pl{};
+  pl.mode = epi == P0_EPI_GEGLU ? 2 : (NT >= g_two_tiles_min_nt ? 1 : 0);
+  const int T = pl.mode == 0 ? 1 : 2;
+  const int slots = pl.mode == 1 ? (NT + 1) / 2 : NT;
+  pl.rowsTot = (epi == P0_EPI_GEGLU ? 2 : 1) * NT * 64;
+  const int Gs = kPer / 32;
+  int kws = (G * W + slots * nsplit - 1) / (slots * nsplit);
+  const int kws_max = Gs / g_min_gpw > 1 ? Gs / g_min_gpw : 1;
+  if (kws > kws_max) kws = kws_max;
+  int kw = 1;
+  while (kw * 2 <= kws && kw * 2 <= W) kw *= 2;
+  pl.kw = kw;
+  pl.tgw = W / kw;
+  pl.waves = W;
+  pl.ntb = (slots + pl.tgw - 1) / pl.tgw;
+  int nks = 1;
+  auto gpw = [&](int n) { return ((Gs + n - 1) / n + kw - 1) / kw; };
+  while (gpw(nks) > g_chain_split_gpw && pl.ntb * nsplit * nks * 2 <= G) nks *= 2;
+  const size_t red = (size_t)W * T * 64 * sizeof(float);
+  const int maxGps = (int)((kChainLds - red) / ((size_t)M * 33 * sizeof(float)));
+  int gps = (Gs + nks - 1) / nks;
+  if (gps > maxGps) gps = maxGps;
+  pl.gps = gps;
+  pl.nks = (Gs + gps - 1) / gps;
+  pl.lds = (size_t)M * gps * 33 * sizeof(float) + red;
+  return pl;
+}
+
 static int launch(GemvP& p, int M, const char* op) {
-  const Plan pl = plan(M, p.NT, p.epi, p.nsplit, p.kPer);
+  ChainBuild* cb = g_chain;
+  if (cb && cb->ops.empty()) {   // the chain's first op fixes M and the workgroup shape
+    cb->M = M;
+    cb->W = M == 1 ? g_chain_waves : 8;
+    cb->G = ctx().cu_count * (cb->W == 16 ? 1 : 2);
+  }
+  if (cb && M != cb->M) {
+    set_error("%s: a chain holds ops of one M (chain M %d, this op %d)", op, cb->M, M);
+    if (cb->error.empty()) cb->error = p0_last_error();
+    return P0_EINVAL;
+  }
+  const Plan pl = cb ? plan_chain(M, p.NT, p.epi, p.nsplit, p.kPer, cb->W, cb->G) : plan(M, p.NT, p.epi, p.nsplit, p.kPer);
   if (pl.nks > 1 && (size_t)p.nsplit * pl.nks * M * pl.rowsTot > ctx().part_floats) {
     set_error("%s: split-K partials exceed the workspace (M %d, N %d, K %d)", op, M, p.N, p.K);
+    if (cb && cb->error.empty()) cb->error = p0_last_error();
     return P0_EINVAL;
   }
   if ((size_t)p.nsplit * pl.ntb > ctx().n_counters) {
     set_error("%s: too many tile blocks for the workspace counters", op);
+    if (cb && cb->error.empty()) cb->error = p0_last_error();
     return P0_EINVAL;
   }
   p.gps = pl.gps;
@@ -422,8 +185,14 @@ static int launch(GemvP& p, int M, const char* op) {
   p.tgw = pl.tgw;
   p.ntb = pl.ntb;
   p.rowsTot = pl.rowsTot;
+  p.mode = pl.mode;
   p.part = ctx().part;
   p.cnt = ctx().counters;
+  if (cb) {
+    cb->ops.push_back(p);
+    if (pl.lds > cb->lds) cb->lds = pl.lds;
+    return P0_OK;
+  }
   gemv_kernel_t k = pick(M, pl.mode);
   dim3 grid((unsigned)pl.ntb, (unsigned)(p.nsplit * pl.nks));
   hipLaunchKernelGGL(k, grid, dim3(64 * pl.waves), pl.lds, ctx().cur, p);
@@ -539,6 +308,111 @@ extern "C" int p0_gemv_tune(int knob, int value) {
          : knob == 3 ? &g_max_kw : nullptr;
   if (!t) return -1;
   const int old = *t;
-  if (value > 0) *t = knob == 3 && value > 8 ? 8 : value;
+  if (value > 0) *t = knob == 3 && value > 16 ? 16 : value;
+  return old;
+}
+
+// ---- chains (engine/llm/drunner.js:1-8, 83-101: a decode token's dispatches recorded once, submitted per token)
+extern "C" int p0_chain_begin(void) {
+  if (int r = require_open("p0_chain_begin")) return r;
+  if (g_chain) { set_error("p0_chain_begin: a chain is already being built"); return P0_EINVAL; }
+  g_chain = new ChainBuild();
+  return P0_OK;
+}
+
+extern "C" int p0_chain_end(void** out) {
+  ChainBuild* cb = g_chain;
+  g_chain = nullptr;
+  if (out) *out = nullptr;
+  if (!cb) { set_error("p0_chain_end: no chain is being built"); return P0_EINVAL; }
+  std::unique_ptr<ChainBuild> hold(cb);
+  if (int r = require_open("p0_chain_end")) return r;
+  if (!cb->error.empty()) { set_error("p0_chain_end: %s", cb->error.c_str()); return P0_EINVAL; }
+  if (cb->ops.empty()) { set_error("p0_chain_end: the chain holds no ops"); return P0_EINVAL; }
+  if (!out) { set_error("p0_chain_end: no output"); return P0_EINVAL; }
+  chain_kernel_t k = pick_chain(cb->M, cb->W);
+  int per_cu = 0;
+  P0_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k, 64 * cb->W, cb->lds), "p0_chain_end");
+  if (per_cu < 1) { set_error("p0_chain_end: a chain workgroup does not fit a CU"); return P0_EINVAL; }
+  int grid = ctx().cu_count * per_cu;
+  if (grid > cb->G) grid = cb->G;   // the plans were made for G workgroups; never more than are resident
+  auto* ex = new ChainExec{};
+  ex->n_ops = (int)cb->ops.size();
+  ex->M = cb->M;
+  ex->W = cb->W;
+  ex->grid = grid;
+  ex->lds = cb->lds;
+  ex->kernel = k;
+  const size_t ob = cb->ops.size() * sizeof(GemvP), sb = (cb->ops.size() + 2) * sizeof(unsigned);
+  hipError_t e = hipMalloc((void**)&ex->ops, ob);
+  if (e == hipSuccess) e = hipMalloc((void**)&ex->st, sb);
+  if (e == hipSuccess) e = hipMemcpy(ex->ops, cb->ops.data(), ob, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemset(ex->st, 0, sb);
+  if (e != hipSuccess) {
+    hipFree(ex->ops);
+    hipFree(ex->st);
+    delete ex;
+    return fail_hip(e, "p0_chain_end");
+  }
+  *out = ex;
+  return P0_OK;
+}
+
+extern "C" int p0_chain_run(void* chain) {
+  if (int r = require_open("p0_chain_run")) return r;
+  if (!chain) { set_error("p0_chain_run: no chain"); return P0_EINVAL; }
+  if (g_chain) { set_error("p0_chain_run: a chain is being built"); return P0_EINVAL; }
+  auto* ex = (ChainExec*)chain;
+  hipLaunchKernelGGL(ex->kernel, dim3((unsigned)ex->grid), dim3(64 * ex->W), ex->lds, ctx().cur, ex->ops, ex->n_ops,
+                     ex->st, g_chain_spin);
+  P0_LAUNCHED("p0_chain_run");
+  return P0_OK;
+}
+
+extern "C" int p0_chain_status(void* chain, int32_t* timed_out) {
+  if (int r = require_open("p0_chain_status")) return r;
+  if (!chain || !timed_out) { set_error("p0_chain_status: no chain or output"); return P0_EINVAL; }
+  auto* ex = (ChainExec*)chain;
+  P0_HIP(hipStreamSynchronize(ctx().cur), "p0_chain_status");
+  unsigned v = 0;
+  P0_HIP(hipMemcpy(&v, ex->st + ex->n_ops + 1, sizeof v, hipMemcpyDeviceToHost), "p0_chain_status");
+  if (v) {
+    // an abandoned run can leave completion counts and split-K arrival counters mid-way: start both from zero
+    P0_HIP(hipMemset(ex->st, 0, (ex->n_ops + 2) * sizeof(unsigned)), "p0_chain_status");
+    P0_HIP(hipMemset(ctx().counters, 0, ctx().n_counters * sizeof(unsigned)), "p0_chain_status");
+    P0_HIP(hipDeviceSynchronize(), "p0_chain_status");
+  }
+  *timed_out = v ? 1 : 0;
+  return P0_OK;
+}
+
+extern "C" int p0_chain_info(void* chain, p0_chain_info_t* out) {
+  if (!chain || !out) { set_error("p0_chain_info: no chain or output"); return P0_EINVAL; }
+  auto* ex = (ChainExec*)chain;
+  out->n_ops = ex->n_ops;
+  out->m = ex->M;
+  out->workgroups = ex->grid;
+  out->waves_per_workgroup = ex->W;
+  out->lds_bytes = (int64_t)ex->lds;
+  return P0_OK;
+}
+
+extern "C" int p0_chain_free(void* chain) {
+  if (!chain) return P0_OK;
+  auto* ex = (ChainExec*)chain;
+  if (ctx().device >= 0) hipStreamSynchronize(ctx().cur);
+  hipFree(ex->ops);
+  hipFree(ex->st);
+  delete ex;
+  return P0_OK;
+}
+
+// chain knobs: 0 = waves per workgroup for M = 1 (8 or 16), 1 = largest wave share (groups) before K is split
+// across workgroups, 2 = polls before a wait gives up. Returns the previous value; a value <= 0 only reads.
+extern "C" int p0_chain_tune(int knob, int value) {
+  int* t = knob == 0 ? &g_chain_waves : knob == 1 ? &g_chain_split_gpw : knob == 2 ? &g_chain_spin : nullptr;
+  if (!t) return -1;
+  const int old = *t;
+  if (value > 0) *t = knob == 0 ? (value >= 16 ? 16 : 8) : value;
   return old;
 }

@@ -1,0 +1,462 @@
+// gemv_kernels.hpp - device code of the q4g32a.t64 GEMV (M = 1), GEMV-M (M <= 16) and GEMV chains for gfx950.
+//
+// Replaces the WebGPU dispatch of gemv (engine/llm/lops.js:108-141) and gemvM (engine/llm/lops_spec.js:159-191) with
+// the same arguments, the same split semantics (nsplit partial rows Y[split * ldy + m * ldm + n]) and the same errors.
+//
+// Data layout (q4g32a.t64, engine/kcheck.js:22-38): a weight W[N][K] is a sequence of 1280-byte records, record
+// (tile, g) = rows 64 tile .. 64 tile + 63, k = 32 g .. 32 g + 31, tile-major. Bytes [16 r, 16 r + 16) hold row r's 32
+// codes (u32 word w, nibble i = k 8 w + i); u32 256 + r = fp16 scale | fp16 min << 16.
+//
+// Kernel mapping (MI355X: 64-lane waves, 160 KB LDS per CU, 256 CUs in 8 XCDs):
+//  * one wave owns one 64-row tile (lane = row; T = 2 tiles per wave on large N, or the gate/up pair of a geglu);
+//  * per record, a lane issues ONE 16-byte load of its row's codes and one 4-byte load of its scale/min: the wave reads
+//    the record's 1024 + 256 bytes as two fully coalesced requests;
+//  * a code word is split with masks into fp16 bit patterns that ARE the codes as subnormals (q * 2^-24; the odd
+//    nibbles land as 16 q * 2^-24), which v_fma_mix_f32 multiplies into fp32 accumulators exactly: 13 VALU ops per
+//    8 weights, no int->float conversion;
+//  * x' = prologue(x) is staged once per workgroup in LDS for the workgroup's K-slice, the odd-k entries pre-scaled by
+//    1/16 (exact) to undo the odd nibbles' factor 16, plus the per-group sums of x' for the min term:
+//    y = sum_g (s_g 2^24) * (2^-24 sum q x') + m_g * sum x'   (the reference's s * sum q x + m * sum x split,
+//    engine/llm/lops.js:71);
+//  * when N alone gives too few waves for 256 CUs, K is split across workgroups; each writes its partial sums to the
+//    context workspace and the LAST workgroup to arrive at a (split, tile block) adds them in K-slice order (so the
+//    result does not depend on arrival order) and runs the epilogue.
+#pragma once
+#include "common.hpp"
+
+namespace p0 {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+// 4-byte alignment is all a record base guarantees (weight offsets are multiples of 4, engine/llm/lops.js:124);
+// global_load_dwordx4 needs only dword alignment, so one 16-byte load per lane serves both cases
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
+
+
+struct GemvP {
+  const uint8_t* w;   // weight base (buf + w_off)
+  int64_t wG;         // groups per weight row (w_cols / 32)
+  int N, K, kPer, nsplit, NT;
+  int pro, epi;
+  const float* X; int64_t ldx, rowB;
+  const float* ST; int64_t statOff, statLd;
+  const float* NW; int64_t nOff;
+  int nsrc; int64_t ldp;
+  const float* EV; int64_t evOff, evLd;
+  float* Y; int64_t ldy, ldm;
+  float* MX; float cap;
+  int gps;            // groups per workgroup K-slice
+  int nks;            // workgroup K-slices per split (> 1: cross-workgroup reduction through the workspace)
+  int kw;             // waves per tile slot inside a workgroup (each takes a contiguous share of the K-slice)
+  int tgw;            // tile slots per workgroup (waves = tgw * kw)
+  int ntb;            // tile blocks (grid.x)
+  int rowsTot;        // rows that carry partials: N, or 2N for a geglu
+  int mode;           // kernel mode (chain ops choose their code path from it)
+  float* part; unsigned* cnt;
+};
+
+__device__ __forceinline__ float gelu_tanh(float v) {   // engine/llm/lops.js:26
+  float t = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+  t = fminf(15.0f, fmaxf(-15.0f, t));
+  return v * 0.5f * (1.0f + tanhf(t));
+}
+
+// prologue value x'[m][k] (engine/llm/lops.js:50-57, engine/llm/lops_spec.js:61-64)
+__device__ __forceinline__ float prologue(const GemvP& p, int m, int k) {
+  if (p.pro == P0_PRO_RAW) return p.X[m * p.ldx + p.rowB + k];
+  if (p.pro == P0_PRO_RMS) return p.X[m * p.ldx + p.rowB + k] * p.ST[p.statOff + m * p.statLd] * p.NW[p.nOff + k];
+  float s = 0.0f;
+  for (int j = 0; j < p.nsrc; ++j) s += p.X[j * p.ldp + m * p.ldx + k];
+  if (p.pro == P0_PRO_SUM) return s;
+  return gelu_tanh(s) * p.EV[p.evOff + m * p.evLd + k];
+}
+
+struct Rec {
+  u32x4 q;
+  uint32_t sm;
+};
+
+__device__ __forceinline__ Rec load_rec(const GemvP& p, int64_t tile, int g, int lane) {
+  const uint8_t* rec = p.w + (int64_t)__builtin_amdgcn_readfirstlane((int)((tile * p.wG + g) >> 0)) * 1280;
+  Rec r;
+  r.q = __builtin_nontemporal_load((const u32x4*)(rec + lane * 16));
+  r.sm = __builtin_nontemporal_load((const uint32_t*)(rec + 1024 + lane * 4));
+  return r;
+}
+
+// 2^-24 * sum_k q_k x'_k over one row's 32 codes; x points at the group's 32 staged values (odd k pre-scaled 1/16)
+__device__ __forceinline__ float dot32(const u32x4 q, const float* __restrict__ x) {
+  const float4* x4 = (const float4*)x;
+  const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+  float da = 0.0f, db = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float4 xa = x4[2 * w], xb = x4[2 * w + 1];   // k = 8w .. 8w+3, 8w+4 .. 8w+7
+    const uint32_t v = u[w], v8 = v >> 8;
+    const h2_t a = __builtin_bit_cast(h2_t, v & 0x000F000Fu);    // nibbles 0 | 4      (k 8w, 8w+4)
+    const h2_t b = __builtin_bit_cast(h2_t, v & 0x00F000F0u);    // nibbles 1 | 5 x16  (k 8w+1, 8w+5)
+    const h2_t c = __builtin_bit_cast(h2_t, v8 & 0x000F000Fu);   // nibbles 2 | 6      (k 8w+2, 8w+6)
+    const h2_t e = __builtin_bit_cast(h2_t, v8 & 0x00F000F0u);   // nibbles 3 | 7 x16  (k 8w+3, 8w+7)
+    da = __builtin_fmaf((float)a.x, xa.x, da);
+    db = __builtin_fmaf((float)a.y, xb.x, db);
+    da = __builtin_fmaf((float)b.x, xa.y, da);
+    db = __builtin_fmaf((float)b.y, xb.y, db);
+    da = __builtin_fmaf((float)c.x, xa.z, da);
+    db = __builtin_fmaf((float)c.y, xb.z, db);
+    da = __builtin_fmaf((float)e.x, xa.w, da);
+    db = __builtin_fmaf((float)e.y, xb.w, db);
+  }
+  return da + db;
+}
+
+__device__ __forceinline__ float h2f_lo(uint32_t v) { return (float)__builtin_bit_cast(h2_t, v).x; }
+__device__ __forceinline__ float h2f_hi(uint32_t v) { return (float)__builtin_bit_cast(h2_t, v).y; }
+
+// wave-wide (max, lowest index) of the softcapped row values: engine/llm/lops.js:96-102
+__device__ __forceinline__ void wave_argmax(float& v, int& r) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    float ov = __shfl_xor(v, off, 64);
+    int orr = __shfl_xor(r, off, 64);
+    if (ov > v || (ov == v && orr < r)) { v = ov; r = orr; }
+  }
+}
+
+// the epilogue of one wave for x row m: tot0 = row sums of tile0 (gate tile for a geglu), tot1 = the up tile's
+__device__ __forceinline__ void epilogue(const GemvP& p, int split, int m, int tile0, int lane, float tot0, float tot1) {
+  const int n = tile0 * 64 + lane;
+  if (p.epi == P0_EPI_STORE) {
+    p.Y[split * p.ldy + m * p.ldm + n] = tot0;
+  } else if (p.epi == P0_EPI_GEGLU) {
+    p.Y[m * p.ldm + n] = gelu_tanh(tot0) * tot1;
+  } else {
+    float v = p.cap * tanhf(fminf(15.0f, fmaxf(-15.0f, tot0 / p.cap)));
+    p.Y[m * p.ldm + n] = v;
+    int r = lane;
+    wave_argmax(v, r);
+    if (lane == 0) {
+      const int o = (m * p.NT + tile0) * 2;
+      p.MX[o] = v;
+      p.MX[o + 1] = __int_as_float(tile0 * 64 + r);
+    }
+  }
+}
+
+// One work item of one op, run by the calling workgroup: tile block bx, (split, K-slice) by. MODE 0: one tile per
+// wave; MODE 1: two tiles per wave; MODE 2: geglu (gate tile + its up tile N/64 tiles later). A workgroup = tgw tile
+// slots x kw waves per slot; it owns the K-slice [g0, g1) of one split, and the kw waves of a slot take contiguous
+// shares of it, reduced through LDS in wave order. `ready()` runs after the item's first weight loads are issued and
+// before its input is read (the chain executor waits for the producing op there; a standalone launch has nothing to
+// wait for); it returns false (in every thread) to abandon the item. Returns true when this workgroup wrote the
+// final outputs of its (split, tile block): always for one K-slice per split, only the last arriving workgroup
+// otherwise. The value is the same in every thread.
+template <int M, int MODE, class Ready>
+__device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float* smem, int* s_last, Ready&& ready) {
+  constexpr int T = MODE == 0 ? 1 : 2;
+  constexpr int TPW = MODE == 1 ? 2 : 1;   // distinct output tiles per wave
+  // Chunks of D groups: all D (x T) records of a chunk are issued, then consumed in order. No load is carried across
+  // the loop's back edge, so the compiler's wait counts stay exact (each consume waits for its own record only; a
+  // rotating pipeline carried across the back edge made the counts collapse to near-full drains). The latency at
+  // the start of each chunk is hidden by the other resident waves. Loads past the share's end re-read its last group
+  // (in bounds, value unused), so every load is unconditional.
+  constexpr int D = MODE == 0 ? 8 : 4;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // wave-uniform indices live in SGPRs: record addresses become a scalar base plus the lane's constant 16-byte offset
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kwv = wv % p.kw, tw = wv / p.kw;
+  const int KL = p.gps * 32;
+  float* xs = smem;                    // [M][KL]   x' of the slice, odd k scaled 1/16
+  float* xsum = smem + M * KL;         // [M][gps]  group sums of x'
+  float* red = xsum + M * p.gps;       // [waves][T][64] in-workgroup reduction
+
+  const int split = by / p.nks, ks = by - split * p.nks;
+  const int k0s = split * p.kPer, k1s = min(p.K, k0s + p.kPer);
+  const int gs0 = k0s >> 5, gs1 = k1s >> 5;
+  const int g0 = min(gs1, gs0 + ks * p.gps), g1 = min(gs1, g0 + p.gps);
+  const int sub = (g1 - g0 + p.kw - 1) / p.kw;
+  const int wg0 = min(g1, g0 + kwv * sub), wg1 = min(g1, wg0 + sub);   // this wave's share
+
+  // tiles of this wave
+  const int slot = bx * p.tgw + tw;
+  int tile[T];
+  if (MODE == 2) {
+    tile[0] = slot;
+    tile[T - 1] = slot + p.NT;
+  } else {
+#pragma unroll
+    for (int t = 0; t < T; ++t) tile[t] = slot * TPW + t;
+  }
+  const bool active = tile[0] < p.NT;
+  // a wave's second tile past N (odd tile count, MODE 1) re-reads its first tile; its results are never stored
+  auto tl = [&](int t) -> int64_t { return (MODE == 1 && tile[t] >= p.NT) ? tile[0] : tile[t]; };
+  const int glast = wg1 - 1;
+  const bool streams = active && wg0 < wg1;
+
+  // ---- the share's first chunk is issued before the input is read: its latency overlaps the wait and the prologue
+  __syncthreads();   // the previous item of this workgroup is done with the LDS
+  Rec r0[D][T];
+  if (streams) {
+#pragma unroll
+    for (int i = 0; i < D; ++i)
+#pragma unroll
+      for (int t = 0; t < T; ++t) r0[i][t] = load_rec(p, tl(t), min(wg0 + i, glast), lane);
+  }
+  if (!ready()) return false;
+
+  // ---- prologue: x'[m][k] for the workgroup's K-slice -> LDS (odd k scaled 1/16), then per-group sums of x'
+  const int kb = g0 * 32, ke = g1 * 32;
+  for (int idx = tid; idx < M * KL; idx += blockDim.x) {
+    const int m = idx / KL, kl = idx - m * KL, k = kb + kl;
+    float v = k < ke ? prologue(p, m, k) : 0.0f;
+    xs[idx] = (k & 1) ? v * 0.0625f : v;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < M * p.gps; idx += blockDim.x) {
+    const int m = idx / p.gps, gl = idx - m * p.gps;
+    const float* xp = xs + m * KL + gl * 32;
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i += 2) s += xp[i] + xp[i + 1] * 16.0f;
+    xsum[idx] = s;
+  }
+  __syncthreads();
+
+  // ---- stream the records of the wave's share
+  float acc[T][M];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[t][m] = 0.0f;
+
+  // one group's records: scale/min unpack, then the M x-rows against each tile's codes
+  auto consume = [&](const Rec (&cur)[T], int g) {
+    const int gl = g - g0;
+    float s24[T], mn[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      s24[t] = h2f_lo(cur[t].sm) * 16777216.0f;   // scale * 2^24 (exact)
+      mn[t] = h2f_hi(cur[t].sm);
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float* xg = xs + m * KL + gl * 32;
+      const float sx = xsum[m * p.gps + gl];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const float d = dot32(cur[t].q, xg);
+        acc[t][m] = __builtin_fmaf(s24[t], d, __builtin_fmaf(mn[t], sx, acc[t][m]));
+      }
+    }
+  };
+  if (streams) {
+#pragma unroll
+    for (int i = 0; i < D; ++i)
+      if (wg0 + i < wg1) consume(r0[i], wg0 + i);
+    for (int c0 = wg0 + D; c0 < wg1; c0 += D) {
+      Rec r[D][T];
+#pragma unroll
+      for (int i = 0; i < D; ++i)
+#pragma unroll
+        for (int t = 0; t < T; ++t) r[i][t] = load_rec(p, tl(t), min(c0 + i, glast), lane);
+#pragma unroll
+      for (int i = 0; i < D; ++i)
+        if (c0 + i < wg1) consume(r[i], c0 + i);
+    }
+  }
+
+  // ---- the kw waves of a slot: sum their shares in wave order into wave kwv == 0
+  if (p.kw > 1) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < T; ++t) red[(wv * T + t) * 64 + lane] = acc[t][m];
+      __syncthreads();
+      if (kwv == 0) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          float s = 0.0f;
+          for (int j = 0; j < p.kw; ++j) s += red[((wv + j) * T + t) * 64 + lane];
+          acc[t][m] = s;
+        }
+      }
+    }
+  }
+
+  // ---- one K-slice per split: the epilogue straight from registers
+  const bool owner = active && kwv == 0;
+  if (p.nks == 1) {
+    if (owner) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        if (MODE == 2) {
+          epilogue(p, split, m, tile[0], lane, acc[0][m], acc[T - 1][m]);
+        } else {
+#pragma unroll
+          for (int t = 0; t < T; ++t)
+            if (tile[t] < p.NT) epilogue(p, split, m, tile[t], lane, acc[t][m], 0.0f);
+        }
+      }
+    }
+    return true;
+  }
+
+  // ---- several K-slices per split: partials -> workspace; the last workgroup of (split, tile block) to arrive
+  // reduces them in K-slice order. One thread fences for the workgroup (a device-scope release / acquire writes back
+  // / invalidates the whole L2 of the XCD, so it is done once, after the barrier that orders every wave's stores).
+  const size_t sliceBase = (size_t)(split * p.nks) * M * p.rowsTot;
+  if (owner) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int row = (MODE == 2 && t == 1) ? p.N + tile[0] * 64 + lane : tile[t] * 64 + lane;
+      if (MODE != 1 || tile[t] < p.NT) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) p.part[sliceBase + ((size_t)ks * M + m) * p.rowsTot + row] = acc[t][m];
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();   // release: the workgroup's partials reach memory before the arrival count
+    unsigned* c = p.cnt + (size_t)split * p.ntb + bx;
+    const unsigned prev = atomicAdd(c, 1u);
+    const int last = prev == (unsigned)(p.nks - 1);
+    if (last) {
+      atomicExch(c, 0u);   // leave the counter at zero for the next use
+      __threadfence();     // acquire: every other workgroup's partials
+    }
+    *s_last = last;
+  }
+  __syncthreads();
+  const bool last = *s_last != 0;
+  if (!last || !owner) return last;
+
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float tot[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      tot[t] = 0.0f;
+      const int row = (MODE == 2 && t == 1) ? p.N + tile[0] * 64 + lane : tile[t] * 64 + lane;
+      if (MODE != 1 || tile[t] < p.NT) {
+        for (int s = 0; s < p.nks; ++s) tot[t] += p.part[sliceBase + ((size_t)s * M + m) * p.rowsTot + row];
+      }
+    }
+    if (MODE == 2) {
+      epilogue(p, split, m, tile[0], lane, tot[0], tot[T - 1]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        if (tile[t] < p.NT) epilogue(p, split, m, tile[t], lane, tot[t], 0.0f);
+    }
+  }
+  return true;
+}
+
+// One op, one launch: grid (tile blocks, splits x K-slices). Up to 16 waves per workgroup for M <= 2; 8 for larger
+// M, whose accumulators need the registers (128 VGPRs per lane at 16 waves would spill).
+template <int M, int MODE>
+__global__ __launch_bounds__(M <= 2 ? 1024 : 512) void q4_gemv_kernel(GemvP p) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];   // 16-byte aligned: ds_read_b128 of x
+  __shared__ int s_last;
+  gemv_item<M, MODE>(p, blockIdx.x, blockIdx.y, smem, &s_last, [] { return true; });
+}
+
+// ---- the chain executor: a recorded sequence of GEMV ops in ONE persistent launch (the analogue of the reference's
+// per-token command buffer, engine/llm/drunner.js:1-8). Op i may read what ops < i wrote, so its items wait until op
+// i - 1 has written all of its outputs; each workgroup issues its first item's weight loads BEFORE that wait, so the
+// next op's weights stream while the previous op finishes. Items are dealt to workgroups round-robin; every
+// workgroup of the grid is resident at once (the grid is sized from the occupancy), so a wait always ends. Each wait
+// is also bounded: past `spin_limit` polls it sets the timed-out word, and every workgroup abandons the rest of the
+// chain at its next wait, so a launch always finishes (its results are then invalid and reported as such). Completion
+// is counted per op (one count per (split, tile block) whose final outputs are written); the last workgroup to leave
+// resets the counts, so a chain replays any number of times with no memset (capturable).
+// st: [0, n_ops) completion counts, [n_ops] workgroups finished, [n_ops + 1] timed out (sticky until read).
+template <int M, int W>
+__global__ __launch_bounds__(64 * W) void q4_gemv_chain_kernel(const GemvP* __restrict__ ops, int n_ops,
+                                                               unsigned* __restrict__ st, int spin_limit) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  __shared__ int s_last, s_go;
+  const int tid = threadIdx.x;
+  unsigned* const finished = st + n_ops;
+  unsigned* const timed_out = st + n_ops + 1;
+  bool abandon = false;
+  for (int i = 0; i < n_ops && !abandon; ++i) {
+    const GemvP& p = ops[i];
+    const int items = p.ntb * p.nsplit * p.nks;
+    const unsigned need = i > 0 ? (unsigned)(ops[i - 1].ntb * ops[i - 1].nsplit) : 0u;
+    bool waited = i == 0;
+    for (int it = blockIdx.x; it < items; it += gridDim.x) {
+      const int bx = it % p.ntb, by = it / p.ntb;
+      auto ready = [&]() -> bool {
+        if (waited) return true;   // only the workgroup's first item of op i waits for op i - 1
+        if (tid == 0) {
+          int go = 1, spins = 0;
+          while (__hip_atomic_load(&st[i - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
+            if (__hip_atomic_load(timed_out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) || ++spins > spin_limit) {
+              atomicOr(timed_out, 1u);
+              go = 0;
+              break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+          }
+          __threadfence();   // acquire: op i - 1's outputs
+          s_go = go;
+        }
+        __syncthreads();
+        waited = true;
+        abandon = s_go == 0;
+        return !abandon;
+      };
+      bool fin;
+      if (p.mode == 0) fin = gemv_item<M, 0>(p, bx, by, smem, &s_last, ready);
+      else if (p.mode == 1) fin = gemv_item<M, 1>(p, bx, by, smem, &s_last, ready);
+      else fin = gemv_item<M, 2>(p, bx, by, smem, &s_last, ready);
+      if (abandon) break;
+      if (fin) {
+        __syncthreads();   // every wave's outputs are written
+        if (tid == 0) {
+          __threadfence();   // release: the outputs reach memory before the count
+          atomicAdd(&st[i], 1u);
+        }
+      }
+    }
+  }
+  // the last workgroup to leave resets the counts for the next run
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    if (atomicAdd(finished, 1u) == gridDim.x - 1) {
+      for (int i = 0; i < n_ops; ++i) atomicExch(&st[i], 0u);
+      atomicExch(finished, 0u);
+      __threadfence();
+    }
+  }
+}
+
+// ---- kernel tables: each M's kernels are instantiated in one of the gemv_m*.hip units (parallel compilation)
+typedef void (*gemv_kernel_t)(GemvP);
+typedef void (*chain_kernel_t)(const GemvP*, int, unsigned*, int);
+
+template <int M>
+gemv_kernel_t pick_m(int mode) {
+  if (mode == 0) return q4_gemv_kernel<M, 0>;
+  if (mode == 1) return q4_gemv_kernel<M, 1>;
+  return q4_gemv_kernel<M, 2>;
+}
+
+template <int M>
+chain_kernel_t pick_chain_m(int W) {   // 16-wave chain workgroups for M = 1, 8-wave ones for every M
+  if (M == 1 && W == 16) return q4_gemv_chain_kernel<M, (M == 1 ? 16 : 8)>;
+  return q4_gemv_chain_kernel<M, 8>;
+}
+
+#define P0_GEMV_EXTERN(M) \
+  extern template gemv_kernel_t pick_m<M>(int); \
+  extern template chain_kernel_t pick_chain_m<M>(int);
+P0_GEMV_EXTERN(1) P0_GEMV_EXTERN(2) P0_GEMV_EXTERN(3) P0_GEMV_EXTERN(4)
+P0_GEMV_EXTERN(5) P0_GEMV_EXTERN(6) P0_GEMV_EXTERN(7) P0_GEMV_EXTERN(8)
+P0_GEMV_EXTERN(9) P0_GEMV_EXTERN(10) P0_GEMV_EXTERN(11) P0_GEMV_EXTERN(12)
+P0_GEMV_EXTERN(13) P0_GEMV_EXTERN(14) P0_GEMV_EXTERN(15) P0_GEMV_EXTERN(16)
+#undef P0_GEMV_EXTERN
+
+}  // namespace p0

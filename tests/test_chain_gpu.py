@@ -1,0 +1,323 @@
+"""GPU parity of GEMV chains (p0_chain_*): a decode step's GEMVs planned once and run as ONE persistent launch.
+
+Each op of a chain is checked against the CPU oracle run on the input that op actually read on the GPU (the previous
+op's output, read back), so a wrong result and a broken dependency wait fail separately: every intermediate buffer is
+NaN-filled before the run, and an op that read its input before the producer finished writing it cannot pass.
+Tolerance as for single GEMVs: relative L2 <= 1e-3 and this build's fp32 bar of 2e-5.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from p0pc0rn_amd import capi
+from tests.conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+TOL, TOL_FP32 = 1e-3, 2e-5
+NAN = 0x7FC00000
+
+
+def _check(got, want, what):
+    r = rel_l2(got, want)
+    print(f"{what}: rel_l2 {r:.3e}", flush=True)
+    assert np.all(np.isfinite(got)), what + ": non-finite output"
+    assert r <= TOL and r <= TOL_FP32, what
+
+
+def _w(rows, K, seed):
+    return O.pack_q4(O.randn(rows * K, seed, 0.05), rows, K)[0]
+
+
+class MiniStep:
+    """A decode-like op sequence at M rows: qkv (rms) -> o (raw, reads qkv) -> gate/up (rms + geglu, reads o) ->
+    down (raw, 2 K-splits, reads the geglu output) -> sum of the 2 partials (pro sum) -> head (rms + softcap).
+    Scalar rms statistics are fixed inputs (computed on the host), so every op's input is the previous op's output."""
+
+    def __init__(self, M=1, D=256, QKV=384, MLP=512, V=4096, seed=3, gemvM=False):
+        self.M, self.D, self.QKV, self.MLP, self.V, self.gemvM = M, D, QKV, MLP, V, gemvM
+        self.host = {
+            "x": O.randn(M * D, seed), "w_qkv": _w(QKV, D, seed + 1), "w_o": _w(D, D, seed + 2),
+            "w_gu": _w(2 * MLP, D, seed + 3), "w_dn": _w(D, MLP, seed + 4), "w_sum": _w(D, D, seed + 5),
+            "w_hd": _w(V, D, seed + 6), "norm": (0.8 + 0.4 * O.rng_uniform(seed + 7, D)).astype(np.float32),
+        }
+        st = np.zeros(2 * M + 8, np.float32)
+        st[1::2][:M] = 0.7                      # rstd of each row for the rms prologues
+        self.host["stat"] = st
+        NT = V // 64
+        self.mx_len = M * NT * 2 + 2 * M + 8
+        mx = np.zeros(self.mx_len, np.float32)
+        mx[M * NT * 2 + 1::2][:M] = 0.9         # head rms rstd slot (gemv softcap reads it from mx)
+        self.host["mx"] = mx
+        self.dev = {k: capi.to_device(v) for k, v in self.host.items()}
+        self.out_len = {"qkv": M * QKV, "o": M * D, "gu": M * MLP, "dn": 2 * M * D, "sum": M * D, "hd": M * V}
+        self.out = {k: capi.Buffer(4 * n) for k, n in self.out_len.items()}
+        self.mx_stat_off = M * NT * 2 + 1
+
+    def ops(self, b):
+        """field dicts of the 6 ops over buffer map b (device Buffers or host pointers)"""
+        M, D, QKV, MLP, V = self.M, self.D, self.QKV, self.MLP, self.V
+        E, P = capi.EPI, capi.PRO
+        ops = [
+            dict(w=b["w_qkv"], w_rows=QKV, w_cols=D, x=b["x"], N=QKV, K=D, pro=P["rms"], epi=E["store"], y=b["qkv"],
+                 stat=b["stat"], stat_off=1, norm=b["norm"]),
+            dict(w=b["w_o"], w_rows=D, w_cols=D, x=b["qkv"], N=D, K=D, pro=P["raw"], epi=E["store"], y=b["o"]),
+            dict(w=b["w_gu"], w_rows=2 * MLP, w_cols=D, x=b["o"], N=MLP, K=D, pro=P["rms"], epi=E["geglu"],
+                 y=b["gu"], stat=b["stat"], stat_off=1, norm=b["norm"]),
+            dict(w=b["w_dn"], w_rows=D, w_cols=MLP, x=b["gu"], N=D, K=MLP, kPer=256, pro=P["raw"], epi=E["store"],
+                 y=b["dn"]),
+            dict(w=b["w_sum"], w_rows=D, w_cols=D, x=b["dn"], N=D, K=D, pro=P["sum"] if not self.gemvM else P["raw"],
+                 epi=E["store"], y=b["sum"], src_n=2, src_ld=D if not self.gemvM else M * D),
+            dict(w=b["w_hd"], w_rows=V, w_cols=D, x=b["sum"], N=V, K=D, pro=P["rms"], epi=E["softcap"], y=b["hd"],
+                 norm=b["norm"], mx=b["mx"], cap=30.0),
+        ]
+        for o in ops:
+            if self.gemvM:
+                o.update(M=M, x_ldx=o["K"], stat_ld=2, y_ldm=o["N"])
+                if o["epi"] == E["store"]:
+                    o.update(y_ldy=M * o["N"])
+            if o["epi"] == E["softcap"]:   # the head's rms rstd sits in mx (engine/llm/lops.js:125)
+                o.update(stat=b["mx"], stat_off=self.mx_stat_off)
+        if self.gemvM:
+            ops[1]["x_ldx"] = QKV                # o reads the q rows of the qkv output (row stride QKV)
+            ops[4].update(src_n=0, src_ld=0)     # gemvM has no 'sum' prologue (engine/llm/lops_spec.js:64): raw
+        return ops
+
+    def _args(self, f):
+        return capi.gemvm_args(**f) if self.gemvM else capi.gemv_args(**f)
+
+    def _enqueue(self):
+        for f in self.ops(self.dev | self.out):
+            (capi.q4_gemvM if self.gemvM else capi.q4_gemv)(self._args(f))
+
+    def make_chain(self):
+        return capi.chain(self._enqueue)
+
+    def reset_outputs(self):
+        for b in self.out.values():
+            b.fill_u32(NAN)
+        self.dev["mx"].upload(self.host["mx"])
+
+    def read(self):
+        r = {k: self.out[k].read(np.float32, n) for k, n in self.out_len.items()}
+        r["mx"] = self.dev["mx"].read(np.float32, self.mx_len)
+        return r
+
+    def check_against_oracle(self, got, what):
+        """each op vs the oracle on the input it read (the GPU's previous output)"""
+        mx = self.host["mx"].copy()
+        names = ["qkv", "o", "gu", "dn", "sum", "hd"]
+        weights = ["w_qkv", "w_o", "w_gu", "w_dn", "w_sum", "w_hd"]
+        inputs = {"qkv": self.host["x"], "o": got["qkv"], "gu": got["o"], "dn": got["gu"], "sum": got["dn"],
+                  "hd": got["sum"]}
+        for i, (name, f) in enumerate(zip(names, self.ops({k: 0 for k in list(self.host) + names}))):
+            y = np.full(self.out_len[name], np.nan, np.float32)
+            xin = np.ascontiguousarray(inputs[name], np.float32)
+            ptrs = {"w": self.host[weights[i]].ctypes.data,
+                    "x": xin.ctypes.data, "y": y.ctypes.data, "norm": self.host["norm"].ctypes.data}
+            f = dict(f, **ptrs)
+            if "stat" in f:
+                f["stat"] = (mx if f["epi"] == capi.EPI["softcap"] else self.host["stat"]).ctypes.data
+            if "mx" in f:
+                f["mx"] = mx.ctypes.data
+            (O.q4_gemvM if self.gemvM else O.q4_gemv)(self._args(f))
+            _check(got[name], y, f"{what} op {i} ({name})")
+        NT = self.V // 64
+        gm, om = got["mx"][:2 * NT * self.M:2], mx[:2 * NT * self.M:2]
+        assert np.allclose(gm, om, rtol=1e-5, atol=1e-5), what + ": tile maxima"
+        gi = got["mx"][1:2 * NT * self.M:2].view(np.uint32)
+        oi = mx[1:2 * NT * self.M:2].view(np.uint32)
+        assert np.mean(gi == oi) > 0.99, what + ": tile argmax"
+
+    def free(self):
+        for b in list(self.dev.values()) + list(self.out.values()):
+            b.free()
+
+
+@pytest.mark.parametrize("M,gemvM", [(1, False), (1, True), (3, True), (8, True)])
+def test_chain_matches_oracle(dev, M, gemvM):
+    s = MiniStep(M=M, gemvM=gemvM, seed=10 + M)
+    ch = s.make_chain()
+    info = ch.info()
+    print("chain", info, flush=True)
+    assert info["n_ops"] == 6 and info["m"] == M
+    s.reset_outputs()
+    ch.run()
+    assert not ch.status()
+    s.check_against_oracle(s.read(), f"chain M={M} gemvM={gemvM}")
+    ch.free()
+    s.free()
+
+
+def test_chain_reruns_are_identical_and_reset(dev):
+    """the chain leaves its counts at zero: every run computes the same bits (fixed plan, ordered reductions)"""
+    s = MiniStep(seed=21)
+    ch = s.make_chain()
+    first = None
+    for r in range(4):
+        s.reset_outputs()
+        ch.run()
+        assert not ch.status()
+        got = s.read()
+        if first is None:
+            first = got
+            s.check_against_oracle(got, "chain run 0")
+        else:
+            for k in first:
+                assert np.array_equal(first[k].view(np.uint32), got[k].view(np.uint32)), f"run {r}: {k}"
+    ch.free()
+    s.free()
+
+
+def test_chain_equals_standalone_calls(dev):
+    """the same ops launched one by one agree with the chain to the fp32 bar"""
+    s = MiniStep(seed=31)
+    ch = s.make_chain()
+    s.reset_outputs()
+    ch.run()
+    assert not ch.status()
+    chained = s.read()
+    s.reset_outputs()
+    s._enqueue()
+    capi.done()
+    single = s.read()
+    for k in ("qkv", "o", "gu", "dn", "sum", "hd"):
+        _check(chained[k], single[k], f"chain vs standalone {k}")
+    ch.free()
+    s.free()
+
+
+@pytest.mark.parametrize("knob,value", [(0, 8), (1, 2)])
+def test_chain_other_plans(dev, knob, value):
+    """8-wave workgroups; and K split across workgroups inside the chain (cross-workgroup reduction + counts)"""
+    old = capi.chain_tune(knob, value)
+    try:
+        s = MiniStep(seed=41 + knob)
+        ch = s.make_chain()
+    finally:
+        capi.chain_tune(knob, old)
+    print("chain", ch.info(), flush=True)
+    for _ in range(2):
+        s.reset_outputs()
+        ch.run()
+        assert not ch.status()
+        s.check_against_oracle(s.read(), f"chain knob {knob}={value}")
+    ch.free()
+    s.free()
+
+
+def test_chain_inside_recording(dev):
+    """a chain run captured into a recording replays correctly, with eager work between the replays"""
+    s = MiniStep(seed=51)
+    ch = s.make_chain()
+    s.reset_outputs()
+    ch.run()
+    want = s.read()
+    rec = capi.record(ch.run)
+    for r in range(3):
+        s.reset_outputs()
+        rec.replay()
+        capi.done()
+        got = s.read()
+        for k in want:
+            assert np.array_equal(want[k].view(np.uint32), got[k].view(np.uint32)), f"replay {r}: {k}"
+    assert not ch.status()
+    rec.free()
+    ch.free()
+    s.free()
+
+
+def test_chain_large_ops(dev):
+    """decode-sized ops: a head with two tiles per wave (65536 rows) after a 2048-wide qkv, checked on sampled rows"""
+    D, V = 2048, 65536
+    w1 = O.fill_q4_sym(3072, D, 5, 0.02)
+    w2 = O.fill_q4_sym(V, 3072, 6, 0.02)
+    x = O.randn(D, 7)
+    b = {k: capi.to_device(v) for k, v in dict(w1=w1, w2=w2, x=x).items()}
+    y1, y2 = capi.Buffer(3072 * 4).fill_u32(NAN), capi.Buffer(V * 4).fill_u32(NAN)
+
+    def enqueue():
+        capi.q4_gemv(capi.gemv_args(w=b["w1"], w_rows=3072, w_cols=D, x=b["x"], N=3072, K=D, y=y1))
+        capi.q4_gemv(capi.gemv_args(w=b["w2"], w_rows=V, w_cols=3072, x=y1, N=V, K=3072, y=y2))
+
+    ch = capi.chain(enqueue)
+    print("chain", ch.info(), flush=True)
+    ch.run()
+    assert not ch.status()
+    g1, g2 = y1.read(np.float32), y2.read(np.float32)
+    want1 = np.full(3072, np.nan, np.float32)
+    O.q4_gemv(capi.gemv_args(w=w1.ctypes.data, w_rows=3072, w_cols=D, x=x.ctypes.data, N=3072, K=D,
+                             y=want1.ctypes.data))
+    _check(g1, want1, "large chain op 0")
+    rows = np.r_[0:64, 30000:30064, V - 64:V]
+    tiles = np.unique(rows // 64)
+    sub = np.concatenate([w2.reshape(V // 64, -1)[t] for t in tiles])     # the sampled tiles' records
+    want2 = np.full(len(tiles) * 64, np.nan, np.float32)
+    O.q4_gemv(capi.gemv_args(w=sub.ctypes.data, w_rows=len(tiles) * 64, w_cols=3072, x=g1.ctypes.data,
+                             N=len(tiles) * 64, K=3072, y=want2.ctypes.data))
+    _check(g2[np.concatenate([np.arange(t * 64, t * 64 + 64) for t in tiles])], want2, "large chain op 1 (sampled)")
+    assert np.all(np.isfinite(g2))
+    ch.free()
+    for v in list(b.values()) + [y1, y2]:
+        v.free()
+
+
+def test_chain_bounded_wait_reports_and_recovers(dev):
+    """a wait forced to give up (a spin limit of 1 poll, set from the host) is reported by p0_chain_status, the
+    launch still ends, and the next run with the normal limit is correct again. Both ops have 65536 rows, so every
+    workgroup waits for the slowest one of the first op."""
+    D, V = 2048, 65536
+    w1 = O.fill_q4_sym(V, D, 8, 0.02)
+    w2 = O.fill_q4_sym(V, D, 9, 0.02)
+    x = O.randn(D, 10)
+    b = {k: capi.to_device(v) for k, v in dict(w1=w1, w2=w2, x=x).items()}
+    y1, y2 = capi.Buffer(V * 4), capi.Buffer(V * 4)
+
+    def enqueue():
+        capi.q4_gemv(capi.gemv_args(w=b["w1"], w_rows=V, w_cols=D, x=b["x"], N=V, K=D, y=y1))
+        capi.q4_gemv(capi.gemv_args(w=b["w2"], w_rows=V, w_cols=D, x=y1, x_rowB=4096, N=V, K=D, y=y2))
+
+    ch = capi.chain(enqueue)
+    old = capi.chain_tune(2, 1)
+    try:
+        ch.run()
+        assert ch.status(), "one-poll waits behind a 65536-row op should have given up"
+    finally:
+        capi.chain_tune(2, old)
+    y1.fill_u32(NAN)
+    y2.fill_u32(NAN)
+    ch.run()
+    assert not ch.status()
+    g1, g2 = y1.read(np.float32), y2.read(np.float32)
+    assert np.all(np.isfinite(g2))
+    want = np.full(128, np.nan, np.float32)
+    head = np.ascontiguousarray(w2[:2 * (D // 32) * 1280])            # tiles 0 and 1
+    O.q4_gemv(capi.gemv_args(w=head.ctypes.data, w_rows=128, w_cols=D, x=g1.ctypes.data, x_rowB=4096, N=128, K=D,
+                             y=want.ctypes.data))
+    _check(g2[:128], want, "after recovery")
+    ch.free()
+    for v in list(b.values()) + [y1, y2]:
+        v.free()
+
+
+def test_chain_errors(dev):
+    capi.check(capi.lib().p0_chain_begin())
+    with pytest.raises(capi.P0Error, match="already being built"):
+        capi.check(capi.lib().p0_chain_begin())
+    with pytest.raises(capi.P0Error, match="holds no ops"):
+        capi.check(capi.lib().p0_chain_end(capi.C.byref(capi.vp())))
+    w, x, y = capi.to_device(_w(64, 64, 1)), capi.to_device(O.randn(64, 2)), capi.Buffer(256)
+
+    def mixed():
+        capi.q4_gemv(capi.gemv_args(w=w, w_rows=64, w_cols=64, x=x, N=64, K=64, y=y))
+        capi.q4_gemvM(capi.gemvm_args(w=w, w_rows=64, w_cols=64, x=x, x_ldx=0, M=2, N=64, K=64, y=y))
+
+    with pytest.raises(capi.P0Error, match="one M"):
+        capi.chain(mixed)
+    # the failed build left no chain open: a fresh one builds
+    ch = capi.chain(lambda: capi.q4_gemv(capi.gemv_args(w=w, w_rows=64, w_cols=64, x=x, N=64, K=64, y=y)))
+    ch.run()
+    assert not ch.status()
+    ch.free()
+    for v in (w, x, y):
+        v.free()
