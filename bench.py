@@ -5,7 +5,8 @@
 
 Headline (`value`): tokens/s of the Gemma-4-E2B-shaped decode step at M=1 (config B): 30 layers x {qkv 3072x2048 rms,
 o 2048x2048 raw kPer 2048, gate_up 2x8192x2048 rms+geglu, down 2048x8192 raw kPer 2048} + lm_head 262144x2048
-rms+softcap (tile max/argmax) = 121 GEMV launches, recorded once and replayed per token (the DecodeRunner analogue).
+rms+softcap (tile max/argmax) = 121 GEMV ops, planned once into a chain that runs as ONE persistent launch per token
+(the DecodeRunner analogue); the same ops recorded as 121 launches are timed beside it.
 Attention, norms and the PLE projections are not part of the step.
 
 Also reported: the step's weight-streaming GB/s, config A (one 8192x2048 GEMV, weight ring of 32 copies), the
@@ -127,30 +128,53 @@ class Step:
         return tot
 
 
-def time_replays(c, rec, warmup, reps):
+def time_runs(c, run, warmup, reps):
+    """ms per run(): HIP events on the library's stream around `reps` back-to-back runs"""
     for _ in range(warmup):
-        rec.replay()
+        run()
     c.done()
     c.timer_start()
     for _ in range(reps):
-        rec.replay()
+        run()
     return c.timer_stop() / reps
 
 
+def time_chain(c, ops, warmup, reps):
+    """ops planned into one chain (p0_chain_*), timed per run; raises if any run's wait gave up"""
+    ch = c.chain(ops)
+    try:
+        ms = time_runs(c, ch.run, warmup, reps)
+        if ch.status():
+            raise RuntimeError("a chain wait gave up during the benchmark")
+        return ms, ch.info()
+    finally:
+        ch.free()
+
+
+def time_recording(c, ops, warmup, reps):
+    """ops recorded as one launch per op (HIP graph), timed per replay"""
+    rec = c.record(ops)
+    try:
+        return time_runs(c, rec.replay, warmup, reps)
+    finally:
+        rec.free()
+
+
 def bench_decode(c, step, steps, warmup):
+    """the M=1 step as one chain (the product path), and as a recording of 121 launches for comparison"""
     step.alloc(1)
-    rec = c.record(step.ops)
-    ms = time_replays(c, rec, warmup, steps)
-    rec.free()
+    ms, info = time_chain(c, step.ops, warmup, steps)
+    ms_graph = time_recording(c, step.ops, warmup, steps)
     by_kind = {}
     for kind in ("qkv", "o", "gu", "down", "head"):
-        r = c.record(lambda: step.ops(kind))
-        kms = time_replays(c, r, 3, 20)
-        r.free()
+        kms, _ = time_chain(c, lambda: step.ops(kind), 3, 20)
+        kms_graph = time_recording(c, lambda: step.ops(kind), 3, 20)
         launches = 1 if kind == "head" else LAYERS
-        by_kind[kind] = {"ms_total": round(kms, 4), "us_per_launch": round(kms * 1e3 / launches, 2),
-                         "GBps": round(step.step_bytes(kind) / (kms * 1e-3) / 1e9, 1)}
-    out = {"ms": ms, "bytes": step.step_bytes(), "by_kind": by_kind}
+        by_kind[kind] = {"ms_total": round(kms, 4), "us_per_op": round(kms * 1e3 / launches, 2),
+                         "GBps": round(step.step_bytes(kind) / (kms * 1e-3) / 1e9, 1),
+                         "us_per_launch_one_launch_per_op": round(kms_graph * 1e3 / launches, 2)}
+    out = {"ms": ms, "ms_one_launch_per_op": ms_graph, "bytes": step.step_bytes(), "by_kind": by_kind,
+           "chain": info}
     step.free_acts()
     return out
 
@@ -159,11 +183,11 @@ def bench_verify(c, step, Ms=(1, 2, 4, 5, 8, 16)):
     res = {}
     for M in Ms:
         step.alloc(M)
-        rec = c.record(step.ops)
-        ms = time_replays(c, rec, 3, 10)
-        rec.free()
+        ms, _ = time_chain(c, step.ops, 3, 10)
+        ms_graph = time_recording(c, step.ops, 3, 10)
         res[str(M)] = {"ms_per_pass": round(ms, 4), "tok_per_s": round(M / (ms * 1e-3), 1),
-                       "GBps": round(step.step_bytes() / (ms * 1e-3) / 1e9, 1)}
+                       "GBps": round(step.step_bytes() / (ms * 1e-3) / 1e9, 1),
+                       "ms_one_launch_per_op": round(ms_graph, 4)}
         step.free_acts()
     return res
 
@@ -184,9 +208,7 @@ def bench_config_a(c, reps=8):
         for b in ws:
             c.q4_gemv(c.gemv_args(w=b, w_rows=N, w_cols=K, x=x, N=N, K=K, y=y))
 
-    rec = c.record(ops)
-    ms = time_replays(c, rec, 2, reps) / R
-    rec.free()
+    ms = time_recording(c, ops, 2, reps) / R
     for b in ws + [x, y]:
         b.free()
     byts = N * K * Q4_BYTES_PER_W + K * 4 + N * 4
@@ -211,9 +233,7 @@ def bench_gemm(c, M, shapes, reps=5):
     for name, b, n, k in ws:
         args = c.gemm_args(w=b, w_rows=n, w_cols=k, x=x, x_ld=k, x_mode=c.XMODE["bf16"], M=M, N=n, K=k,
                            epi=c.GEPI["f16"], y=y)
-        rec = c.record(lambda: c.q4_gemm(args))
-        ms = time_replays(c, rec, 2, reps)
-        rec.free()
+        ms = time_recording(c, lambda: c.q4_gemm(args), 2, reps)
         fl = 2.0 * M * n * k
         res[name] = {"ms": round(ms, 4), "TFLOPS": round(fl / (ms * 1e-3) / 1e12, 1)}
         tot_fl += fl
@@ -287,7 +307,8 @@ def main():
 
     extra = {"decode_step": {"ms": round(ms, 4), "algorithmic_bytes": int(dec["bytes"]),
                              "GBps": round(step_gbps, 1), "frac_hbm_peak": round(step_gbps / HBM_PEAK_GBPS, 4),
-                             "by_projection": dec["by_kind"]}}
+                             "ms_one_launch_per_op": round(dec["ms_one_launch_per_op"], 4),
+                             "chain": dec["chain"], "by_projection": dec["by_kind"]}}
     if not args.no_extra:
         extra["config_a_gemv"] = bench_config_a(c)
         log("config A", extra["config_a_gemv"])
@@ -306,19 +327,17 @@ def main():
                 c, 32760, [("qkv", 9216, 3072), ("glu_up", 16384, 3072), ("down", 3072, 8192)], reps=2)
             log("gemm SANA", extra["gemm_sana_video_M32760"])
 
-    # the dominant kernel: the gate_up GEMV (mode-2 q4_gemv_kernel, 43% of the step's bytes), back-to-back over the
-    # 30 layers' distinct weights (629 MB > the last-level cache)
-    gu = dec["by_kind"]["gu"]
-    gu_bytes_per_launch = 2 * MLP * D * Q4_BYTES_PER_W + D * 4 + MLP * 4
-    achieved = gu_bytes_per_launch / (gu["us_per_launch"] * 1e-6) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                "kernel": "q4_gemv_kernel<1,2> (gate_up 16384x2048 rms+geglu)",
-                "bytes_per_launch": int(gu_bytes_per_launch), "us_per_launch": gu["us_per_launch"]}
+    # the dominant kernel: the chain kernel running the whole step (one launch per token); its algorithmic bytes are
+    # the step's weights + activations in and out (step_bytes), its duration the event-timed run
+    roofline = {"bound": "hbm", "achieved": round(step_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(step_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                "kernel": "q4_gemv_chain_kernel<1,%d> (the whole M=1 decode step: 121 GEMV ops, one launch)"
+                          % dec["chain"]["waves_per_workgroup"],
+                "bytes_per_launch": int(dec["bytes"]), "us_per_launch": round(ms * 1e3, 2)}
     prof = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(prof):
         try:
-            roofline["traffic"] = json.load(open(prof)).get("gate_up_gemv_bytes_per_launch")
+            roofline["traffic"] = json.load(open(prof)).get("decode_chain_bytes_per_launch")
         except Exception:
             pass
 
@@ -335,7 +354,7 @@ def main():
         "config": {"workload": "gemma4-e2b-shaped decode step, M=1: 30 x {qkv 3072x2048 rms, o 2048x2048, "
                                "gate_up 2x8192x2048 rms+geglu, down 2048x8192 kPer 2048} + lm_head 262144x2048 "
                                "rms+softcap; q4g32a.t64 int4 weights (0.625 B/weight), fp32 accumulate",
-                   "weights_GB": round(step.weight_bytes / 1e9, 3), "launches_per_step": 121,
+                   "weights_GB": round(step.weight_bytes / 1e9, 3), "launches_per_step": 1, "gemv_ops_per_step": 121,
                    "gemv_GBps": round(step_gbps, 1),
                    "gemm_TFLOPS_M4608": extra.get("gemm_flux2_klein_M4608", {}).get("TFLOPS")},
         "roofline": roofline, "cpu_baseline": cpu, "extra": extra,

@@ -200,8 +200,10 @@ int p0_chain_status(void* chain, int32_t* timed_out);
 int p0_chain_info(void* chain, p0_chain_info_t* out);
 int p0_chain_free(void* chain);
 /* knob 0: waves per chain workgroup for M = 1 (8 or 16, default 16); knob 1: largest wave share in q4 groups before
- * a chain op splits K across workgroups (default 16); knob 2: polls before a chain wait gives up (default 2^22).
- * Applies to chains begun afterwards (knob 2: to runs). value <= 0 only queries; returns the previous value. */
+ * a chain op splits K across workgroups (default 16); knob 2: polls before a chain wait gives up (default 2^22);
+ * knob 3: 1 = every wait of later runs gives up at once (for tests of the timed-out path), 0 = normal.
+ * Knobs 0-1 apply to chains begun afterwards, 2-3 to runs. value < 0 only queries (knobs 0-2 also ignore 0);
+ * returns the previous value. */
 int p0_chain_tune(int knob, int value);
 
 /* ---- synthetic weights on the device (the reference's GPU filler, engine/tune/autotune.js:73-87) ----------------- */

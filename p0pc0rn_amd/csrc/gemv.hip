@@ -108,6 +108,7 @@ static chain_kernel_t pick_chain(int M, int W) {
 static int g_chain_waves = 16;          // waves per chain workgroup for M = 1 (8 or 16)
 static int g_chain_split_gpw = 16;      // a wave share above this many groups splits K across workgroups
 static int g_chain_spin = 1 << 22;      // polls before a chain wait gives up (about 0.3 s)
+static int g_chain_force_give_up = 0;   // tests: every wait gives up at once
 static constexpr size_t kChainLds = 64 * 1024;
 
 struct ChainBuild {
@@ -119,6 +120,7 @@ struct ChainBuild {
 struct ChainExec {
   GemvP* ops;
   unsigned* st;
+  size_t st_words;
   int n_ops, M, W, grid;
   size_t lds;
   chain_kernel_t kernel;
@@ -336,6 +338,7 @@ extern "C" int p0_chain_end(void** out) {
   if (per_cu < 1) { set_error("p0_chain_end: a chain workgroup does not fit a CU"); return P0_EINVAL; }
   int grid = ctx().cu_count * per_cu;
   if (grid > cb->G) grid = cb->G;   // the plans were made for G workgroups; never more than are resident
+  if (grid > kChainMaxGrid) grid = kChainMaxGrid;
   auto* ex = new ChainExec{};
   ex->n_ops = (int)cb->ops.size();
   ex->M = cb->M;
@@ -343,7 +346,10 @@ extern "C" int p0_chain_end(void** out) {
   ex->grid = grid;
   ex->lds = cb->lds;
   ex->kernel = k;
-  const size_t ob = cb->ops.size() * sizeof(GemvP), sb = (cb->ops.size() + 2) * sizeof(unsigned);
+  // chain state: last tag, timed out (one 128-byte line each), then one flag per (op, workgroup)
+  const size_t words = kFlagBase + cb->ops.size() * (size_t)grid;
+  const size_t ob = cb->ops.size() * sizeof(GemvP), sb = words * sizeof(unsigned);
+  ex->st_words = words;
   hipError_t e = hipMalloc((void**)&ex->ops, ob);
   if (e == hipSuccess) e = hipMalloc((void**)&ex->st, sb);
   if (e == hipSuccess) e = hipMemcpy(ex->ops, cb->ops.data(), ob, hipMemcpyHostToDevice);
@@ -364,7 +370,7 @@ extern "C" int p0_chain_run(void* chain) {
   if (g_chain) { set_error("p0_chain_run: a chain is being built"); return P0_EINVAL; }
   auto* ex = (ChainExec*)chain;
   hipLaunchKernelGGL(ex->kernel, dim3((unsigned)ex->grid), dim3(64 * ex->W), ex->lds, ctx().cur, ex->ops, ex->n_ops,
-                     ex->st, g_chain_spin);
+                     ex->st, g_chain_force_give_up ? -1 : g_chain_spin);
   P0_LAUNCHED("p0_chain_run");
   return P0_OK;
 }
@@ -375,10 +381,10 @@ extern "C" int p0_chain_status(void* chain, int32_t* timed_out) {
   auto* ex = (ChainExec*)chain;
   P0_HIP(hipStreamSynchronize(ctx().cur), "p0_chain_status");
   unsigned v = 0;
-  P0_HIP(hipMemcpy(&v, ex->st + ex->n_ops + 1, sizeof v, hipMemcpyDeviceToHost), "p0_chain_status");
+  P0_HIP(hipMemcpy(&v, ex->st + kCtrStride, sizeof v, hipMemcpyDeviceToHost), "p0_chain_status");
   if (v) {
-    // an abandoned run can leave completion counts and split-K arrival counters mid-way: start both from zero
-    P0_HIP(hipMemset(ex->st, 0, (ex->n_ops + 2) * sizeof(unsigned)), "p0_chain_status");
+    // an abandoned run can leave split-K arrival counters mid-way: clear them, and the chain state with them
+    P0_HIP(hipMemset(ex->st, 0, ex->st_words * sizeof(unsigned)), "p0_chain_status");
     P0_HIP(hipMemset(ctx().counters, 0, ctx().n_counters * sizeof(unsigned)), "p0_chain_status");
     P0_HIP(hipDeviceSynchronize(), "p0_chain_status");
   }
@@ -408,8 +414,14 @@ extern "C" int p0_chain_free(void* chain) {
 }
 
 // chain knobs: 0 = waves per workgroup for M = 1 (8 or 16), 1 = largest wave share (groups) before K is split
-// across workgroups, 2 = polls before a wait gives up. Returns the previous value; a value <= 0 only reads.
+// across workgroups, 2 = polls before a wait gives up, 3 = 1: every wait gives up at once (tests). Returns the
+// previous value; a value < 0 only reads (knob 3 also takes 0).
 extern "C" int p0_chain_tune(int knob, int value) {
+  if (knob == 3) {
+    const int old = g_chain_force_give_up;
+    if (value >= 0) g_chain_force_give_up = value ? 1 : 0;
+    return old;
+  }
   int* t = knob == 0 ? &g_chain_waves : knob == 1 ? &g_chain_split_gpw : knob == 2 ? &g_chain_spin : nullptr;
   if (!t) return -1;
   const int old = *t;

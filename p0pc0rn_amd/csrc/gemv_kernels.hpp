@@ -30,6 +30,10 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 // 4-byte alignment is all a record base guarantees (weight offsets are multiples of 4, engine/llm/lops.js:124);
 // global_load_dwordx4 needs only dword alignment, so one 16-byte load per lane serves both cases
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
+// Global-memory view of a pointer. Pointers read from memory (a chain's op table) are generic to the compiler, which
+// then emits flat instructions; flat loads also count on the LDS wait counter, so every LDS wait would wait for the
+// weight stream too. The cast makes them global loads / stores / atomics again.
+#define P0_GLOBAL(T, ptr) ((__attribute__((address_space(1))) T*)(ptr))
 
 
 struct GemvP {
@@ -60,14 +64,31 @@ __device__ __forceinline__ float gelu_tanh(float v) {   // engine/llm/lops.js:26
   return v * 0.5f * (1.0f + tanhf(t));
 }
 
+// Activation loads and output stores. Inside a chain (COH), ops hand data to each other within one launch: outputs are
+// written with device-coherent stores and inputs read with device-coherent loads (relaxed agent-scope atomics: they
+// bypass the non-coherent per-XCD L2 copies), so no whole-L2 writeback / invalidate is needed around the hand-off.
+template <bool COH>
+__device__ __forceinline__ float ldf(const float* a) {
+  if (COH) return __hip_atomic_load(P0_GLOBAL(float, const_cast<float*>(a)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return *P0_GLOBAL(const float, a);
+}
+template <bool COH>
+__device__ __forceinline__ void stf(float* a, float v) {
+  if (COH) __hip_atomic_store(P0_GLOBAL(float, a), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *P0_GLOBAL(float, a) = v;
+}
+
 // prologue value x'[m][k] (engine/llm/lops.js:50-57, engine/llm/lops_spec.js:61-64)
+template <bool COH>
 __device__ __forceinline__ float prologue(const GemvP& p, int m, int k) {
-  if (p.pro == P0_PRO_RAW) return p.X[m * p.ldx + p.rowB + k];
-  if (p.pro == P0_PRO_RMS) return p.X[m * p.ldx + p.rowB + k] * p.ST[p.statOff + m * p.statLd] * p.NW[p.nOff + k];
+  if (p.pro == P0_PRO_RAW) return ldf<COH>(&p.X[m * p.ldx + p.rowB + k]);
+  if (p.pro == P0_PRO_RMS)
+    return ldf<COH>(&p.X[m * p.ldx + p.rowB + k]) * ldf<COH>(&p.ST[p.statOff + m * p.statLd]) *
+           ldf<COH>(&p.NW[p.nOff + k]);
   float s = 0.0f;
-  for (int j = 0; j < p.nsrc; ++j) s += p.X[j * p.ldp + m * p.ldx + k];
+  for (int j = 0; j < p.nsrc; ++j) s += ldf<COH>(&p.X[j * p.ldp + m * p.ldx + k]);
   if (p.pro == P0_PRO_SUM) return s;
-  return gelu_tanh(s) * p.EV[p.evOff + m * p.evLd + k];
+  return gelu_tanh(s) * ldf<COH>(&p.EV[p.evOff + m * p.evLd + k]);
 }
 
 struct Rec {
@@ -78,8 +99,8 @@ struct Rec {
 __device__ __forceinline__ Rec load_rec(const GemvP& p, int64_t tile, int g, int lane) {
   const uint8_t* rec = p.w + (int64_t)__builtin_amdgcn_readfirstlane((int)((tile * p.wG + g) >> 0)) * 1280;
   Rec r;
-  r.q = __builtin_nontemporal_load((const u32x4*)(rec + lane * 16));
-  r.sm = __builtin_nontemporal_load((const uint32_t*)(rec + 1024 + lane * 4));
+  r.q = __builtin_nontemporal_load(P0_GLOBAL(const u32x4, rec + lane * 16));
+  r.sm = __builtin_nontemporal_load(P0_GLOBAL(const uint32_t, rec + 1024 + lane * 4));
   return r;
 }
 
@@ -122,21 +143,22 @@ __device__ __forceinline__ void wave_argmax(float& v, int& r) {
 }
 
 // the epilogue of one wave for x row m: tot0 = row sums of tile0 (gate tile for a geglu), tot1 = the up tile's
+template <bool COH>
 __device__ __forceinline__ void epilogue(const GemvP& p, int split, int m, int tile0, int lane, float tot0, float tot1) {
   const int n = tile0 * 64 + lane;
   if (p.epi == P0_EPI_STORE) {
-    p.Y[split * p.ldy + m * p.ldm + n] = tot0;
+    stf<COH>(&p.Y[split * p.ldy + m * p.ldm + n], tot0);
   } else if (p.epi == P0_EPI_GEGLU) {
-    p.Y[m * p.ldm + n] = gelu_tanh(tot0) * tot1;
+    stf<COH>(&p.Y[m * p.ldm + n], gelu_tanh(tot0) * tot1);
   } else {
     float v = p.cap * tanhf(fminf(15.0f, fmaxf(-15.0f, tot0 / p.cap)));
-    p.Y[m * p.ldm + n] = v;
+    stf<COH>(&p.Y[m * p.ldm + n], v);
     int r = lane;
     wave_argmax(v, r);
     if (lane == 0) {
       const int o = (m * p.NT + tile0) * 2;
-      p.MX[o] = v;
-      p.MX[o + 1] = __int_as_float(tile0 * 64 + r);
+      stf<COH>(&p.MX[o], v);
+      stf<COH>(&p.MX[o + 1], __int_as_float(tile0 * 64 + r));
     }
   }
 }
@@ -148,8 +170,10 @@ __device__ __forceinline__ void epilogue(const GemvP& p, int split, int m, int t
 // before its input is read (the chain executor waits for the producing op there; a standalone launch has nothing to
 // wait for); it returns false (in every thread) to abandon the item. Returns true when this workgroup wrote the
 // final outputs of its (split, tile block): always for one K-slice per split, only the last arriving workgroup
-// otherwise. The value is the same in every thread.
-template <int M, int MODE, class Ready>
+// otherwise. The value is the same in every thread. CHAIN: activations move through device-coherent accesses, and
+// wave 0 (whose first thread polls in `ready()`) issues its first chunk after the wait, so that its poll does not
+// queue behind its own weight loads (a wave's loads return in order).
+template <int M, int MODE, bool CHAIN, class Ready>
 __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float* smem, int* s_last, Ready&& ready) {
   constexpr int T = MODE == 0 ? 1 : 2;
   constexpr int TPW = MODE == 1 ? 2 : 1;   // distinct output tiles per wave
@@ -194,19 +218,26 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
   // ---- the share's first chunk is issued before the input is read: its latency overlaps the wait and the prologue
   __syncthreads();   // the previous item of this workgroup is done with the LDS
   Rec r0[D][T];
-  if (streams) {
+  const bool late = CHAIN && wv == 0;
+  if (streams && !late) {
 #pragma unroll
     for (int i = 0; i < D; ++i)
 #pragma unroll
       for (int t = 0; t < T; ++t) r0[i][t] = load_rec(p, tl(t), min(wg0 + i, glast), lane);
   }
   if (!ready()) return false;
+  if (streams && late) {
+#pragma unroll
+    for (int i = 0; i < D; ++i)
+#pragma unroll
+      for (int t = 0; t < T; ++t) r0[i][t] = load_rec(p, tl(t), min(wg0 + i, glast), lane);
+  }
 
   // ---- prologue: x'[m][k] for the workgroup's K-slice -> LDS (odd k scaled 1/16), then per-group sums of x'
   const int kb = g0 * 32, ke = g1 * 32;
   for (int idx = tid; idx < M * KL; idx += blockDim.x) {
     const int m = idx / KL, kl = idx - m * KL, k = kb + kl;
-    float v = k < ke ? prologue(p, m, k) : 0.0f;
+    float v = k < ke ? prologue<CHAIN>(p, m, k) : 0.0f;
     xs[idx] = (k & 1) ? v * 0.0625f : v;
   }
   __syncthreads();
@@ -289,11 +320,11 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         if (MODE == 2) {
-          epilogue(p, split, m, tile[0], lane, acc[0][m], acc[T - 1][m]);
+          epilogue<CHAIN>(p, split, m, tile[0], lane, acc[0][m], acc[T - 1][m]);
         } else {
 #pragma unroll
           for (int t = 0; t < T; ++t)
-            if (tile[t] < p.NT) epilogue(p, split, m, tile[t], lane, acc[t][m], 0.0f);
+            if (tile[t] < p.NT) epilogue<CHAIN>(p, split, m, tile[t], lane, acc[t][m], 0.0f);
         }
       }
     }
@@ -310,18 +341,18 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
       const int row = (MODE == 2 && t == 1) ? p.N + tile[0] * 64 + lane : tile[t] * 64 + lane;
       if (MODE != 1 || tile[t] < p.NT) {
 #pragma unroll
-        for (int m = 0; m < M; ++m) p.part[sliceBase + ((size_t)ks * M + m) * p.rowsTot + row] = acc[t][m];
+        for (int m = 0; m < M; ++m) *P0_GLOBAL(float, &p.part[sliceBase + ((size_t)ks * M + m) * p.rowsTot + row]) = acc[t][m];
       }
     }
   }
   __syncthreads();
   if (tid == 0) {
     __threadfence();   // release: the workgroup's partials reach memory before the arrival count
-    unsigned* c = p.cnt + (size_t)split * p.ntb + bx;
-    const unsigned prev = atomicAdd(c, 1u);
+    auto* c = P0_GLOBAL(unsigned, p.cnt + (size_t)split * p.ntb + bx);
+    const unsigned prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int last = prev == (unsigned)(p.nks - 1);
     if (last) {
-      atomicExch(c, 0u);   // leave the counter at zero for the next use
+      __hip_atomic_exchange(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // leave the counter at zero
       __threadfence();     // acquire: every other workgroup's partials
     }
     *s_last = last;
@@ -338,15 +369,15 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
       tot[t] = 0.0f;
       const int row = (MODE == 2 && t == 1) ? p.N + tile[0] * 64 + lane : tile[t] * 64 + lane;
       if (MODE != 1 || tile[t] < p.NT) {
-        for (int s = 0; s < p.nks; ++s) tot[t] += p.part[sliceBase + ((size_t)s * M + m) * p.rowsTot + row];
+        for (int s = 0; s < p.nks; ++s) tot[t] += *P0_GLOBAL(const float, &p.part[sliceBase + ((size_t)s * M + m) * p.rowsTot + row]);
       }
     }
     if (MODE == 2) {
-      epilogue(p, split, m, tile[0], lane, tot[0], tot[T - 1]);
+      epilogue<CHAIN>(p, split, m, tile[0], lane, tot[0], tot[T - 1]);
     } else {
 #pragma unroll
       for (int t = 0; t < T; ++t)
-        if (tile[t] < p.NT) epilogue(p, split, m, tile[t], lane, tot[t], 0.0f);
+        if (tile[t] < p.NT) epilogue<CHAIN>(p, split, m, tile[t], lane, tot[t], 0.0f);
     }
   }
   return true;
@@ -358,7 +389,7 @@ template <int M, int MODE>
 __global__ __launch_bounds__(M <= 2 ? 1024 : 512) void q4_gemv_kernel(GemvP p) {
   extern __shared__ __attribute__((aligned(16))) float smem[];   // 16-byte aligned: ds_read_b128 of x
   __shared__ int s_last;
-  gemv_item<M, MODE>(p, blockIdx.x, blockIdx.y, smem, &s_last, [] { return true; });
+  gemv_item<M, MODE, false>(p, blockIdx.x, blockIdx.y, smem, &s_last, [] { return true; });
 }
 
 // ---- the chain executor: a recorded sequence of GEMV ops in ONE persistent launch (the analogue of the reference's
@@ -367,69 +398,93 @@ __global__ __launch_bounds__(M <= 2 ? 1024 : 512) void q4_gemv_kernel(GemvP p) {
 // next op's weights stream while the previous op finishes. Items are dealt to workgroups round-robin; every
 // workgroup of the grid is resident at once (the grid is sized from the occupancy), so a wait always ends. Each wait
 // is also bounded: past `spin_limit` polls it sets the timed-out word, and every workgroup abandons the rest of the
-// chain at its next wait, so a launch always finishes (its results are then invalid and reported as such). Completion
-// is counted per op (one count per (split, tile block) whose final outputs are written); the last workgroup to leave
-// resets the counts, so a chain replays any number of times with no memset (capturable).
-// st: [0, n_ops) completion counts, [n_ops] workgroups finished, [n_ops + 1] timed out (sticky until read).
+// chain at its next wait, so a launch always finishes (its results are then invalid and reported as such).
+//
+// Completion is published per workgroup, not counted: when a workgroup has finished its items of op i (or has none),
+// it stores the run's tag into flag[i][workgroup]; op i is complete when all of op i's flags hold the tag. A waiter's
+// wave reads all of them with one round of coherent loads and a ballot, so no atomic sits on the dependency path
+// (device-scope atomics on one address serialise). The tag is the last run's tag + 1, read from the state at the
+// start and stored back at the end, so a chain runs any number of times with no reset (capturable).
+// State words: [0] last tag, [kCtrStride] timed out (sticky until read), then the flags, op i's G words at
+// kFlagBase + i G.
+constexpr int kCtrStride = 32;   // 128 bytes: one line per word that is polled or updated on its own
+constexpr int kFlagBase = 2 * kCtrStride;
+
+__device__ __forceinline__ unsigned ld_coh(const unsigned* a) {
+  return __hip_atomic_load(P0_GLOBAL(unsigned, const_cast<unsigned*>(a)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh(unsigned* a, unsigned v) {
+  __hip_atomic_store(P0_GLOBAL(unsigned, a), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+constexpr int kChainMaxGrid = 512;   // flags one wave reads per poll: 8 per lane
+
+// Run by one whole wave: polls until all G flags hold `tag` (true), or gives up (false, and marks the run timed out).
+// The G loads of a poll are independent, so one poll costs one memory round trip.
+__device__ __forceinline__ bool wait_flags(const unsigned* flags, int G, unsigned tag, int spin_limit,
+                                           unsigned* timed_out, int lane) {
+  for (int spins = 0;; ++spins) {
+    bool ok = spin_limit >= 0;   // spin_limit < 0: the host asks every wait to give up at once (tests)
+    unsigned v[kChainMaxGrid / 64];
+#pragma unroll
+    for (int j = 0; j < kChainMaxGrid / 64; ++j) v[j] = lane + 64 * j < G ? ld_coh(flags + lane + 64 * j) : tag;
+#pragma unroll
+    for (int j = 0; j < kChainMaxGrid / 64; ++j) ok = ok && v[j] == tag;
+    if (__builtin_amdgcn_ballot_w64(!ok) == 0) return true;
+    if (spins >= spin_limit || (spins % 64 == 63 && ld_coh(timed_out))) {
+      if (lane == 0) atomicOr(timed_out, 1u);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
 template <int M, int W>
 __global__ __launch_bounds__(64 * W) void q4_gemv_chain_kernel(const GemvP* __restrict__ ops, int n_ops,
                                                                unsigned* __restrict__ st, int spin_limit) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   __shared__ int s_last, s_go;
-  const int tid = threadIdx.x;
-  unsigned* const finished = st + n_ops;
-  unsigned* const timed_out = st + n_ops + 1;
+  __shared__ unsigned s_tag;
+  const int tid = threadIdx.x, lane = tid & 63, G = gridDim.x;
+  unsigned* const timed_out = st + kCtrStride;
+  unsigned* const flags = st + kFlagBase;
+  if (tid == 0) s_tag = ld_coh(st) + 1;
+  __syncthreads();
+  const unsigned tag = s_tag;
   bool abandon = false;
   for (int i = 0; i < n_ops && !abandon; ++i) {
     const GemvP& p = ops[i];
     const int items = p.ntb * p.nsplit * p.nks;
-    const unsigned need = i > 0 ? (unsigned)(ops[i - 1].ntb * ops[i - 1].nsplit) : 0u;
     bool waited = i == 0;
-    for (int it = blockIdx.x; it < items; it += gridDim.x) {
+    for (int it = blockIdx.x; it < items; it += G) {
       const int bx = it % p.ntb, by = it / p.ntb;
       auto ready = [&]() -> bool {
         if (waited) return true;   // only the workgroup's first item of op i waits for op i - 1
-        if (tid == 0) {
-          int go = 1, spins = 0;
-          while (__hip_atomic_load(&st[i - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
-            if (__hip_atomic_load(timed_out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) || ++spins > spin_limit) {
-              atomicOr(timed_out, 1u);
-              go = 0;
-              break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-          }
-          __threadfence();   // acquire: op i - 1's outputs
-          s_go = go;
+        if (tid < 64) {
+          const bool go = wait_flags(flags + (size_t)(i - 1) * G, G, tag, spin_limit, timed_out, lane);
+          if (lane == 0) s_go = go;   // op i - 1's outputs are read with coherent loads: no L2 invalidate
         }
         __syncthreads();
         waited = true;
         abandon = s_go == 0;
         return !abandon;
       };
-      bool fin;
-      if (p.mode == 0) fin = gemv_item<M, 0>(p, bx, by, smem, &s_last, ready);
-      else if (p.mode == 1) fin = gemv_item<M, 1>(p, bx, by, smem, &s_last, ready);
-      else fin = gemv_item<M, 2>(p, bx, by, smem, &s_last, ready);
+      if (p.mode == 0) gemv_item<M, 0, true>(p, bx, by, smem, &s_last, ready);
+      else if (p.mode == 1) gemv_item<M, 1, true>(p, bx, by, smem, &s_last, ready);
+      else gemv_item<M, 2, true>(p, bx, by, smem, &s_last, ready);
       if (abandon) break;
-      if (fin) {
-        __syncthreads();   // every wave's outputs are written
-        if (tid == 0) {
-          __threadfence();   // release: the outputs reach memory before the count
-          atomicAdd(&st[i], 1u);
-        }
-      }
     }
+    if (abandon) break;
+    // every wave's coherent output stores are complete (acknowledged) before the flag: no L2 writeback
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) st_coh(flags + (size_t)i * G + blockIdx.x, tag);
   }
-  // the last workgroup to leave resets the counts for the next run
-  __syncthreads();
-  if (tid == 0) {
-    __threadfence();
-    if (atomicAdd(finished, 1u) == gridDim.x - 1) {
-      for (int i = 0; i < n_ops; ++i) atomicExch(&st[i], 0u);
-      atomicExch(finished, 0u);
-      __threadfence();
-    }
+  // workgroup 0 stores the tag once every workgroup is through the last op (so every workgroup has read the old
+  // one); a wait that gives up here stores it too, so a run's stale flags never match the next run's tag
+  if (blockIdx.x == 0 && tid < 64) {
+    wait_flags(flags + (size_t)(n_ops - 1) * G, G, tag, abandon ? -1 : spin_limit, timed_out, lane);
+    if (lane == 0) st_coh(st, tag);
   }
 }
 
