@@ -5,8 +5,9 @@
 
 Headline (`value`): tokens/s of the Gemma-4-E2B-shaped decode step at M=1 (config B): 30 layers x {qkv 3072x2048 rms,
 o 2048x2048 raw kPer 2048, gate_up 2x8192x2048 rms+geglu, down 2048x8192 raw kPer 2048} + lm_head 262144x2048
-rms+softcap (tile max/argmax) = 121 GEMV ops, planned once into a chain that runs as ONE persistent launch per token
-(the DecodeRunner analogue); the same ops recorded as 121 launches are timed beside it.
+rms+softcap (tile max/argmax) = 121 GEMV ops, run per token both ways the library offers (the DecodeRunner
+analogue): planned once into a chain that runs as ONE persistent launch, and recorded as a graph of 121 launches;
+the faster is the headline and both are reported.
 Attention, norms and the PLE projections are not part of the step.
 
 Also reported: the step's weight-streaming GB/s, config A (one 8192x2048 GEMV, weight ring of 32 copies), the
@@ -160,21 +161,24 @@ def time_recording(c, ops, warmup, reps):
         rec.free()
 
 
-def bench_decode(c, step, steps, warmup):
-    """the M=1 step as one chain (the product path), and as a recording of 121 launches for comparison"""
+def bench_decode(c, step, steps, warmup, breakdown=True):
+    """the M=1 step two ways, both product paths: one chain launch per token (p0_chain_*) and a recording of 121
+    launches (p0_record_*); the faster is the headline"""
     step.alloc(1)
-    ms, info = time_chain(c, step.ops, warmup, steps)
+    ms_chain, info = time_chain(c, step.ops, warmup, steps)
     ms_graph = time_recording(c, step.ops, warmup, steps)
     by_kind = {}
-    for kind in ("qkv", "o", "gu", "down", "head"):
+    for kind in ("qkv", "o", "gu", "down", "head") if breakdown else ():
         kms, _ = time_chain(c, lambda: step.ops(kind), 3, 20)
         kms_graph = time_recording(c, lambda: step.ops(kind), 3, 20)
         launches = 1 if kind == "head" else LAYERS
-        by_kind[kind] = {"ms_total": round(kms, 4), "us_per_op": round(kms * 1e3 / launches, 2),
-                         "GBps": round(step.step_bytes(kind) / (kms * 1e-3) / 1e9, 1),
-                         "us_per_launch_one_launch_per_op": round(kms_graph * 1e3 / launches, 2)}
-    out = {"ms": ms, "ms_one_launch_per_op": ms_graph, "bytes": step.step_bytes(), "by_kind": by_kind,
-           "chain": info}
+        by_kind[kind] = {"us_per_op_chain": round(kms * 1e3 / launches, 2),
+                         "us_per_launch": round(kms_graph * 1e3 / launches, 2),
+                         "GBps_chain": round(step.step_bytes(kind) / (kms * 1e-3) / 1e9, 1),
+                         "GBps": round(step.step_bytes(kind) / (kms_graph * 1e-3) / 1e9, 1)}
+    mode = "chain" if ms_chain <= ms_graph else "graph"
+    out = {"ms": min(ms_chain, ms_graph), "mode": mode, "ms_chain": ms_chain, "ms_graph": ms_graph,
+           "bytes": step.step_bytes(), "by_kind": by_kind, "chain": info}
     step.free_acts()
     return out
 
@@ -183,11 +187,12 @@ def bench_verify(c, step, Ms=(1, 2, 4, 5, 8, 16)):
     res = {}
     for M in Ms:
         step.alloc(M)
-        ms, _ = time_chain(c, step.ops, 3, 10)
+        ms_chain, _ = time_chain(c, step.ops, 3, 10)
         ms_graph = time_recording(c, step.ops, 3, 10)
+        ms = min(ms_chain, ms_graph)
         res[str(M)] = {"ms_per_pass": round(ms, 4), "tok_per_s": round(M / (ms * 1e-3), 1),
                        "GBps": round(step.step_bytes() / (ms * 1e-3) / 1e9, 1),
-                       "ms_one_launch_per_op": round(ms_graph, 4)}
+                       "ms_chain": round(ms_chain, 4), "ms_graph": round(ms_graph, 4)}
         step.free_acts()
     return res
 
@@ -247,6 +252,22 @@ def bench_gemm(c, M, shapes, reps=5):
             "frac_fp16_peak": round(tot_fl / (tot_ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4), "per_gemm": res}
 
 
+CAL_COPY_BYTES = 256 << 20
+
+
+def calibrate(c, reps=3):
+    """a plain copy of known size, profiled beside the step to scale FETCH_SIZE / WRITE_SIZE: copy16_kernel reads and
+    writes CAL_COPY_BYTES with 16-byte lane accesses, the same request shape as the GEMV's record loads"""
+    a, b = c.Buffer(CAL_COPY_BYTES), c.Buffer(CAL_COPY_BYTES)
+    a.fill_u32(0x3F800000)
+    for _ in range(reps):
+        c.copy(a, 0, b, 0, CAL_COPY_BYTES)
+    c.done()
+    a.free()
+    b.free()
+    log("calibration kernel: copy16_kernel reads and writes %d B" % CAL_COPY_BYTES)
+
+
 def cpu_baseline(min_seconds=10.0):
     """the oracle's fp32 port of lgemv (engine/llm/lops.js:60-88) over one layer + 1/16 of the head"""
     from oracle import oracle as O
@@ -284,6 +305,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="decode step only")
+    ap.add_argument("--no-breakdown", action="store_true",
+                    help="skip the per-projection timings (short runs under PMC counters)")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also run a copy of known size (copy16_kernel, CAL_COPY_BYTES) to calibrate PMC byte "
+                         "counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; --gpus %d is not supported (the hot path runs on one MI355X, "
@@ -299,7 +325,7 @@ def main():
     step = Step(c)
     c.done()
     log("weights filled: %.2f GB in %.1f s" % (step.weight_bytes / 1e9, time.time() - t0))
-    dec = bench_decode(c, step, args.steps, args.warmup)
+    dec = bench_decode(c, step, args.steps, args.warmup, not args.no_breakdown)
     ms = dec["ms"]
     tok_s = 1e3 / ms
     step_gbps = dec["bytes"] / (ms * 1e-3) / 1e9
@@ -307,8 +333,9 @@ def main():
 
     extra = {"decode_step": {"ms": round(ms, 4), "algorithmic_bytes": int(dec["bytes"]),
                              "GBps": round(step_gbps, 1), "frac_hbm_peak": round(step_gbps / HBM_PEAK_GBPS, 4),
-                             "ms_one_launch_per_op": round(dec["ms_one_launch_per_op"], 4),
-                             "chain": dec["chain"], "by_projection": dec["by_kind"]}}
+                             "mode": dec["mode"], "ms_chain": round(dec["ms_chain"], 4),
+                             "ms_graph": round(dec["ms_graph"], 4), "chain": dec["chain"],
+                             "by_projection": dec["by_kind"]}}
     if not args.no_extra:
         extra["config_a_gemv"] = bench_config_a(c)
         log("config A", extra["config_a_gemv"])
@@ -318,6 +345,8 @@ def main():
         for (b, n, k) in t.values():
             b.free()
     step.head.free()
+    if args.calibrate:
+        calibrate(c)
     if not args.no_gemm:
         extra["gemm_flux2_klein_M4608"] = bench_gemm(
             c, 4608, [("qkv", 9216, 3072), ("out", 3072, 3072), ("mlp_up", 9216, 3072), ("mlp_down", 3072, 9216)])
@@ -327,17 +356,31 @@ def main():
                 c, 32760, [("qkv", 9216, 3072), ("glu_up", 16384, 3072), ("down", 3072, 8192)], reps=2)
             log("gemm SANA", extra["gemm_sana_video_M32760"])
 
-    # the dominant kernel: the chain kernel running the whole step (one launch per token); its algorithmic bytes are
-    # the step's weights + activations in and out (step_bytes), its duration the event-timed run
-    roofline = {"bound": "hbm", "achieved": round(step_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(step_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                "kernel": "q4_gemv_chain_kernel<1,%d> (the whole M=1 decode step: 121 GEMV ops, one launch)"
-                          % dec["chain"]["waves_per_workgroup"],
-                "bytes_per_launch": int(dec["bytes"]), "us_per_launch": round(ms * 1e3, 2)}
+    # the dominant kernel, measured live with HIP events on the library's stream. Chain mode: the chain kernel is the
+    # whole step (one launch per token), its algorithmic bytes the step's (weights + activations in and out). Graph
+    # mode: the gate_up GEMV (mode-2 q4_gemv_kernel, 57% of a layer's bytes), 30 distinct weights back to back.
+    if dec["mode"] == "chain":
+        roofline = {"bound": "hbm", "achieved": round(step_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(step_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                    "kernel": "q4_gemv_chain_kernel<1,%d> (the whole M=1 decode step: 121 GEMV ops, one launch)"
+                              % dec["chain"]["waves_per_workgroup"],
+                    "bytes_per_launch": int(dec["bytes"]), "us_per_launch": round(ms * 1e3, 2)}
+        traffic_key = "decode_chain_bytes_per_launch"
+    elif not dec["by_kind"]:
+        roofline, traffic_key = None, None
+    else:
+        gu = dec["by_kind"]["gu"]
+        gu_bytes = 2 * MLP * D * Q4_BYTES_PER_W + D * 4 + MLP * 4
+        achieved = gu_bytes / (gu["us_per_launch"] * 1e-6) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                    "kernel": "q4_gemv_kernel<1,2> (gate_up 16384x2048 rms+geglu)",
+                    "bytes_per_launch": int(gu_bytes), "us_per_launch": gu["us_per_launch"]}
+        traffic_key = "gate_up_gemv_bytes_per_launch"
     prof = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(prof):
+    if roofline and os.path.exists(prof):
         try:
-            roofline["traffic"] = json.load(open(prof)).get("decode_chain_bytes_per_launch")
+            roofline["traffic"] = json.load(open(prof)).get(traffic_key)
         except Exception:
             pass
 
@@ -354,7 +397,8 @@ def main():
         "config": {"workload": "gemma4-e2b-shaped decode step, M=1: 30 x {qkv 3072x2048 rms, o 2048x2048, "
                                "gate_up 2x8192x2048 rms+geglu, down 2048x8192 kPer 2048} + lm_head 262144x2048 "
                                "rms+softcap; q4g32a.t64 int4 weights (0.625 B/weight), fp32 accumulate",
-                   "weights_GB": round(step.weight_bytes / 1e9, 3), "launches_per_step": 1, "gemv_ops_per_step": 121,
+                   "weights_GB": round(step.weight_bytes / 1e9, 3), "launches_per_step": 1 if dec["mode"] == "chain" else 121, "gemv_ops_per_step": 121,
+                   "decode_path": dec["mode"],
                    "gemv_GBps": round(step_gbps, 1),
                    "gemm_TFLOPS_M4608": extra.get("gemm_flux2_klein_M4608", {}).get("TFLOPS")},
         "roofline": roofline, "cpu_baseline": cpu, "extra": extra,

@@ -11,6 +11,7 @@
  *   p0_buffer / p0_free                  <- Gpu.buffer / Gpu.free                 engine/core/gpu.js:81-95
  *   p0_upload / p0_read                  <- Gpu.upload / Gpu.read / readInto      engine/core/gpu.js:98-140
  *   p0_done                              <- Gpu.done                              engine/core/gpu.js:141-147
+ *   p0_copy                              <- runner.copy                           engine/core/gpu.js:237-242
  *   p0_q4_gemv                           <- gemv(g, a)                            engine/llm/lops.js:108-141
  *   p0_q4_gemvM                          <- gemvM(g, a)                           engine/llm/lops_spec.js:159-191
  *   p0_q4_gemm                           <- gemm(gpu, a)                          engine/ops/gemm.js:255-322
@@ -82,6 +83,9 @@ int p0_upload(void* dst, size_t dst_off, const void* src, size_t bytes);   /* ho
 int p0_read(void* host_dst, const void* src, size_t src_off, size_t bytes); /* device -> host; waits for the stream */
 int p0_fill(void* dst, size_t dst_off, uint32_t value, size_t words);       /* 32-bit pattern fill (NaN-fill checks) */
 int p0_done(void);                             /* wait for every op enqueued on the stream */
+/* device-to-device copy, ordered on the stream (runner.copy, engine/core/gpu.js:237-242): offsets and size multiples
+ * of 4 (copyBufferToBuffer's rule); overlapping ranges are rejected */
+int p0_copy(const void* src, size_t src_off, void* dst, size_t dst_off, size_t bytes);
 
 /* Event timing on the current stream (for benchmarks): p0_timer_start records a start event, p0_timer_stop records a
  * stop event, waits for it and returns the elapsed milliseconds. */

@@ -23,7 +23,7 @@ ACT = {"silu": 0, "gelu": 1}
 # every symbol the header declares (tests check the library exports each one)
 HEADER_SYMBOLS = [
     "p0_last_error", "p0_version", "p0_open", "p0_close", "p0_device_info", "p0_set_stream", "p0_get_stream",
-    "p0_buffer", "p0_free", "p0_upload", "p0_read", "p0_fill", "p0_done", "p0_timer_start", "p0_timer_stop",
+    "p0_buffer", "p0_free", "p0_upload", "p0_read", "p0_fill", "p0_copy", "p0_done", "p0_timer_start", "p0_timer_stop",
     "p0_q4_gemv", "p0_q4_gemvM", "p0_q4_gemm", "p0_q4_dequant", "p0_fill_q4_sym", "p0_fill_randn", "p0_gemv_tune",
     "p0_record_begin", "p0_record_end", "p0_replay", "p0_record_free",
     "p0_chain_begin", "p0_chain_end", "p0_chain_run", "p0_chain_status", "p0_chain_info", "p0_chain_free",
@@ -89,6 +89,7 @@ def lib():
             "p0_buffer": [C.c_size_t, C.POINTER(vp)], "p0_free": [vp],
             "p0_upload": [vp, C.c_size_t, vp, C.c_size_t], "p0_read": [vp, vp, C.c_size_t, C.c_size_t],
             "p0_fill": [vp, C.c_size_t, C.c_uint32, C.c_size_t], "p0_done": [], "p0_timer_start": [],
+            "p0_copy": [vp, C.c_size_t, vp, C.c_size_t, C.c_size_t],
             "p0_timer_stop": [C.POINTER(f32)],
             "p0_q4_gemv": [C.POINTER(GemvArgs), C.POINTER(i32)], "p0_q4_gemvM": [C.POINTER(GemvMArgs), C.POINTER(i32)],
             "p0_q4_gemm": [C.POINTER(GemmArgs), C.POINTER(C.c_double)],
@@ -175,6 +176,11 @@ def device_info():
 
 def done():
     check(lib().p0_done())
+
+
+def copy(src, src_off, dst, dst_off, nbytes):
+    """device-to-device copy on the library's stream (runner.copy)"""
+    check(lib().p0_copy(_ptr(src), src_off, _ptr(dst), dst_off, nbytes))
 
 
 def timer_start():

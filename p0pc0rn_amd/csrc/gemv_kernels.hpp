@@ -96,11 +96,21 @@ struct Rec {
   uint32_t sm;
 };
 
+// One record's lane slice: 16 bytes of the lane's row codes and its 4-byte scale/min. Nontemporal loads (STREAM) for
+// ops that stream hundreds of MB (the two-tiles-per-wave mode): they keep the cache for the activations; plain loads
+// otherwise, whose latency is lower (measured on MI355X: dependent HBM loads 280 ns plain, 330 ns nontemporal), which is
+// what a small, latency-bound op waits on.
+template <bool STREAM>
 __device__ __forceinline__ Rec load_rec(const GemvP& p, int64_t tile, int g, int lane) {
-  const uint8_t* rec = p.w + (int64_t)__builtin_amdgcn_readfirstlane((int)((tile * p.wG + g) >> 0)) * 1280;
+  const uint8_t* rec = p.w + (int64_t)__builtin_amdgcn_readfirstlane((int)(tile * p.wG + g)) * 1280;
   Rec r;
-  r.q = __builtin_nontemporal_load(P0_GLOBAL(const u32x4, rec + lane * 16));
-  r.sm = __builtin_nontemporal_load(P0_GLOBAL(const uint32_t, rec + 1024 + lane * 4));
+  if (STREAM) {
+    r.q = __builtin_nontemporal_load(P0_GLOBAL(const u32x4, rec + lane * 16));
+    r.sm = __builtin_nontemporal_load(P0_GLOBAL(const uint32_t, rec + 1024 + lane * 4));
+  } else {
+    r.q = *P0_GLOBAL(const u32x4, rec + lane * 16);
+    r.sm = *P0_GLOBAL(const uint32_t, rec + 1024 + lane * 4);
+  }
   return r;
 }
 
@@ -223,14 +233,14 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
 #pragma unroll
     for (int i = 0; i < D; ++i)
 #pragma unroll
-      for (int t = 0; t < T; ++t) r0[i][t] = load_rec(p, tl(t), min(wg0 + i, glast), lane);
+      for (int t = 0; t < T; ++t) r0[i][t] = load_rec<MODE == 1>(p, tl(t), min(wg0 + i, glast), lane);
   }
   if (!ready()) return false;
   if (streams && late) {
 #pragma unroll
     for (int i = 0; i < D; ++i)
 #pragma unroll
-      for (int t = 0; t < T; ++t) r0[i][t] = load_rec(p, tl(t), min(wg0 + i, glast), lane);
+      for (int t = 0; t < T; ++t) r0[i][t] = load_rec<MODE == 1>(p, tl(t), min(wg0 + i, glast), lane);
   }
 
   // ---- prologue: x'[m][k] for the workgroup's K-slice -> LDS (odd k scaled 1/16), then per-group sums of x'
@@ -287,7 +297,7 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
 #pragma unroll
       for (int i = 0; i < D; ++i)
 #pragma unroll
-        for (int t = 0; t < T; ++t) r[i][t] = load_rec(p, tl(t), min(c0 + i, glast), lane);
+        for (int t = 0; t < T; ++t) r[i][t] = load_rec<MODE == 1>(p, tl(t), min(c0 + i, glast), lane);
 #pragma unroll
       for (int i = 0; i < D; ++i)
         if (c0 + i < wg1) consume(r[i], c0 + i);

@@ -166,6 +166,14 @@ napi_value Fill(napi_env env, napi_callback_info info) {   // fill(dst, off, u32
   return undef(env);
 }
 
+napi_value Copy(napi_env env, napi_callback_info info) {   // copy(src, srcOff, dst, dstOff, size)
+  auto a = args(env, info, 5);
+  if (fail(env, p0_copy((const void*)(uintptr_t)num(env, a[0]), (size_t)num(env, a[1]), (void*)(uintptr_t)num(env, a[2]),
+                        (size_t)num(env, a[3]), (size_t)num(env, a[4]))))
+    return nullptr;
+  return undef(env);
+}
+
 napi_value Done(napi_env env, napi_callback_info) {
   if (fail(env, p0_done())) return nullptr;
   return undef(env);
@@ -273,7 +281,7 @@ napi_value Version(napi_env env, napi_callback_info) { return make_num(env, p0_v
 napi_value Init(napi_env env, napi_value exports) {
   struct { const char* name; napi_callback fn; } fns[] = {
       {"open", Open}, {"close", Close}, {"info", Info}, {"buffer", Buffer}, {"free", Free}, {"upload", Upload},
-      {"read", Read}, {"fill", Fill}, {"done", Done}, {"timerStart", TimerStart}, {"timerStop", TimerStop},
+      {"read", Read}, {"fill", Fill}, {"copy", Copy}, {"done", Done}, {"timerStart", TimerStart}, {"timerStop", TimerStop},
       {"gemv", Gemv}, {"gemvM", GemvM}, {"gemm", Gemm}, {"dequant", Dequant}, {"fillQ4Sym", FillQ4Sym},
       {"fillRandn", FillRandn}, {"version", Version},
   };

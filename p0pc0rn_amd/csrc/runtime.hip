@@ -28,6 +28,17 @@ __global__ void fill_u32_kernel(uint32_t* __restrict__ p, uint32_t v, size_t n) 
   for (; i < n; i += stride) p[i] = v;
 }
 
+// buffer copy (engine/core/gpu.js:237-242 runner.copy). 16 bytes per lane when source, destination and size allow it:
+// the same request shape as the GEMV's record loads, which makes it the calibration kernel for HBM byte counters.
+__global__ void copy16_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x, stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) dst[i] = src[i];
+}
+__global__ void copy4_kernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x, stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) dst[i] = src[i];
+}
+
 }  // namespace p0
 
 using namespace p0;
@@ -158,6 +169,29 @@ int p0_fill(void* dst, size_t dst_off, uint32_t value, size_t words) {
   hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx().cur,
                      (uint32_t*)((char*)dst + dst_off), value, words);
   P0_LAUNCHED("p0_fill");
+  return P0_OK;
+}
+
+int p0_copy(const void* src, size_t src_off, void* dst, size_t dst_off, size_t bytes) {
+  if (int r = require_open("p0_copy")) return r;
+  const char* a = (const char*)src + src_off;
+  char* b = (char*)dst + dst_off;
+  if (((uintptr_t)a | (uintptr_t)b | bytes) & 3) {   // copyBufferToBuffer's rule: offsets and size multiples of 4
+    set_error("p0_copy: offsets and size must be multiples of 4");
+    return P0_EINVAL;
+  }
+  if (!bytes) return P0_OK;
+  if ((a < b + bytes) && (b < a + bytes)) {
+    set_error("p0_copy: source and destination overlap");
+    return P0_EINVAL;
+  }
+  const bool wide = !(((uintptr_t)a | (uintptr_t)b | bytes) & 15);
+  const size_t n = wide ? bytes / 16 : bytes / 4;
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  if (wide) hipLaunchKernelGGL(copy16_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx().cur, (const uint4*)a, (uint4*)b, n);
+  else hipLaunchKernelGGL(copy4_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx().cur, (const uint32_t*)a, (uint32_t*)b, n);
+  P0_LAUNCHED("p0_copy");
   return P0_OK;
 }
 

@@ -32,7 +32,12 @@ export class Gpu {
     this.lostInfo = null;
     // measured-rate placeholders the reference uses for dispatch sizing; MI355X-scale defaults (HBM, fp16 MFMA)
     this.rate = { mm: 1.0e15, mm16: 1.0e15, mm32: 1.0e15, attn: 0.2e15, mem: 6e12 };
-    this.runner = { flush() {}, sync() {}, forget() {}, dispatches: 0, submits: 0 };
+    // the reference's batching runner: ops are enqueued on the library's stream as they are called, so flush / sync
+    // have nothing to do; copy is a stream-ordered device copy (engine/core/gpu.js:237-242)
+    this.runner = {
+      flush() {}, sync() {}, forget() {}, dispatches: 0, submits: 0,
+      copy(src, srcOff, dst, dstOff, size) { native().copy(src.ptr, srcOff, dst.ptr, dstOff, size); },
+    };
   }
 
   init() {

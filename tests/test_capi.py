@@ -134,3 +134,15 @@ def test_ops_without_a_device_fail_loudly():
     assert rc == capi.P0_ENODEV and "no device" in err
     p = capi.vp()
     assert capi.lib().p0_buffer(64, capi.C.byref(p)) == capi.P0_ENODEV
+    assert capi.lib().p0_copy(None, 0, None, 0, 16) == capi.P0_ENODEV
+    assert capi.lib().p0_chain_begin() == capi.P0_ENODEV
+
+
+def test_chain_tune_knobs_round_trip():
+    """chain knobs answer queries without a device and clamp the waves knob to 8 or 16"""
+    old = capi.chain_tune(0, 0)
+    assert old in (8, 16)
+    assert capi.chain_tune(0, 9) == old and capi.chain_tune(0, -1) == 8
+    assert capi.chain_tune(0, 16) == 8 and capi.chain_tune(0, -1) == 16
+    capi.chain_tune(0, old)
+    assert capi.chain_tune(3, -1) == 0 and capi.chain_tune(9, 1) == -1

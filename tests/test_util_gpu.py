@@ -54,3 +54,26 @@ def test_fill_randn_matches_oracle(dev):
     assert np.count_nonzero(g16 != w16) <= 10
     assert np.array_equal(g32.view(np.uint32) == w32.view(np.uint32), g16 == w16)
     b32.free(); b16.free()
+
+
+@pytest.mark.parametrize("src_off,dst_off,n", [(0, 0, 1 << 20), (4, 12, 4096 + 8), (16, 32, 12)])
+def test_copy(dev, src_off, dst_off, n):
+    """runner.copy (engine/core/gpu.js:237-242): the 16-byte path when everything is 16-aligned, else 4-byte words"""
+    src = np.random.default_rng(5).integers(0, 2**32, (src_off + n) // 4, dtype=np.uint32)
+    a = capi.to_device(src)
+    b = capi.Buffer(dst_off + n + 64).fill_u32(0xDEADBEEF)
+    capi.copy(a, src_off, b, dst_off, n)
+    got = b.read(np.uint32)
+    assert np.array_equal(got[dst_off // 4: (dst_off + n) // 4], src[src_off // 4:])
+    assert np.all(got[: dst_off // 4] == 0xDEADBEEF) and np.all(got[(dst_off + n) // 4:] == 0xDEADBEEF)
+    a.free()
+    b.free()
+
+
+def test_copy_errors(dev):
+    a = capi.Buffer(256)
+    with pytest.raises(capi.P0Error, match="multiples of 4"):
+        capi.copy(a, 2, a, 128, 16)
+    with pytest.raises(capi.P0Error, match="overlap"):
+        capi.copy(a, 0, a, 16, 64)
+    a.free()
