@@ -276,6 +276,56 @@ napi_value FillRandn(napi_env env, napi_callback_info info) {   // fillRandn(dst
   return undef(env);
 }
 
+// ---- recorded op sequences and chains: opaque handles cross as numbers (host addresses, exact below 2^53)
+void* handle(napi_env env, napi_value v) { return reinterpret_cast<void*>(static_cast<uintptr_t>(num(env, v))); }
+
+napi_value RecordBegin(napi_env env, napi_callback_info) {
+  if (fail(env, p0_record_begin())) return nullptr;
+  return undef(env);
+}
+napi_value RecordEnd(napi_env env, napi_callback_info) {
+  void* h = nullptr;
+  if (fail(env, p0_record_end(&h))) return nullptr;
+  return make_num(env, (double)reinterpret_cast<uintptr_t>(h));
+}
+napi_value Replay(napi_env env, napi_callback_info info) {
+  auto a = args(env, info, 1);
+  if (fail(env, p0_replay(handle(env, a[0])))) return nullptr;
+  return undef(env);
+}
+napi_value RecordFree(napi_env env, napi_callback_info info) {
+  auto a = args(env, info, 1);
+  if (fail(env, p0_record_free(handle(env, a[0])))) return nullptr;
+  return undef(env);
+}
+napi_value ChainBegin(napi_env env, napi_callback_info) {
+  if (fail(env, p0_chain_begin())) return nullptr;
+  return undef(env);
+}
+napi_value ChainEnd(napi_env env, napi_callback_info) {
+  void* h = nullptr;
+  if (fail(env, p0_chain_end(&h))) return nullptr;
+  return make_num(env, (double)reinterpret_cast<uintptr_t>(h));
+}
+napi_value ChainRun(napi_env env, napi_callback_info info) {
+  auto a = args(env, info, 1);
+  if (fail(env, p0_chain_run(handle(env, a[0])))) return nullptr;
+  return undef(env);
+}
+napi_value ChainStatus(napi_env env, napi_callback_info info) {   // -> true if a wait of an earlier run gave up
+  auto a = args(env, info, 1);
+  int32_t t = 0;
+  if (fail(env, p0_chain_status(handle(env, a[0]), &t))) return nullptr;
+  napi_value v;
+  napi_get_boolean(env, t != 0, &v);
+  return v;
+}
+napi_value ChainFree(napi_env env, napi_callback_info info) {
+  auto a = args(env, info, 1);
+  if (fail(env, p0_chain_free(handle(env, a[0])))) return nullptr;
+  return undef(env);
+}
+
 napi_value Version(napi_env env, napi_callback_info) { return make_num(env, p0_version()); }
 
 napi_value Init(napi_env env, napi_value exports) {
@@ -283,7 +333,9 @@ napi_value Init(napi_env env, napi_value exports) {
       {"open", Open}, {"close", Close}, {"info", Info}, {"buffer", Buffer}, {"free", Free}, {"upload", Upload},
       {"read", Read}, {"fill", Fill}, {"copy", Copy}, {"done", Done}, {"timerStart", TimerStart}, {"timerStop", TimerStop},
       {"gemv", Gemv}, {"gemvM", GemvM}, {"gemm", Gemm}, {"dequant", Dequant}, {"fillQ4Sym", FillQ4Sym},
-      {"fillRandn", FillRandn}, {"version", Version},
+      {"fillRandn", FillRandn}, {"version", Version}, {"recordBegin", RecordBegin}, {"recordEnd", RecordEnd},
+      {"replay", Replay}, {"recordFree", RecordFree}, {"chainBegin", ChainBegin}, {"chainEnd", ChainEnd},
+      {"chainRun", ChainRun}, {"chainStatus", ChainStatus}, {"chainFree", ChainFree},
   };
   for (auto& f : fns) {
     napi_value v;

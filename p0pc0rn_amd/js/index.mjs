@@ -3,3 +3,4 @@ export { createGpu, Gpu, GpuError, view, f2h, h2f, toF16, fromF16, MB } from './
 export { gemv, KCH } from './llm/lops.mjs';
 export { gemvM } from './llm/lops_spec.mjs';
 export { gemm, DEFAULT_TILE } from './ops/gemm.mjs';
+export { DecodeRunner } from './llm/drunner.mjs';

@@ -1,0 +1,167 @@
+"""The Node.js host (p0pc0rn_amd/js), the reference-shaped boundary, driven through `node`.
+
+CPU: argument errors arrive as thrown Errors with the reference's own texts (engine/llm/lops.js:114-124,
+engine/llm/lops_spec.js:163-173, engine/ops/gemm.js:267-278), and opening a device where there is none throws
+GpuError. GPU: gemv / gemvM / gemm called with the reference's argument objects agree with the oracle (relative L2
+<= 1e-3, BASELINE, and this build's fp32 bar of 2e-5; 1e-5 for the fp32-out GEMM), and the DecodeRunner analogue
+(engine/llm/drunner.js) replays a recorded two-op token in both of its modes.
+"""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from p0pc0rn_amd import capi
+from tests.conftest import rel_l2
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INDEX = "file://" + os.path.join(ROOT, "p0pc0rn_amd", "js", "index.mjs")
+NODE = shutil.which("node")
+ADDON = os.path.join(ROOT, "p0pc0rn_amd", "js", "p0pc0rn.node")
+
+pytestmark = pytest.mark.skipif(not NODE or not os.path.exists(ADDON), reason="node or the N-API addon is missing")
+
+
+def run_node(tmp_path, body, timeout=120):
+    script = tmp_path / "t.mjs"
+    # await_gpu(): the synchronous part of createGpu (Gpu + init), so the test bodies stay linear
+    script.write_text("import * as P from '%s';\nimport fs from 'fs';\n"
+                      "const await_gpu = () => { const g = new P.Gpu({ device: 0 }); g.init(); return g; };\n%s\n"
+                      % (INDEX, body))
+    r = subprocess.run([NODE, str(script)], cwd=str(tmp_path), capture_output=True, text=True, timeout=timeout)
+    assert r.returncode == 0, r.stderr[-2000:]
+    return r.stdout
+
+
+def test_js_argument_errors_carry_the_reference_texts(tmp_path):
+    out = run_node(tmp_path, r"""
+const g = {}, B = { ptr: 0 };
+const w = (rows, cols) => ({ buf: B, off: 0, enc: 'q4g32a.t64', rows, cols });
+const res = [];
+const t = (f) => { try { f(); res.push('no error'); } catch (e) { res.push(e.message); } };
+t(() => P.gemv(g, { w: w(64, 8192), x: { buf: B }, N: 64, K: 8192, pro: 'raw', epi: 'store', y: { buf: B } }));
+t(() => P.gemv(g, { w: w(96, 256), x: { buf: B }, N: 96, K: 256, pro: 'raw', epi: 'store', y: { buf: B } }));
+t(() => P.gemv(g, { w: w(64, 4096), x: { buf: B }, N: 64, K: 4096, kPer: 2048, pro: 'rms', epi: 'geglu', y: { buf: B } }));
+t(() => P.gemv(g, { w: w(64, 256), x: { buf: B }, N: 64, K: 256, kPer: 48, pro: 'raw', epi: 'store', y: { buf: B } }));
+t(() => P.gemv(g, { w: Object.assign(w(64, 256), { off: 2 }), x: { buf: B }, N: 64, K: 256, y: { buf: B } }));
+t(() => P.gemvM(g, { w: w(64, 256), x: { buf: B }, M: 2, N: 64, K: 256, pro: 'sum', epi: 'store', y: { buf: B } }));
+t(() => P.gemm(g, { w: w(64, 100), x: { buf: B }, M: 4, N: 64, K: 100, y: { buf: B } }));
+t(() => P.gemm(g, { w: { buf: B, enc: 'q3', rows: 64, cols: 64 }, x: { buf: B }, M: 4, N: 64, K: 64, y: { buf: B } }));
+P.createGpu({ device: 0 }).then(() => res.push('no error'), (e) => res.push((e instanceof P.GpuError ? 'GpuError: ' : '') + e.message))
+  .then(() => console.log(JSON.stringify(res)));
+""")
+    res = json.loads(out.strip().splitlines()[-1])
+    assert res[0] == "gemv: K 8192 needs a kPer"
+    assert res[1] == "gemv: N % 64"
+    assert res[2] == "gemv: geglu needs one split"
+    assert res[3] == "gemv: kPer must be a multiple of 32"
+    assert res[4] == "gemv: weight offset"
+    assert res[5] == "gemvM: prologue sum"
+    assert res[6] == "gemm: K must be a multiple of 32"
+    assert res[7].startswith("gemm: unsupported weight encoding")
+    assert res[8].startswith("GpuError: ") and ("no HIP device" in res[8] or "gfx950" in res[8])
+
+
+def _save(tmp_path, **arrays):
+    for k, v in arrays.items():
+        np.ascontiguousarray(v).tofile(str(tmp_path / (k + ".bin")))
+
+
+@pytest.mark.gpu
+def test_js_ops_match_the_oracle(tmp_path):
+    N, K, M = 256, 2048, 5
+    w, _ = O.pack_q4(O.randn(N * K, 3, 0.05), N, K)
+    x = O.randn(M * K, 4)
+    nw = np.linspace(0.8, 1.2, K).astype(np.float32)
+    st = np.array([0, 0.7, 0, 0.9, 0, 1.1, 0, 0.8, 0, 1.2, 0, 0], np.float32)
+    Mg, Ng, Kg = 64, 128, 256
+    wg, _ = O.pack_q4(O.randn(Ng * Kg, 5, 0.05), Ng, Kg)
+    xg = O.randn(Mg * Kg, 6).astype(np.float16)
+    _save(tmp_path, w=w, x=x, nw=nw, st=st, wg=wg, xg=xg)
+    run_node(tmp_path, r"""
+const g = await_gpu();
+const up = (name) => { const b = fs.readFileSync(name + '.bin'); return g.upload(new Uint8Array(b.buffer, b.byteOffset, b.length)); };
+const [w, x, nw, st, wg, xg] = ['w', 'x', 'nw', 'st', 'wg', 'xg'].map(up);
+const N = 256, K = 2048, M = 5, y1 = g.buffer(N * 4), yM = g.buffer(M * N * 4), yg = g.buffer(64 * 128 * 4);
+const W = { buf: w, off: 0, enc: 'q4g32a.t64', rows: N, cols: K };
+const ns = P.gemv(g, { w: W, x: { buf: x, rowB: 0 }, N, K, pro: 'rms', epi: 'store', y: { buf: y1 },
+                       stat: { buf: st, off: 1 }, norm: { buf: nw, off: 0 } });
+const nsM = P.gemvM(g, { w: W, x: { buf: x, ldx: K }, M, N, K, pro: 'rms', epi: 'store', y: { buf: yM, ldm: N },
+                         stat: { buf: st, off: 1, ld: 2 }, norm: { buf: nw, off: 0 } });
+const fl = P.gemm(g, { w: { buf: wg, off: 0, enc: 'q4g32a.t64', rows: 128, cols: 256 }, x: { buf: xg }, M: 64, N: 128,
+                       K: 256, epi: 'f32', y: { buf: yg } });
+(async () => {
+  await g.done();
+  fs.writeFileSync('y1.bin', Buffer.from(await g.read(y1)));
+  fs.writeFileSync('yM.bin', Buffer.from(await g.read(yM)));
+  fs.writeFileSync('yg.bin', Buffer.from(await g.read(yg)));
+  console.log(JSON.stringify({ ns, nsM, fl }));
+  g.freeAll(); g.device.destroy();
+})();
+""")
+    y1 = np.fromfile(str(tmp_path / "y1.bin"), np.float32)
+    yM = np.fromfile(str(tmp_path / "yM.bin"), np.float32)
+    yg = np.fromfile(str(tmp_path / "yg.bin"), np.float32)
+    want1 = np.zeros(N, np.float32)
+    O.q4_gemv(capi.gemv_args(w=w.ctypes.data, w_rows=N, w_cols=K, x=x.ctypes.data, N=N, K=K, pro=capi.PRO["rms"],
+                             y=want1.ctypes.data, stat=st.ctypes.data, stat_off=1, norm=nw.ctypes.data))
+    wantM = np.zeros(M * N, np.float32)
+    O.q4_gemvM(capi.gemvm_args(w=w.ctypes.data, w_rows=N, w_cols=K, x=x.ctypes.data, x_ldx=K, M=M, N=N, K=K,
+                               pro=capi.PRO["rms"], y=wantM.ctypes.data, y_ldm=N, stat=st.ctypes.data, stat_off=1,
+                               stat_ld=2, norm=nw.ctypes.data))
+    wantg = np.zeros(Mg * Ng, np.float32)
+    O.q4_gemm(capi.gemm_args(w=wg.ctypes.data, w_rows=Ng, w_cols=Kg, x=xg.ctypes.data, M=Mg, N=Ng, K=Kg,
+                             epi=capi.GEPI["f32"], y=wantg.ctypes.data))
+    for got, want, tol, what in ((y1, want1, 2e-5, "gemv"), (yM, wantM, 2e-5, "gemvM"), (yg, wantg, 1e-5, "gemm")):
+        r = rel_l2(got, want)
+        print(what, r)
+        assert np.all(np.isfinite(got)) and r <= 1e-3 and r <= tol, what
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["graph", "chain"])
+def test_js_decode_runner(tmp_path, mode):
+    """a token of two dependent GEMVs (y1 = W1 x; y2 = W2 y1), recorded once and submitted three times"""
+    N1, K1, N2 = 512, 1024, 256
+    w1, _ = O.pack_q4(O.randn(N1 * K1, 7, 0.05), N1, K1)
+    w2, _ = O.pack_q4(O.randn(N2 * N1, 8, 0.05), N2, N1)
+    x = O.randn(K1, 9)
+    _save(tmp_path, w1=w1, w2=w2, x=x)
+    out = run_node(tmp_path, r"""
+const g = await_gpu();
+const up = (name) => { const b = fs.readFileSync(name + '.bin'); return g.upload(new Uint8Array(b.buffer, b.byteOffset, b.length)); };
+const [w1, w2, x] = ['w1', 'w2', 'x'].map(up);
+const y1 = g.buffer(512 * 4), y2 = g.buffer(256 * 4);
+const r = new P.DecodeRunner(g, { mode: '%s' });
+r.begin();
+P.gemv(g, { w: { buf: w1, off: 0, enc: 'q4g32a.t64', rows: 512, cols: 1024 }, x: { buf: x }, N: 512, K: 1024, y: { buf: y1 } });
+P.gemv(g, { w: { buf: w2, off: 0, enc: 'q4g32a.t64', rows: 256, cols: 512 }, x: { buf: y1 }, N: 256, K: 512, y: { buf: y2 } });
+const tk = r.end();
+(async () => {
+  const outs = [];
+  for (let i = 0; i < 3; i++) {
+    g.fill(y1, 0, 0x7fc00000, 512); g.fill(y2, 0, 0x7fc00000, 256);
+    await r.submit(tk);
+    outs.push(Buffer.from(await g.read(y2)).toString('base64'));
+  }
+  fs.writeFileSync('y1.bin', Buffer.from(await g.read(y1)));
+  fs.writeFileSync('y2.bin', Buffer.from(await g.read(y2)));
+  console.log(JSON.stringify({ same: outs.every((o) => o === outs[0]), submits: r.submits }));
+  r.forget(); g.freeAll(); g.device.destroy();
+})();
+""" % mode)
+    res = json.loads(out.strip().splitlines()[-1])
+    assert res["same"] and res["submits"] == 3
+    y1 = np.fromfile(str(tmp_path / "y1.bin"), np.float32)
+    y2 = np.fromfile(str(tmp_path / "y2.bin"), np.float32)
+    want1 = np.zeros(N1, np.float32)
+    O.q4_gemv(capi.gemv_args(w=w1.ctypes.data, w_rows=N1, w_cols=K1, x=x.ctypes.data, N=N1, K=K1, y=want1.ctypes.data))
+    want2 = np.zeros(N2, np.float32)
+    O.q4_gemv(capi.gemv_args(w=w2.ctypes.data, w_rows=N2, w_cols=N1, x=y1.ctypes.data, N=N2, K=N1, y=want2.ctypes.data))
+    for got, want, what in ((y1, want1, "op 0"), (y2, want2, "op 1")):
+        r = rel_l2(got, want)
+        assert np.all(np.isfinite(got)) and r <= 2e-5, (mode, what, r)
