@@ -24,10 +24,15 @@ struct Ctx {
   size_t part_floats = 0;
   unsigned* counters = nullptr;
   size_t n_counters = 0;
+  // fp16 staging of GEMM activations that the MFMA kernel cannot stream as they are (bf16, the f32 prologues,
+  // misaligned fp16): grown on demand, never inside a stream capture (ensure_xstage)
+  void* xstage = nullptr;
+  size_t xstage_bytes = 0;
   int cu_count = 0;
   hipDeviceProp_t prop{};
 };
 Ctx& ctx();
+int ensure_xstage(size_t bytes, const char* op);   // P0_OK, or an error (no room while the stream is being captured)
 
 // Thread-local message of the last failure (p0_last_error).
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));

@@ -4,69 +4,91 @@
 // f16 | lnmod | rms (engine/ops/gemm.js:55-63; plus bf16 activations converted to fp16) and epilogues
 // f16 | f32 | resadd | swiglu | bias (engine/ops/gemm.js:187-211).
 //
-// Mapping: a workgroup of 4 waves owns a BM x BN output tile; per 32-k step (one q4 group, the reference's BK) it stages
-// the prologue-applied fp16 X tile and the dequantised fp16 W tile in LDS, then each wave runs 32x32x16 fp16 MFMAs
-// over its (BM/2) x (BN/2) sub-tile with fp32 accumulators. The W tile value is fl16(fl32(q * s + m)), the
-// reference's own fp16 tile rounding (engine/ops/gemm.js:147-148), so the only difference from the reference is the
-// fp32 summation order inside the MFMA.
+// Two kernels:
+//  * x_stage_kernel<XM> writes X' (the prologue-applied activations, fp16, dense rows of K) into the context's staging
+//    workspace, once per call, when X is not already fp16 rows the MFMA kernel can stream (bf16, lnmod, rms, or fp16
+//    rows that are not 16-byte aligned). The reference applies the prologue inside its tile loads; doing it once here
+//    instead of once per output-column block costs one streaming pass over X.
+//  * q4_gemm_kernel: a workgroup of 4 waves owns a 256 x 256 output tile; per 64-k step (two q4 groups) it
+//      - streams the fp16 X tile straight from global memory into LDS (global_load_lds_dwordx4: no registers, no ALU),
+//      - dequantises the W tile from its records exactly (fl16 of the fp32 value, the reference's own tile rounding,
+//        engine/ops/gemm.js:147-148) into LDS,
+//      - runs 4 x 4 blocks of v_mfma_f32_32x32x16_f16 per wave over its 128 x 128 sub-tile (fp32 accumulators in AGPRs),
+//    with two LDS stages: the next step's X loads and W records are in flight during this step's MFMAs.
+//    LDS rows are 128 B (64 k); the 16-byte chunk c of row r sits at position c ^ (r & 7), which makes the direct-load
+//    writes, the dequant writes and the MFMA fragment reads all bank-conflict free.
 #include "common.hpp"
 
 namespace p0 {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));   // a 16-byte load at 4-byte alignment
+typedef uint32_t u32x4n __attribute__((ext_vector_type(4)));               // 16-byte aligned (LDS, registers)
 typedef float float16v __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
 
 struct GemmP {
   const uint8_t* w; int64_t wG; int64_t Nw;
-  const uint8_t* x; int64_t ldx, kx0; int xmode;
+  const _Float16* x; int64_t ldx;   // fp16 X' rows (the caller's, or the staging workspace), k offset folded in
   int M, N, K;
   int64_t wr0, wr1, wk0;
   int epi;
   uint8_t* y; int64_t ldy, ny0;
   const float* ev; int64_t evOff;
-  const float* st; int64_t stOff;
-  const float* pv; int64_t pvOff; uint32_t pvShift;   // shift base = (pv_off + pv_stride) mod 2^32
   const float* bv; int64_t bvOff, bvUp;
   int act, store, res;
 };
 
-constexpr int BM = 128, BN = 128, BK = 32, LDK = BK + 8;   // LDS row stride 40 halves (80 B)
+struct XStageP {   // the prologue of engine/ops/gemm.js:55-63 over the caller's X
+  const uint8_t* x; int64_t ldx, kx0; int xmode;
+  int M, K;
+  const float* st; int64_t stOff;
+  const float* pv; int64_t pvOff; uint32_t pvShift;   // shift base = (pv_off + pv_stride) mod 2^32
+  _Float16* out;     // [M][K]
+};
+
+constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int kStage = (BM + BN) * BK * 2;     // one stage: X and W tiles, 64 KB
+constexpr int kGemmLds = 2 * kStage;           // two stages: 128 KB of the 160 KB
 
 __device__ __forceinline__ _Float16 to_h(float v) { return (_Float16)v; }   // RNE
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, to_h(lo)) | ((uint32_t)__builtin_bit_cast(uint16_t, to_h(hi)) << 16);
+}
+// byte offset of the 16-byte chunk c (0..7) of tile row r
+__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
 
-__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
-
-// 8 prologue-applied fp16 values of X row `row`, k = k0 + 8 c .. + 7 (engine/ops/gemm.js:55-63)
-__device__ __forceinline__ half8 xload8(const GemmP& p, int row, int k) {
-  half8 h;
-  const int64_t idx = (int64_t)row * p.ldx + p.kx0 + k;
-  if (p.xmode == P0_XMODE_F16 || p.xmode == P0_XMODE_BF16) {
-    const uint16_t* src = (const uint16_t*)p.x + idx;
-    uint16_t v[8];
+// ------------------------------------------------------------------------------------------------ X staging
+__global__ __launch_bounds__(256) void x_stage_kernel(XStageP p) {
+  const int64_t chunks = (int64_t)p.M * (p.K / 8);
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < chunks; c += (int64_t)gridDim.x * 256) {
+    const int m = (int)(c / (p.K / 8)), k = (int)(c % (p.K / 8)) * 8;
+    const int64_t idx = (int64_t)m * p.ldx + p.kx0 + k;
+    float f[8];
+    if (p.xmode == P0_XMODE_F16 || p.xmode == P0_XMODE_BF16) {
+      const uint16_t* src = (const uint16_t*)p.x + idx;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = src[j];
+      for (int j = 0; j < 8; ++j)
+        f[j] = p.xmode == P0_XMODE_F16 ? (float)__builtin_bit_cast(_Float16, src[j]) : __uint_as_float((uint32_t)src[j] << 16);
+    } else {   // engine/ops/gemm.js:59-63
+      const float* src = (const float*)p.x + idx;
+      const float mean = p.st[(p.stOff + m) * 2], rstd = p.st[(p.stOff + m) * 2 + 1];
+      const int64_t kk = p.kx0 + k;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) h[j] = p.xmode == P0_XMODE_F16 ? __builtin_bit_cast(_Float16, v[j]) : to_h(bf16_to_f32(v[j]));
-  } else {
-    const float* src = (const float*)p.x + idx;
-    const float* s = p.st + (p.stOff + row) * 2;
-    const float mean = s[0], rstd = s[1];
-    const int64_t kk = p.kx0 + k;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float xv = src[j];
-      float t;
-      if (p.xmode == P0_XMODE_LNMOD) t = (xv - mean) * rstd * (1.0f + p.pv[p.pvOff + kk + j]) + p.pv[(int64_t)p.pvShift + kk + j];
-      else t = xv * rstd * p.pv[p.pvOff + kk + j];
-      h[j] = to_h(t);
+      for (int j = 0; j < 8; ++j)
+        f[j] = p.xmode == P0_XMODE_LNMOD
+                   ? (src[j] - mean) * rstd * (1.0f + p.pv[p.pvOff + kk + j]) + p.pv[(int64_t)p.pvShift + kk + j]
+                   : src[j] * rstd * p.pv[p.pvOff + kk + j];
     }
+    u32x4n o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = pack_h2(f[2 * i], f[2 * i + 1]);
+    *(u32x4n*)(p.out + (int64_t)m * p.K + k) = o;
   }
-  return h;
 }
 
-// weight row of ws column n (engine/ops/gemm.js:94-97)
+// ------------------------------------------------------------------------------------------------ the GEMM
+// weight row of output column n (engine/ops/gemm.js:94-97)
 __device__ __forceinline__ int64_t wrow(const GemmP& p, int n) {
   if (p.epi == P0_GEPI_SWIGLU) return ((n & 1) ? p.wr1 : p.wr0) + (n >> 1);
   const int64_t r = p.wr0 + n;
@@ -82,108 +104,192 @@ __device__ __forceinline__ float act_f(const GemmP& p, float g) {
   return g / (1.0f + __expf(-g));
 }
 
+// q s + m is exact in fp32 for every q in [0, 15] when the fp16 exponent fields a = max(e_s, 1), b = max(e_m, 1)
+// satisfy -12 <= a - b <= 8 (the sum then spans at most 24 bits), or when s or m is zero
+__device__ __forceinline__ bool pk_exact(uint32_t sm) {
+  const int es = (sm >> 10) & 31, em = (sm >> 26) & 31;
+  const int a = es > 1 ? es : 1, b = em > 1 ? em : 1;
+  const bool zero = (sm & 0x7FFFu) == 0 || (sm & 0x7FFF0000u) == 0;
+  return zero || (a - b <= 8 && a - b >= -12);
+}
+
+// One q4 code word (k = 8 w .. 8 w + 7 of one row) -> 8 fp16 weights in k order, each fl16(fl32(q s + m)).
+// Fast path: the byte j of the word holds k 2j (low nibble) and 2j + 1 (high nibble); a byte permute spreads the
+// nibbles of byte j into the two halves of pair j, OR-ing 0x6400 makes them fp16 1024 + q, v_pk_add_f16 takes 1024 off
+// exactly and v_pk_fma_f16 rounds q s + m once to fp16. That single rounding equals fl16(fl32(q s + m)) whenever q s + m
+// is exact in fp32 (pk_exact); otherwise the fp32 path rounds twice, exactly as the reference does.
+__device__ __forceinline__ u32x4n deq_word(uint32_t v, uint32_t sm, bool fast) {
+  u32x4n o;
+  if (fast) {
+    const h2 s2 = {__builtin_bit_cast(h2, sm).x, __builtin_bit_cast(h2, sm).x};
+    const h2 m2 = {__builtin_bit_cast(h2, sm).y, __builtin_bit_cast(h2, sm).y};
+    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;   // byte j: k 2j | k 2j + 1
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // bytes [lo.j, 0, hi.j, 0] (selector 0x0C gives zero); then the fp16 exponent of 1024
+      const uint32_t sel = (uint32_t)j | (0x0Cu << 8) | ((uint32_t)(4 + j) << 16) | (0x0Cu << 24);
+      const uint32_t b = __builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u;
+      const h2 q = __builtin_bit_cast(h2, b) - k1024;
+      o[j] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, s2, m2));
+    }
+  } else {
+    const float s = (float)__builtin_bit_cast(h2, sm).x, m = (float)__builtin_bit_cast(h2, sm).y;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float q0 = (float)((v >> (8 * j)) & 15u), q1 = (float)((v >> (8 * j + 4)) & 15u);
+      o[j] = pack_h2(__builtin_fmaf(q0, s, m), __builtin_fmaf(q1, s, m));
+    }
+  }
+  return o;
+}
+
 __global__ __launch_bounds__(256) void q4_gemm_kernel(GemmP p) {
-  __shared__ _Float16 xs[BM * LDK];
-  __shared__ _Float16 ws[BN * LDK];
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int wm = wv >> 1, wn = wv & 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
 
-  float16v acc[2][2];
+  // XCD-aware tile order: consecutive workgroups go to the 8 XCDs in turn, so tile t is given to workgroup
+  // (t % per) * 8 + t / per: each XCD walks a contiguous run of row-major tiles and keeps their X rows in its L2
+  const int nbx = (p.N + BN - 1) / BN, nby = (p.M + BM - 1) / BM, T = nbx * nby;
+  int t = blockIdx.x;
+  if (T % 8 == 0) t = (blockIdx.x % 8) * (T / 8) + blockIdx.x / 8;
+  const int m0 = (t / nbx) * BM, n0 = (t % nbx) * BN;
+
+  float16v acc[4][4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  // staging assignments: X: thread -> (row tid / 2, 16 k from (tid & 1) * 16); W: thread -> (row tid / 2, words 2 (tid & 1) .. +1)
-  const int sr = tid >> 1, sc = tid & 1;
-  const int xrow = min(m0 + sr, p.M - 1);   // rows past M repeat the last row (engine/ops/gemm.js:132-133); never stored
-  const int ncol = n0 + sr;
+  // X direct loads: instruction r of wave wv fills tile rows wv * 64 + 8 r .. + 7 (1 KB); lane l lands at byte 16 l,
+  // i.e. row + l / 8, position l % 8, which holds chunk (l % 8) ^ (l / 8) of that row (the swizzle)
+  const int xchunk = (lane & 7) ^ (lane >> 3);
+  const _Float16* xsrc[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int row = min(m0 + wv * 64 + 8 * r + (lane >> 3), p.M - 1);   // rows past M repeat the last row
+    xsrc[r] = p.x + (int64_t)row * p.ldx + xchunk * 8;
+  }
+  // W: thread -> row tid of the tile, both groups of a K step; rows past N are dequantised as zero
+  const int ncol = n0 + tid;
   const bool wvalid = ncol < p.N;
-  const int64_t wr = wvalid ? wrow(p, ncol) : 0;
-  const uint8_t* wrec_row = p.w + (wr >> 6) * p.wG * 1280 + (wr & 63) * 16;
-  const uint8_t* wsm_row = p.w + (wr >> 6) * p.wG * 1280 + 1024 + (wr & 63) * 4;
+  const int64_t wr = wrow(p, wvalid ? ncol : n0);
+  const uint8_t* wtile = p.w + (wr >> 6) * p.wG * 1280;   // the row's tile: one 1280-byte record per group
+  const int wr64 = (int)(wr & 63);
 
-  for (int k0 = 0; k0 < p.K; k0 += BK) {
-    // ---- X tile (prologue applied, fp16)
-    {
-      const half8 a = xload8(p, xrow, k0 + sc * 16), b = xload8(p, xrow, k0 + sc * 16 + 8);
-      *(half8*)&xs[sr * LDK + sc * 16] = a;
-      *(half8*)&xs[sr * LDK + sc * 16 + 8] = b;
-    }
-    // ---- W tile: two code words of one row -> 16 fp16 weights
-    {
-      const int64_t gi = (p.wk0 + k0) >> 5;
-      half8 o0, o1;
-      if (wvalid) {
-        const uint32_t* q = (const uint32_t*)(wrec_row + gi * 1280) + sc * 2;
-        const h2_t sm = __builtin_bit_cast(h2_t, *(const uint32_t*)(wsm_row + gi * 1280));
-        const float s = (float)sm.x, mn = (float)sm.y;
-        const uint32_t q0 = q[0], q1 = q[1];
+  auto x_load = [&](int k0, int buf) {   // k0 < K; chunks past K are read from k0 (finite data) and never used
+    uint8_t* xs = lds + buf * kStage + wv * 64 * 128;
+    const int kc = k0 + xchunk * 8 < p.K ? k0 : 0;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          o0[j] = to_h((float)((q0 >> (4 * j)) & 15u) * s + mn);
-          o1[j] = to_h((float)((q1 >> (4 * j)) & 15u) * s + mn);
+    for (int r = 0; r < 8; ++r)
+      __builtin_amdgcn_global_load_lds((const void*)(xsrc[r] + kc), (__attribute__((address_space(3))) void*)(xs + r * 1024),
+                                       16, 0, 0);
+  };
+  u32x4n wq[2];
+  uint32_t wsm[2];
+  auto w_load = [&](int k0) {   // the two groups' records of this row, loaded as they are (used after the MFMAs)
+    const int64_t gi = (p.wk0 + k0) >> 5;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int64_t gg = k0 + 32 * g < p.K ? gi + g : gi;
+      const uint8_t* rec = wtile + gg * 1280;
+      wq[g] = u32x4n(*(const u32x4*)(rec + wr64 * 16));   // weight offsets guarantee 4-byte alignment only
+      wsm[g] = *(const uint32_t*)(rec + 1024 + wr64 * 4);
+    }
+  };
+  auto w_stage = [&](int k0, int buf) {
+    uint8_t* ws = lds + buf * kStage + BM * 128;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const uint32_t sm = (wvalid && k0 + 32 * g < p.K) ? wsm[g] : 0u;   // scale 0, min 0: zero weights
+      const bool fast = pk_exact(sm);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) *(u32x4n*)(ws + swz(tid, 4 * g + w)) = deq_word(wq[g][w], sm, fast);
+    }
+  };
+
+  const int nk = (p.K + BK - 1) / BK;
+  x_load(0, 0);
+  w_load(0);
+  w_stage(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int it = 0; it < nk; ++it) {
+    const int buf = it & 1, k0 = it * BK;
+    if (it + 1 < nk) {   // the next step's X (into the other stage) and W records are in flight during the MFMAs
+      x_load(k0 + BK, buf ^ 1);
+      w_load(k0 + BK);
+    }
+    const uint8_t* xs = lds + buf * kStage;
+    const uint8_t* ws = xs + BM * 128;
+    const int ksteps = p.K - k0 >= BK ? 4 : (p.K - k0) / 16;   // a last step of one group runs 2 of the 4
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if (s < ksteps) {
+        const int c = 2 * s + (lane >> 5);   // this lane's 8 k of the 16: chunk 2 s (lanes 0-31) or 2 s + 1
+        u32x4n av[4], bv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          av[i] = *(const u32x4n*)(xs + swz(wm * 128 + i * 32 + (lane & 31), c));
+          bv[i] = *(const u32x4n*)(ws + swz(wn * 128 + i * 32 + (lane & 31), c));
         }
-      } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) { o0[j] = (_Float16)0.0f; o1[j] = (_Float16)0.0f; }
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, av[i]),
+                                                               __builtin_bit_cast(half8, bv[j]), acc[i][j], 0, 0, 0);
       }
-      *(half8*)&ws[sr * LDK + sc * 16] = o0;
-      *(half8*)&ws[sr * LDK + sc * 16 + 8] = o1;
     }
-    __syncthreads();
-    // ---- MFMA: 2 k-steps of 16, 2 x 2 blocks of 32 x 32 per wave
-#pragma unroll
-    for (int kk = 0; kk < BK; kk += 16) {
-      half8 av[2], bv[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        av[i] = *(const half8*)&xs[(wm * 64 + i * 32 + (lane & 31)) * LDK + kk + (lane >> 5) * 8];
-        bv[i] = *(const half8*)&ws[(wn * 64 + i * 32 + (lane & 31)) * LDK + kk + (lane >> 5) * 8];
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
-    }
+    if (it + 1 < nk) w_stage(k0 + BK, buf ^ 1);
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's direct X loads of the next stage have landed
     __syncthreads();
   }
 
-  // ---- epilogue: acc[i][j][e] is row 8 (e / 4) + 4 (lane / 32) + e % 4, column lane % 32 of block (i, j)
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        const int n = n0 + wn * 64 + j * 32 + (lane & 31);
-        const float a = acc[i][j][e];
-        const float up = __shfl_xor(a, 1, 64);   // swiglu: the odd column (up) of an even column's pair
-        if (m >= p.M || n >= p.N) continue;
-        const int64_t o = (int64_t)m * p.ldy + p.ny0;
-        if (p.epi == P0_GEPI_F16) {
-          ((_Float16*)p.y)[o + n] = to_h(a);
-        } else if (p.epi == P0_GEPI_F32) {
-          ((float*)p.y)[o + n] = a;
-        } else if (p.epi == P0_GEPI_RESADD) {
-          const float g = p.ev ? p.ev[p.evOff + n] : 1.0f, b = p.bv ? p.bv[p.bvOff + n] : 0.0f;
-          float* yp = (float*)p.y + o + n;
-          *yp = p.store ? g * (a + b) : *yp + g * (a + b);
-        } else if (p.epi == P0_GEPI_BIAS) {
-          _Float16* yp = (_Float16*)p.y + o + n;
-          float r = a + p.ev[p.evOff + n];
-          if (p.res) r += (float)*yp;
-          *yp = to_h(r);
-        } else if (!(n & 1)) {   // swiglu: gate = even column, up = the next one (engine/ops/gemm.js:200-206)
-          const int jn = n >> 1;
-          const float gB = p.bv ? p.bv[p.bvOff + jn] : 0.0f, uB = p.bv ? p.bv[p.bvOff + p.bvUp + jn] : 0.0f;
-          ((_Float16*)p.y)[o + jn] = to_h(act_f(p, a + gB) * (up + uB));
-        }
+  // ---- epilogue: acc[i][j][e] is row 8 (e / 4) + 4 (lane / 32) + e % 4, column lane % 32 of block (i, j).
+  // One loop per epilogue (a uniform branch), each small enough to unroll completely: the accumulators stay in
+  // registers.
+  const int mb = m0 + wm * 128 + 4 * (lane >> 5), nb = n0 + wn * 128 + (lane & 31);
+#define P0_EPI_LOOP(...)                                                    \
+  _Pragma("unroll") for (int i = 0; i < 4; ++i)                             \
+  _Pragma("unroll") for (int j = 0; j < 4; ++j)                             \
+  _Pragma("unroll") for (int e = 0; e < 16; ++e) {                          \
+    const int m = mb + i * 32 + 8 * (e >> 2) + (e & 3), n = nb + j * 32;    \
+    const float a = acc[i][j][e];                                           \
+    const int64_t o = (int64_t)m * p.ldy + p.ny0;                           \
+    __VA_ARGS__                                                             \
+  }
+  if (p.epi == P0_GEPI_F16) {
+    P0_EPI_LOOP(if (m < p.M && n < p.N) ((_Float16*)p.y)[o + n] = to_h(a);)
+  } else if (p.epi == P0_GEPI_F32) {
+    P0_EPI_LOOP(if (m < p.M && n < p.N) ((float*)p.y)[o + n] = a;)
+  } else if (p.epi == P0_GEPI_RESADD) {   // engine/ops/gemm.js:192-197
+    P0_EPI_LOOP(if (m < p.M && n < p.N) {
+      const float g = p.ev ? p.ev[p.evOff + n] : 1.0f, b = p.bv ? p.bv[p.bvOff + n] : 0.0f;
+      float* yp = (float*)p.y + o + n;
+      *yp = p.store ? g * (a + b) : *yp + g * (a + b);
+    })
+  } else if (p.epi == P0_GEPI_BIAS) {
+    P0_EPI_LOOP(if (m < p.M && n < p.N) {
+      _Float16* yp = (_Float16*)p.y + o + n;
+      float r = a + p.ev[p.evOff + n];
+      if (p.res) r += (float)*yp;
+      *yp = to_h(r);
+    })
+  } else {   // swiglu: gate = even column, up = the next one, in the neighbouring lane (engine/ops/gemm.js:200-206)
+    P0_EPI_LOOP({
+      const float up = __shfl_xor(a, 1, 64);
+      if (m < p.M && n < p.N && !(n & 1)) {
+        const int jn = n >> 1;
+        const float gB = p.bv ? p.bv[p.bvOff + jn] : 0.0f, uB = p.bv ? p.bv[p.bvOff + p.bvUp + jn] : 0.0f;
+        ((_Float16*)p.y)[o + jn] = to_h(act_f(p, a + gB) * (up + uB));
       }
+    })
+  }
+#undef P0_EPI_LOOP
 }
 
 static const char* gepi_name(int e) {
@@ -230,10 +336,6 @@ extern "C" int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out) {
   p.w = (const uint8_t*)a->w + a->w_off;
   p.wG = a->w_cols / 32;
   p.Nw = a->w_rows;
-  p.x = (const uint8_t*)a->x + a->x_off;
-  p.ldx = a->x_ld ? a->x_ld : K;
-  p.kx0 = a->x_k0;
-  p.xmode = a->x_mode;
   p.M = (int)M; p.N = (int)N; p.K = (int)K;
   p.wr0 = a->wr0; p.wr1 = a->wr1; p.wk0 = a->wk0;
   p.epi = a->epi;
@@ -241,13 +343,39 @@ extern "C" int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out) {
   p.ldy = a->y_ld ? a->y_ld : N;
   p.ny0 = a->y_n0;
   p.ev = a->ev; p.evOff = a->ev_off;
-  p.st = a->stats; p.stOff = a->stats_off;
-  p.pv = a->pv; p.pvOff = a->pv_off; p.pvShift = (uint32_t)(a->pv_off + a->pv_stride);
   p.bv = a->bv; p.bvOff = a->bv_off; p.bvUp = a->bv_up;
   p.act = a->act; p.store = a->store; p.res = a->res;
   (void)gepi_name;
-  dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
-  hipLaunchKernelGGL(q4_gemm_kernel, grid, dim3(256), 0, ctx().cur, p);
+
+  // X': the caller's fp16 rows when they can be streamed as they are (16-byte aligned rows), else one staging pass
+  const int64_t ldx = a->x_ld ? a->x_ld : K;
+  const uint8_t* xbase = (const uint8_t*)a->x + a->x_off;
+  const bool direct = a->x_mode == P0_XMODE_F16 && ((uintptr_t)(xbase + 2 * a->x_k0) % 16 == 0) && (2 * ldx) % 16 == 0;
+  if (direct) {
+    p.x = (const _Float16*)xbase + a->x_k0;
+    p.ldx = ldx;
+  } else {
+    if (int r = ensure_xstage((size_t)M * K * 2, "gemm")) return r;
+    XStageP q{};
+    q.x = xbase; q.ldx = ldx; q.kx0 = a->x_k0; q.xmode = a->x_mode;
+    q.M = (int)M; q.K = (int)K;
+    q.st = a->stats; q.stOff = a->stats_off;
+    q.pv = a->pv; q.pvOff = a->pv_off; q.pvShift = (uint32_t)(a->pv_off + a->pv_stride);
+    q.out = (_Float16*)ctx().xstage;
+    const int64_t chunks = M * (K / 8);
+    const int64_t blocks = (chunks + 255) / 256 < 8192 ? (chunks + 255) / 256 : 8192;
+    hipLaunchKernelGGL(x_stage_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx().cur, q);
+    P0_LAUNCHED("gemm");
+    p.x = (const _Float16*)ctx().xstage;
+    p.ldx = K;
+  }
+  static bool lds_set = false;
+  if (!lds_set) {   // more than 64 KB of dynamic LDS must be allowed once
+    P0_HIP(hipFuncSetAttribute((const void*)q4_gemm_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds), "gemm");
+    lds_set = true;
+  }
+  const int64_t tiles = ((N + BN - 1) / BN) * ((M + BM - 1) / BM);
+  hipLaunchKernelGGL(q4_gemm_kernel, dim3((unsigned)tiles), dim3(256), kGemmLds, ctx().cur, p);
   P0_LAUNCHED("gemm");
   if (flops_out) *flops_out = 2.0 * (double)M * (double)N * (double)K;
   return P0_OK;

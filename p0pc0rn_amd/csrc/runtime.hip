@@ -13,6 +13,28 @@ Ctx& ctx() {
 
 static thread_local std::string g_err;
 
+int ensure_xstage(size_t bytes, const char* op) {
+  Ctx& c = ctx();
+  if (bytes <= c.xstage_bytes) return P0_OK;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(c.cur, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+    set_error("%s: the activation staging workspace needs %zu B; run the call once before recording it", op, bytes);
+    return P0_EINVAL;
+  }
+  size_t want = bytes < (256ull << 20) ? (256ull << 20) : (bytes + (1ull << 20) - 1) / (1ull << 20) * (1ull << 20);
+  P0_HIP(hipStreamSynchronize(c.cur), op);   // the old buffer may still be read by enqueued work
+  if (c.xstage) hipFree(c.xstage);
+  c.xstage = nullptr;
+  c.xstage_bytes = 0;
+  hipError_t e = hipMalloc(&c.xstage, want);
+  if (e != hipSuccess) {
+    set_error("%s: activation staging workspace of %zu B: %s", op, want, hipGetErrorString(e));
+    return P0_ENOMEM;
+  }
+  c.xstage_bytes = want;
+  return P0_OK;
+}
+
 void set_error(const char* fmt, ...) {
   char buf[512];
   va_list ap;
@@ -92,6 +114,7 @@ int p0_close(void) {
   hipStreamSynchronize(c.own);
   hipFree(c.part);
   hipFree(c.counters);
+  if (c.xstage) hipFree(c.xstage);
   hipEventDestroy(c.ev0);
   hipEventDestroy(c.ev1);
   hipStreamDestroy(c.own);
