@@ -55,8 +55,10 @@ __device__ __forceinline__ _Float16 to_h(float v) { return (_Float16)v; }   // R
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
   return (uint32_t)__builtin_bit_cast(uint16_t, to_h(lo)) | ((uint32_t)__builtin_bit_cast(uint16_t, to_h(hi)) << 16);
 }
-// byte offset of the 16-byte chunk c (0..7) of tile row r
-__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+// byte offset of the 16-byte chunk c (0..7) of tile row r. LDS serves a 16-byte access 16 lanes per pass (64 banks);
+// consecutive rows r..r+15 reading one logical chunk land in distinct banks when position = c ^ ((r >> 1) & 7)
+__device__ __forceinline__ int swz_key(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ swz_key(r)) << 4); }
 
 // ------------------------------------------------------------------------------------------------ X staging
 __global__ __launch_bounds__(256) void x_stage_kernel(XStageP p) {
@@ -144,10 +146,14 @@ __device__ __forceinline__ u32x4n deq_word(uint32_t v, uint32_t sm, bool fast) {
   return o;
 }
 
-__global__ __launch_bounds__(256) void q4_gemm_kernel(GemmP p) {
+// 8 waves in 2 (M) x 4 (N), two per SIMD so that one wave's waits are covered by the other's MFMAs; each wave owns a
+// 128 x 64 sub-tile as 4 x 2 blocks of 32 x 32 (128 fp32 accumulators per lane)
+constexpr int kWaves = 8, kThreads = 64 * kWaves, WTM = 128, WTN = 64, IB = WTM / 32, JB = WTN / 32;
+
+__global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmP p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int wm = wv >> 1, wn = wv & 1;
+  const int wm = wv >> 2, wn = wv & 3;
 
   // XCD-aware tile order: consecutive workgroups go to the 8 XCDs in turn, so tile t is given to workgroup
   // (t % per) * 8 + t / per: each XCD walks a contiguous run of row-major tiles and keeps their X rows in its L2
@@ -156,106 +162,153 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(GemmP p) {
   if (T % 8 == 0) t = (blockIdx.x % 8) * (T / 8) + blockIdx.x / 8;
   const int m0 = (t / nbx) * BM, n0 = (t % nbx) * BN;
 
-  float16v acc[4][4];
+  float16v acc[IB][JB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < IB; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < JB; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  // X direct loads: instruction r of wave wv fills tile rows wv * 64 + 8 r .. + 7 (1 KB); lane l lands at byte 16 l,
-  // i.e. row + l / 8, position l % 8, which holds chunk (l % 8) ^ (l / 8) of that row (the swizzle)
-  const int xchunk = (lane & 7) ^ (lane >> 3);
-  const _Float16* xsrc[8];
+  // X direct loads: instruction r of wave wv fills tile rows wv * 32 + 8 r .. + 7 (1 KB); lane l lands at byte 16 l,
+  // i.e. row wv * 32 + 8 r + l / 8, position l % 8, which must hold logical chunk (l % 8) ^ key(row)
+  const _Float16* xsrc[4];
+  int xk[4];
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    const int row = min(m0 + wv * 64 + 8 * r + (lane >> 3), p.M - 1);   // rows past M repeat the last row
-    xsrc[r] = p.x + (int64_t)row * p.ldx + xchunk * 8;
+  for (int r = 0; r < 4; ++r) {
+    const int trow = wv * 32 + 8 * r + (lane >> 3);
+    const int row = min(m0 + trow, p.M - 1);   // rows past M repeat the last row (never stored)
+    xk[r] = ((lane & 7) ^ swz_key(trow)) << 3;
+    xsrc[r] = p.x + (int64_t)row * p.ldx + xk[r];
   }
-  // W: thread -> row tid of the tile, both groups of a K step; rows past N are dequantised as zero
-  const int ncol = n0 + tid;
+  // W: thread -> (row tid % 256 of the tile, group tid / 256 of a K step); rows past N are dequantised as zero
+  const int wrow_t = tid & (BN - 1), wg = tid >> 8;
+  const int ncol = n0 + wrow_t;
   const bool wvalid = ncol < p.N;
   const int64_t wr = wrow(p, wvalid ? ncol : n0);
   const uint8_t* wtile = p.w + (wr >> 6) * p.wG * 1280;   // the row's tile: one 1280-byte record per group
   const int wr64 = (int)(wr & 63);
+  const int wkey = swz_key(wrow_t);
 
-  auto x_load = [&](int k0, int buf) {   // k0 < K; chunks past K are read from k0 (finite data) and never used
-    uint8_t* xs = lds + buf * kStage + wv * 64 * 128;
-    const int kc = k0 + xchunk * 8 < p.K ? k0 : 0;
+  auto x_load = [&](int k0, int buf) {
+    uint8_t* xs = lds + buf * kStage + wv * 32 * 128;
 #pragma unroll
-    for (int r = 0; r < 8; ++r)
+    for (int r = 0; r < 4; ++r) {   // a chunk past K (a last step of one group) reads k0's: finite, never used
+      const int kc = k0 + xk[r] < p.K ? k0 : 0;
       __builtin_amdgcn_global_load_lds((const void*)(xsrc[r] + kc), (__attribute__((address_space(3))) void*)(xs + r * 1024),
                                        16, 0, 0);
+    }
   };
+  // W records of one step, two register sets (see `step`)
   u32x4n wq[2];
   uint32_t wsm[2];
-  auto w_load = [&](int k0) {   // the two groups' records of this row, loaded as they are (used after the MFMAs)
-    const int64_t gi = (p.wk0 + k0) >> 5;
+  auto w_load = [&](int k0, int set) {
+    const bool in = k0 + 32 * wg < p.K;
+    const uint8_t* rec = wtile + (((p.wk0 + k0) >> 5) + (in ? wg : 0)) * 1280;
+    wq[set] = u32x4n(*(const u32x4*)(rec + wr64 * 16));   // weight offsets guarantee 4-byte alignment only
+    wsm[set] = *(const uint32_t*)(rec + 1024 + wr64 * 4);
+  };
+  // dequantise this thread's group of one step into a stage. The fast path is straight-line code (it interleaves with
+  // the MFMAs); a group whose q s + m may not be exact in fp32 is redone by the fp32 path afterwards (rare: a branch)
+  auto w_stage_fast = [&](int k0, int buf, int set) {
+    uint8_t* ws = lds + buf * kStage + BM * 128 + wrow_t * 128;
+    const uint32_t sm = (wvalid && k0 + 32 * wg < p.K) ? wsm[set] : 0u;   // scale 0, min 0: zero weights
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const int64_t gg = k0 + 32 * g < p.K ? gi + g : gi;
-      const uint8_t* rec = wtile + gg * 1280;
-      wq[g] = u32x4n(*(const u32x4*)(rec + wr64 * 16));   // weight offsets guarantee 4-byte alignment only
-      wsm[g] = *(const uint32_t*)(rec + 1024 + wr64 * 4);
+    for (int w = 0; w < 4; ++w) *(u32x4n*)(ws + (((4 * wg + w) ^ wkey) << 4)) = deq_word(wq[set][w], sm, true);
+  };
+  auto w_stage_fix = [&](int k0, int buf, int set) {
+    uint8_t* ws = lds + buf * kStage + BM * 128 + wrow_t * 128;
+    const uint32_t sm = (wvalid && k0 + 32 * wg < p.K) ? wsm[set] : 0u;
+    const bool fast = pk_exact(sm);
+    if (__builtin_amdgcn_ballot_w64(!fast) != 0 && !fast) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) *(u32x4n*)(ws + (((4 * wg + w) ^ wkey) << 4)) = deq_word(wq[set][w], sm, false);
     }
   };
-  auto w_stage = [&](int k0, int buf) {
-    uint8_t* ws = lds + buf * kStage + BM * 128;
+
+  // MFMA operand addresses: rows wm * 128 + 32 i + lane % 32 (A) and wn * 64 + 32 j + lane % 32 (B) share the swizzle
+  // key of lane % 32, so one offset per k-step serves all fragments (the 32-row blocks are 4096 B apart)
+  const int frow = lane & 31, fkey = swz_key(frow), fhalf = lane >> 5;
+  const int aoff = (wm * WTM + frow) * 128, boff = BM * 128 + (wn * WTN + frow) * 128;
+  u32x4n av[2][IB], bv[2][JB];
+  auto frag = [&](const uint8_t* st, int s, int h) {
+    const int cs = ((2 * s + fhalf) ^ fkey) << 4;
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const uint32_t sm = (wvalid && k0 + 32 * g < p.K) ? wsm[g] : 0u;   // scale 0, min 0: zero weights
-      const bool fast = pk_exact(sm);
+    for (int i = 0; i < IB; ++i) av[h][i] = *(const u32x4n*)(st + aoff + i * 4096 + cs);
 #pragma unroll
-      for (int w = 0; w < 4; ++w) *(u32x4n*)(ws + swz(tid, 4 * g + w)) = deq_word(wq[g][w], sm, fast);
+    for (int j = 0; j < JB; ++j) bv[h][j] = *(const u32x4n*)(st + boff + j * 4096 + cs);
+  };
+  auto mfmas = [&](int h) {
+#pragma unroll
+    for (int i = 0; i < IB; ++i)
+#pragma unroll
+      for (int j = 0; j < JB; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, av[h][i]),
+                                                           __builtin_bit_cast(half8, bv[h][j]), acc[i][j], 0, 0, 0);
+  };
+  // one steady-state step (all four k-steps; the next stage exists). Step j's W records live in register set j & 1:
+  // on entry SET = (it + 1) & 1 holds step it + 1 (dequantised now) and the other set holds step it + 2; SET is then
+  // refilled with step it + 3.
+  auto step = [&](int it, int set) {
+    const int buf = it & 1, k0 = it * BK;
+    const uint8_t* st = lds + buf * kStage;
+    frag(st, 0, 0);
+    x_load(k0 + BK, buf ^ 1);   // the next step's X streams into the other stage meanwhile
+    frag(st, 1, 1);
+    mfmas(0);
+    frag(st, 2, 0);
+    w_stage_fast(k0 + BK, buf ^ 1, set);   // W of the next step, amid the MFMAs
+    mfmas(1);
+    frag(st, 3, 1);
+    mfmas(0);
+    w_load(min(k0 + 3 * BK, (p.K - 1) / BK * BK), set);   // step it + 3's records (clamped: the last is re-read)
+    mfmas(1);
+#pragma unroll
+    for (int q = 0; q < 4 * IB * JB; ++q) {   // spread VALU and LDS work between the MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
+    w_stage_fix(k0 + BK, buf ^ 1, set);
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's direct X loads and LDS writes of the next stage are done
+    __syncthreads();
   };
 
   const int nk = (p.K + BK - 1) / BK;
   x_load(0, 0);
-  w_load(0);
-  w_stage(0, 0);
+  w_load(0, 0);
+  if (nk > 1) w_load(BK, 1);
+  w_stage_fast(0, 0, 0);
+  w_stage_fix(0, 0, 0);
+  if (nk > 2) w_load(2 * BK, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  for (int it = 0; it < nk; ++it) {
+  int it = 0;
+  for (; it + 2 < nk; it += 2) {   // two steps per trip: the register sets are compile-time
+    step(it, 1);
+    step(it + 1, 0);
+  }
+  if (it + 1 < nk) {
+    step(it, 1);
+    ++it;
+  }
+  {   // the last step (possibly one group only: two of the four k-steps)
     const int buf = it & 1, k0 = it * BK;
-    if (it + 1 < nk) {   // the next step's X (into the other stage) and W records are in flight during the MFMAs
-      x_load(k0 + BK, buf ^ 1);
-      w_load(k0 + BK);
+    const uint8_t* st = lds + buf * kStage;
+    const int ksteps = p.K - k0 >= BK ? 4 : (p.K - k0) / 16;
+    for (int s = 0; s < ksteps; ++s) {
+      frag(st, s, 0);
+      mfmas(0);
     }
-    const uint8_t* xs = lds + buf * kStage;
-    const uint8_t* ws = xs + BM * 128;
-    const int ksteps = p.K - k0 >= BK ? 4 : (p.K - k0) / 16;   // a last step of one group runs 2 of the 4
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if (s < ksteps) {
-        const int c = 2 * s + (lane >> 5);   // this lane's 8 k of the 16: chunk 2 s (lanes 0-31) or 2 s + 1
-        u32x4n av[4], bv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          av[i] = *(const u32x4n*)(xs + swz(wm * 128 + i * 32 + (lane & 31), c));
-          bv[i] = *(const u32x4n*)(ws + swz(wn * 128 + i * 32 + (lane & 31), c));
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, av[i]),
-                                                               __builtin_bit_cast(half8, bv[j]), acc[i][j], 0, 0, 0);
-      }
-    }
-    if (it + 1 < nk) w_stage(k0 + BK, buf ^ 1);
-    __builtin_amdgcn_s_waitcnt(0);   // this wave's direct X loads of the next stage have landed
-    __syncthreads();
   }
 
   // ---- epilogue: acc[i][j][e] is row 8 (e / 4) + 4 (lane / 32) + e % 4, column lane % 32 of block (i, j).
   // One loop per epilogue (a uniform branch), each small enough to unroll completely: the accumulators stay in
   // registers.
-  const int mb = m0 + wm * 128 + 4 * (lane >> 5), nb = n0 + wn * 128 + (lane & 31);
+  const int mb = m0 + wm * WTM + 4 * (lane >> 5), nb = n0 + wn * WTN + (lane & 31);
 #define P0_EPI_LOOP(...)                                                    \
-  _Pragma("unroll") for (int i = 0; i < 4; ++i)                             \
-  _Pragma("unroll") for (int j = 0; j < 4; ++j)                             \
+  _Pragma("unroll") for (int i = 0; i < IB; ++i)                            \
+  _Pragma("unroll") for (int j = 0; j < JB; ++j)                            \
   _Pragma("unroll") for (int e = 0; e < 16; ++e) {                          \
     const int m = mb + i * 32 + 8 * (e >> 2) + (e & 3), n = nb + j * 32;    \
     const float a = acc[i][j][e];                                           \
@@ -375,7 +428,7 @@ extern "C" int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out) {
     lds_set = true;
   }
   const int64_t tiles = ((N + BN - 1) / BN) * ((M + BM - 1) / BM);
-  hipLaunchKernelGGL(q4_gemm_kernel, dim3((unsigned)tiles), dim3(256), kGemmLds, ctx().cur, p);
+  hipLaunchKernelGGL(q4_gemm_kernel, dim3((unsigned)tiles), dim3(kThreads), kGemmLds, ctx().cur, p);
   P0_LAUNCHED("gemm");
   if (flops_out) *flops_out = 2.0 * (double)M * (double)N * (double)K;
   return P0_OK;
