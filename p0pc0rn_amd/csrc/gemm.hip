@@ -45,6 +45,7 @@ struct XStageP {   // the prologue of engine/ops/gemm.js:55-63 over the caller's
   const float* st; int64_t stOff;
   const float* pv; int64_t pvOff; uint32_t pvShift;   // shift base = (pv_off + pv_stride) mod 2^32
   _Float16* out;     // [M][K]
+  int vec;           // rows and the k offset are 16-byte aligned: vector loads
 };
 
 constexpr int BM = 256, BN = 256, BK = 64;
@@ -69,18 +70,36 @@ __global__ __launch_bounds__(256) void x_stage_kernel(XStageP p) {
     float f[8];
     if (p.xmode == P0_XMODE_F16 || p.xmode == P0_XMODE_BF16) {
       const uint16_t* src = (const uint16_t*)p.x + idx;
+      uint16_t v[8];
+      if (p.vec) {
+        const u32x4n d = *(const u32x4n*)src;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { v[2 * i] = (uint16_t)d[i]; v[2 * i + 1] = (uint16_t)(d[i] >> 16); }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = src[j];
+      }
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        f[j] = p.xmode == P0_XMODE_F16 ? (float)__builtin_bit_cast(_Float16, src[j]) : __uint_as_float((uint32_t)src[j] << 16);
+        f[j] = p.xmode == P0_XMODE_F16 ? (float)__builtin_bit_cast(_Float16, v[j]) : __uint_as_float((uint32_t)v[j] << 16);
     } else {   // engine/ops/gemm.js:59-63
       const float* src = (const float*)p.x + idx;
       const float mean = p.st[(p.stOff + m) * 2], rstd = p.st[(p.stOff + m) * 2 + 1];
       const int64_t kk = p.kx0 + k;
+      float xv[8];
+      if (p.vec) {
+        const u32x4n d0 = *(const u32x4n*)src, d1 = *(const u32x4n*)(src + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { xv[i] = __uint_as_float(d0[i]); xv[i + 4] = __uint_as_float(d1[i]); }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xv[j] = src[j];
+      }
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         f[j] = p.xmode == P0_XMODE_LNMOD
-                   ? (src[j] - mean) * rstd * (1.0f + p.pv[p.pvOff + kk + j]) + p.pv[(int64_t)p.pvShift + kk + j]
-                   : src[j] * rstd * p.pv[p.pvOff + kk + j];
+                   ? (xv[j] - mean) * rstd * (1.0f + p.pv[p.pvOff + kk + j]) + p.pv[(int64_t)p.pvShift + kk + j]
+                   : xv[j] * rstd * p.pv[p.pvOff + kk + j];
     }
     u32x4n o;
 #pragma unroll
@@ -254,14 +273,15 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmP p) {
     const uint8_t* st = lds + buf * kStage;
     frag(st, 0, 0);
     x_load(k0 + BK, buf ^ 1);   // the next step's X streams into the other stage meanwhile
+    w_stage_fast(k0 + BK, buf ^ 1, set);   // W of the next step (spread amid the MFMAs by the scheduler)
+    w_stage_fix(k0 + BK, buf ^ 1, set);
+    w_load(min(k0 + 3 * BK, (p.K - 1) / BK * BK), set);   // step it + 3's records (clamped: the last is re-read)
     frag(st, 1, 1);
     mfmas(0);
     frag(st, 2, 0);
-    w_stage_fast(k0 + BK, buf ^ 1, set);   // W of the next step, amid the MFMAs
     mfmas(1);
     frag(st, 3, 1);
     mfmas(0);
-    w_load(min(k0 + 3 * BK, (p.K - 1) / BK * BK), set);   // step it + 3's records (clamped: the last is re-read)
     mfmas(1);
 #pragma unroll
     for (int q = 0; q < 4 * IB * JB; ++q) {   // spread VALU and LDS work between the MFMAs
@@ -269,8 +289,9 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmP p) {
       __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    w_stage_fix(k0 + BK, buf ^ 1, set);
-    __builtin_amdgcn_s_waitcnt(0);   // this wave's direct X loads and LDS writes of the next stage are done
+    // every memory operation of this step was issued at its start: waiting for all of them here (this wave's direct
+    // X loads of the next stage in particular) costs nothing once the MFMAs have run
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   };
 
@@ -415,6 +436,8 @@ extern "C" int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out) {
     q.st = a->stats; q.stOff = a->stats_off;
     q.pv = a->pv; q.pvOff = a->pv_off; q.pvShift = (uint32_t)(a->pv_off + a->pv_stride);
     q.out = (_Float16*)ctx().xstage;
+    const int esz = (a->x_mode == P0_XMODE_F16 || a->x_mode == P0_XMODE_BF16) ? 2 : 4;
+    q.vec = ((uintptr_t)(xbase + esz * a->x_k0) % 16 == 0) && (esz * ldx) % 16 == 0;
     const int64_t chunks = M * (K / 8);
     const int64_t blocks = (chunks + 255) / 256 < 8192 ? (chunks + 255) / 256 : 8192;
     hipLaunchKernelGGL(x_stage_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx().cur, q);
