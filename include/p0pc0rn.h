@@ -191,7 +191,7 @@ int p0_gemv_tune(int knob, int value);
  * p0_chain_end; a chain runs any number of times, also inside p0_record_begin / p0_record_end. Every wait is bounded:
  * a wait that gives up (which needs another kernel holding the GPU's CUs meanwhile) marks the chain, and
  * p0_chain_status (which waits for the stream) returns 1 once in *timed_out and resets the chain and the split-K
- * counters; the results of that run are invalid.
+ * counters; the results of that run are invalid, and runs of the chain started before that call do nothing.
  * Runs of one chain, or of chains sharing the context's workspace, must not overlap (one stream). */
 typedef struct {
   int32_t n_ops, m, workgroups, waves_per_workgroup;

@@ -346,8 +346,8 @@ extern "C" int p0_chain_end(void** out) {
   ex->grid = grid;
   ex->lds = cb->lds;
   ex->kernel = k;
-  // chain state: last tag, timed out (one 128-byte line each), then one flag per (op, workgroup)
-  const size_t words = kFlagBase + cb->ops.size() * (size_t)grid;
+  // chain state: last tag, timed out, the workgroups' lines and the completion counters (one 128-byte line each)
+  const size_t words = chain_state_words((int)cb->ops.size(), grid);
   const size_t ob = cb->ops.size() * sizeof(GemvP), sb = words * sizeof(unsigned);
   ex->st_words = words;
   hipError_t e = hipMalloc((void**)&ex->ops, ob);
