@@ -127,6 +127,49 @@ struct ChainExec {
 };
 static ChainBuild* g_chain = nullptr;
 
+// Device-coherent accesses of the ops of a chain (GemvP::coh). Op i reads its inputs with coherent loads when an
+// earlier op writes into them, and writes its outputs with coherent stores when a later op reads them or another op
+// writes the same lines (plain stores of two ops to one line from two XCDs would sit in two L2 caches, written back
+// in no set order). Everything else takes plain, L2-cached accesses. Spans are compared as whole 128-byte lines.
+struct Span { uintptr_t a, b; };
+static Span span_of(const float* base, int64_t lo, int64_t hi) {   // floats [lo, hi) of base, widened to lines
+  const uintptr_t a = (uintptr_t)(base + lo), b = (uintptr_t)(base + hi);
+  return {a & ~(uintptr_t)127, (b + 127) & ~(uintptr_t)127};
+}
+static void op_spans(const GemvP& p, int M, std::vector<Span>& rd, std::vector<Span>& wr) {
+  const int64_t m1 = M - 1;
+  if (p.pro == P0_PRO_RAW || p.pro == P0_PRO_RMS) rd.push_back(span_of(p.X, p.rowB, m1 * p.ldx + p.rowB + p.K));
+  else rd.push_back(span_of(p.X, 0, (int64_t)(p.nsrc - 1) * p.ldp + m1 * p.ldx + p.K));   // X[j ldp + m ldx + k]
+  if (p.pro == P0_PRO_RMS) {
+    rd.push_back(span_of(p.ST, p.statOff, p.statOff + m1 * p.statLd + 1));
+    rd.push_back(span_of(p.NW, p.nOff, p.nOff + p.K));
+  }
+  if (p.pro == P0_PRO_PLEG) rd.push_back(span_of(p.EV, p.evOff, p.evOff + m1 * p.evLd + p.K));
+  if (p.epi == P0_EPI_STORE) wr.push_back(span_of(p.Y, 0, (int64_t)(p.nsplit - 1) * p.ldy + m1 * p.ldm + p.N));
+  else wr.push_back(span_of(p.Y, 0, m1 * p.ldm + p.N));
+  if (p.epi == P0_EPI_SOFTCAP) wr.push_back(span_of(p.MX, 0, (int64_t)M * p.NT * 2));
+}
+static void mark_coherence(std::vector<GemvP>& ops, int M) {
+  const size_t n = ops.size();
+  std::vector<std::vector<Span>> rd(n), wr(n);
+  for (size_t i = 0; i < n; ++i) op_spans(ops[i], M, rd[i], wr[i]);
+  auto meet = [](const std::vector<Span>& x, const std::vector<Span>& y) {
+    for (const Span& a : x)
+      for (const Span& b : y)
+        if (a.a < b.b && b.a < a.b) return true;
+    return false;
+  };
+  for (size_t i = 0; i < n; ++i) {
+    int c = 0;
+    for (size_t j = 0; j < n; ++j) {
+      if (j < i && meet(rd[i], wr[j])) c |= 1;
+      if (j > i && meet(wr[i], rd[j])) c |= 2;
+      if (j != i && meet(wr[i], wr[j])) c |= 2;
+    }
+    ops[i].coh = c;
+  }
+}
+
 // plan of one op inside a chain: all W waves of a workgroup busy (tgw = W / kw), one K-slice per split unless the op
 // leaves half the grid idle AND a wave's share would exceed g_chain_split_gpw groups
 static Plan plan_chain(int M, int NT, int epi, int nsplit, int kPer, int W, int G) {
@@ -190,6 +233,7 @@ static int launch(GemvP& p, int M, const char* op) {
   p.mode = pl.mode;
   p.part = ctx().part;
   p.cnt = ctx().counters;
+  p.coh = 0;   // chains: set for the whole chain by p0_chain_end
   if (cb) {
     cb->ops.push_back(p);
     if (pl.lds > cb->lds) cb->lds = pl.lds;
@@ -339,6 +383,7 @@ extern "C" int p0_chain_end(void** out) {
   int grid = ctx().cu_count * per_cu;
   if (grid > cb->G) grid = cb->G;   // the plans were made for G workgroups; never more than are resident
   if (grid > kChainMaxGrid) grid = kChainMaxGrid;
+  mark_coherence(cb->ops, cb->M);
   auto* ex = new ChainExec{};
   ex->n_ops = (int)cb->ops.size();
   ex->M = cb->M;

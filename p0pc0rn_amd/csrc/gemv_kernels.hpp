@@ -55,6 +55,9 @@ struct GemvP {
   int ntb;            // tile blocks (grid.x)
   int rowsTot;        // rows that carry partials: N, or 2N for a geglu
   int mode;           // kernel mode (chain ops choose their code path from it)
+  // chain ops: bit 0 = read the inputs with device-coherent loads (an earlier op of the chain writes into them), bit
+  // 1 = write the outputs with device-coherent stores (a later op reads them, or another op writes the same lines)
+  int coh;
   float* part; unsigned* cnt;
 };
 
@@ -89,6 +92,66 @@ __device__ __forceinline__ float prologue(const GemvP& p, int m, int k) {
   for (int j = 0; j < p.nsrc; ++j) s += ldf<COH>(&p.X[j * p.ldp + m * p.ldx + k]);
   if (p.pro == P0_PRO_SUM) return s;
   return gelu_tanh(s) * ldf<COH>(&p.EV[p.evOff + m * p.evLd + k]);
+}
+
+// U prologue values of one thread, every load issued before any is used (the device-coherent loads of a chain are
+// ordered memory operations: interleaved with their uses they would wait one at a time). Element u is x'[m[u]][kb +
+// kl[u]]; only the first nu (the same in the whole wave) are loaded, the rest are 0, and so are entries at or past
+// ke (which read the slice's last element, in bounds).
+template <bool COH, int U, int M>
+__device__ __forceinline__ void prologue_batch(const GemvP& p, int nu, const int (&m)[U], int kb, int ke,
+                                               const int (&kl)[U], float (&v)[U]) {
+  int k[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    k[u] = min(kb + kl[u], ke - 1);
+    v[u] = 0.0f;
+  }
+  if (p.pro == P0_PRO_RAW || p.pro == P0_PRO_RMS) {
+    float a[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (u < nu) a[u] = ldf<COH>(&p.X[m[u] * p.ldx + p.rowB + k[u]]);
+    if (p.pro == P0_PRO_RMS) {
+      float b[U], c[U];
+      if (M == 1) {
+        const float b0 = ldf<COH>(&p.ST[p.statOff]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) b[u] = b0;
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (u < nu) b[u] = ldf<COH>(&p.ST[p.statOff + m[u] * p.statLd]);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (u < nu) c[u] = ldf<COH>(&p.NW[p.nOff + k[u]]);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (u < nu) a[u] = a[u] * b[u] * c[u];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (u < nu && kb + kl[u] < ke) v[u] = a[u];
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (u < nu && kb + kl[u] < ke) v[u] = prologue<COH>(p, m[u], k[u]);
+  }
+}
+
+// sum over the 32 lanes 32j .. 32j + 31 (a pairwise tree: quads, halves of rows, rows of 16, then the two rows); every
+// lane of the 32 gets the same value
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float sum32(float v) {
+  v += dpp_f<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+  v += dpp_f<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+  v += dpp_f<0x141>(v);   // row_half_mirror
+  v += dpp_f<0x140>(v);   // row_mirror
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));   // lane ^ 16
 }
 
 struct Rec {
@@ -180,9 +243,11 @@ __device__ __forceinline__ void epilogue(const GemvP& p, int split, int m, int t
 // before its input is read (the chain executor waits for the producing op there; a standalone launch has nothing to
 // wait for); it returns false (in every thread) to abandon the item. Returns true when this workgroup wrote the
 // final outputs of its (split, tile block): always for one K-slice per split, only the last arriving workgroup
-// otherwise. The value is the same in every thread. CHAIN: activations move through device-coherent accesses, and
-// wave 0 (whose first thread polls in `ready()`) issues its first chunk after the wait, so that its poll does not
-// queue behind its own weight loads (a wave's loads return in order).
+// otherwise. The value is the same in every thread. CHAIN: activations that ops hand to each other move through
+// device-coherent accesses (GemvP::coh). Every wave issues its first chunk before the wait, the polling wave too: its
+// first poll then returns behind those loads (a wave's loads complete in order), which costs nothing when the wait is
+// longer than the loads' latency, and a wave that issued them after the wait would hold the whole workgroup at the
+// prologue's barrier for a full HBM latency.
 template <int M, int MODE, bool CHAIN, class Ready>
 __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float* smem, int* s_last, Ready&& ready) {
   constexpr int T = MODE == 0 ? 1 : 2;
@@ -194,6 +259,7 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
   // (in bounds, value unused), so every load is unconditional.
   constexpr int D = MODE == 0 ? 8 : 4;
   const int tid = threadIdx.x, lane = tid & 63;
+  const bool coh_in = CHAIN && (p.coh & 1), coh_out = CHAIN && (p.coh & 2);
   // wave-uniform indices live in SGPRs: record addresses become a scalar base plus the lane's constant 16-byte offset
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kwv = wv % p.kw, tw = wv / p.kw;
@@ -228,36 +294,43 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
   // ---- the share's first chunk is issued before the input is read: its latency overlaps the wait and the prologue
   __syncthreads();   // the previous item of this workgroup is done with the LDS
   Rec r0[D][T];
-  const bool late = CHAIN && wv == 0;
-  if (streams && !late) {
+  if (streams) {
 #pragma unroll
     for (int i = 0; i < D; ++i)
 #pragma unroll
       for (int t = 0; t < T; ++t) r0[i][t] = load_rec<MODE == 1>(p, tl(t), min(wg0 + i, glast), lane);
   }
   if (!ready()) return false;
-  if (streams && late) {
-#pragma unroll
-    for (int i = 0; i < D; ++i)
-#pragma unroll
-      for (int t = 0; t < T; ++t) r0[i][t] = load_rec<MODE == 1>(p, tl(t), min(wg0 + i, glast), lane);
-  }
 
-  // ---- prologue: x'[m][k] for the workgroup's K-slice -> LDS (odd k scaled 1/16), then per-group sums of x'
-  const int kb = g0 * 32, ke = g1 * 32;
-  for (int idx = tid; idx < M * KL; idx += blockDim.x) {
-    const int m = idx / KL, kl = idx - m * KL, k = kb + kl;
-    float v = k < ke ? prologue<CHAIN>(p, m, k) : 0.0f;
-    xs[idx] = (k & 1) ? v * 0.0625f : v;
-  }
-  __syncthreads();
-  for (int idx = tid; idx < M * p.gps; idx += blockDim.x) {
-    const int m = idx / p.gps, gl = idx - m * p.gps;
-    const float* xp = xs + m * KL + gl * 32;
-    float s = 0.0f;
+  // ---- prologue: x'[m][k] for the workgroup's K-slice -> LDS (odd k scaled 1/16), and the per-group sums of x'.
+  // Thread tid takes elements u * blockDim + tid of each batch of U: the 32 lanes of a 32-aligned lane group hold one
+  // group's 32 k (KL and the block size are multiples of 32), which they sum with cross-lane adds. Every thread runs
+  // the same number of batches, so all lanes take part in the cross-lane adds.
+  {
+    constexpr int U = M == 1 ? 4 : 8;
+    const int kb = g0 * 32, ke = g1 * 32, nx = M * KL, nt = blockDim.x;
+    for (int i0 = 0; i0 < nx; i0 += U * nt) {
+      int mm[U], kl[U];
+      float v[U];
 #pragma unroll
-    for (int i = 0; i < 32; i += 2) s += xp[i] + xp[i + 1] * 16.0f;
-    xsum[idx] = s;
+      for (int u = 0; u < U; ++u) {
+        const int idx = i0 + u * nt + tid;
+        mm[u] = M == 1 ? 0 : min(idx / KL, M - 1);
+        kl[u] = idx - mm[u] * KL;   // >= KL (so past ke) for idx >= nx
+      }
+      // batches of this wave that hold elements (u * nt + the wave's first thread < nx - i0)
+      const int nu = ke > kb ? min(U, max(0, (nx - i0 - (wv << 6) + nt - 1) / nt)) : 0;
+      if (coh_in) prologue_batch<true, U, M>(p, nu, mm, kb, ke, kl, v);
+      else prologue_batch<false, U, M>(p, nu, mm, kb, ke, kl, v);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float gs = sum32(v[u]);
+        if (i0 + u * nt + tid < nx) {
+          xs[mm[u] * KL + kl[u]] = (kl[u] & 1) ? v[u] * 0.0625f : v[u];   // kb is even: k and kl share parity
+          if ((lane & 31) == 0) xsum[mm[u] * p.gps + (kl[u] >> 5)] = gs;
+        }
+      }
+    }
   }
   __syncthreads();
 
@@ -304,8 +377,11 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
     }
   }
 
-  // ---- the kw waves of a slot: sum their shares in wave order into wave kwv == 0
+  // ---- the kw waves of a slot: sum their shares in wave order into wave kwv == 0. The reads are unrolled to the
+  // largest kw (the workgroup's wave count) with clamped indices, so they issue back to back and wait once; the
+  // entries past kw add an exact zero.
   if (p.kw > 1) {
+    constexpr int KWMAX = M <= 2 ? 16 : 8;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       __syncthreads();
@@ -315,8 +391,12 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
       if (kwv == 0) {
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-          float s = 0.0f;
-          for (int j = 0; j < p.kw; ++j) s += red[((wv + j) * T + t) * 64 + lane];
+          float v[KWMAX];
+#pragma unroll
+          for (int j = 0; j < KWMAX; ++j) v[j] = red[((wv + min(j, p.kw - 1)) * T + t) * 64 + lane];
+          float s = v[0];
+#pragma unroll
+          for (int j = 1; j < KWMAX; ++j) s += j < p.kw ? v[j] : 0.0f;
           acc[t][m] = s;
         }
       }
@@ -325,16 +405,20 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
 
   // ---- one K-slice per split: the epilogue straight from registers
   const bool owner = active && kwv == 0;
+  auto epi = [&](int sp, int m, int t0, float v0, float v1) {
+    if (coh_out) epilogue<true>(p, sp, m, t0, lane, v0, v1);
+    else epilogue<false>(p, sp, m, t0, lane, v0, v1);
+  };
   if (p.nks == 1) {
     if (owner) {
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         if (MODE == 2) {
-          epilogue<CHAIN>(p, split, m, tile[0], lane, acc[0][m], acc[T - 1][m]);
+          epi(split, m, tile[0], acc[0][m], acc[T - 1][m]);
         } else {
 #pragma unroll
           for (int t = 0; t < T; ++t)
-            if (tile[t] < p.NT) epilogue<CHAIN>(p, split, m, tile[t], lane, acc[t][m], 0.0f);
+            if (tile[t] < p.NT) epi(split, m, tile[t], acc[t][m], 0.0f);
         }
       }
     }
@@ -383,11 +467,11 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
       }
     }
     if (MODE == 2) {
-      epilogue<CHAIN>(p, split, m, tile[0], lane, tot[0], tot[T - 1]);
+      epi(split, m, tile[0], tot[0], tot[T - 1]);
     } else {
 #pragma unroll
       for (int t = 0; t < T; ++t)
-        if (tile[t] < p.NT) epilogue<CHAIN>(p, split, m, tile[t], lane, tot[t], 0.0f);
+        if (tile[t] < p.NT) epi(split, m, tile[t], tot[t], 0.0f);
     }
   }
   return true;
@@ -469,16 +553,13 @@ __global__ __launch_bounds__(64 * W) void q4_gemv_chain_kernel(const GemvP* __re
         if (waited) return true;   // only the workgroup's first item of op i waits for op i - 1
         if (tid == 0) {
           const unsigned want = (tag << 16) | (unsigned)i;   // op i - 1 complete
-          int go = 1;
-          for (int spins = 0; ld_coh(box + (size_t)b * kCtrStride) != want; ++spins) {
-            // spin_limit < 0: the host asks every wait to give up at once (tests of the timed-out path)
-            if (spin_limit < 0 || spins >= spin_limit || (spins % 64 == 63 && ld_coh(timed_out))) {
-              atomicOr(timed_out, 1u);
-              go = 0;
-              break;
-            }
-            __builtin_amdgcn_s_sleep(1);
+          // spin_limit < 0: the host asks every wait to give up at once (tests of the timed-out path)
+          int go = spin_limit >= 0;
+          for (int spins = 0; go && ld_coh(box + (size_t)b * kCtrStride) != want; ++spins) {
+            if (spins >= spin_limit || (spins % 64 == 63 && ld_coh(timed_out))) go = 0;
+            else __builtin_amdgcn_s_sleep(1);
           }
+          if (!go) atomicOr(timed_out, 1u);
           s_go = go;   // op i - 1's outputs are read with coherent loads: no L2 invalidate
         }
         __syncthreads();

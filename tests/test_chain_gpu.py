@@ -187,6 +187,54 @@ def test_chain_equals_standalone_calls(dev):
     s.free()
 
 
+def test_chain_layers_reuse_buffers(dev):
+    """Six layers that read and rewrite the same two buffers (a -> b -> a ...), then two ops that write one output.
+    Each op must read what the op before it wrote in this run, never a copy that an earlier layer left in a cache, and
+    the last writer of a buffer must win. The final a is checked against the oracle run op by op on the host (twelve
+    dependent fp32 GEMVs: relative L2 within 1e-4, the fp32 bar compounded); the last writer's output exactly, to the
+    fp32 bar, on the chain's own input."""
+    D, L = 256, 6
+    ws = [_w(D, D, 100 + i) for i in range(2 * L + 2)]
+    a0 = O.randn(D, 99)
+    wd = [capi.to_device(w) for w in ws]
+    a, b, z = capi.to_device(a0), capi.Buffer(4 * D), capi.Buffer(4 * D)
+
+    def op(w, x, y):
+        capi.q4_gemv(capi.gemv_args(w=w, w_rows=D, w_cols=D, x=x, N=D, K=D, y=y))
+
+    def enqueue():
+        for l in range(L):
+            op(wd[2 * l], a, b)
+            op(wd[2 * l + 1], b, a)
+        op(wd[2 * L], a, z)
+        op(wd[2 * L + 1], a, z)
+
+    ch = capi.chain(enqueue)
+    want = a0.copy()
+    for i in range(2 * L):
+        y = np.zeros(D, np.float32)
+        O.q4_gemv(capi.gemv_args(w=ws[i].ctypes.data, w_rows=D, w_cols=D, x=want.ctypes.data, N=D, K=D,
+                                 y=y.ctypes.data))
+        want = y
+    for r in range(3):
+        a.upload(a0)
+        b.fill_u32(NAN)
+        z.fill_u32(NAN)
+        ch.run()
+        assert not ch.status()
+        ga, gz = a.read(np.float32), z.read(np.float32)
+        r_a = rel_l2(ga, want)
+        print(f"run {r}: final a rel_l2 {r_a:.3e}", flush=True)
+        assert np.all(np.isfinite(ga)) and r_a <= 1e-4
+        wz = np.zeros(D, np.float32)
+        O.q4_gemv(capi.gemv_args(w=ws[2 * L + 1].ctypes.data, w_rows=D, w_cols=D, x=ga.ctypes.data, N=D, K=D,
+                                 y=wz.ctypes.data))
+        _check(gz, wz, f"run {r}: last writer of z")
+    ch.free()
+    for buf in wd + [a, b, z]:
+        buf.free()
+
+
 @pytest.mark.parametrize("knob,value", [(0, 8), (1, 2)])
 def test_chain_other_plans(dev, knob, value):
     """8-wave workgroups; and K split across workgroups inside the chain (cross-workgroup reduction + counts)"""
