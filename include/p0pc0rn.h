@@ -205,8 +205,13 @@ int p0_chain_info(void* chain, p0_chain_info_t* out);
 int p0_chain_free(void* chain);
 /* knob 0: waves per chain workgroup for M = 1 (8 or 16, default 16); knob 1: largest wave share in q4 groups before
  * a chain op splits K across workgroups (default 16); knob 2: polls before a chain wait gives up (default 2^22);
- * knob 3: 1 = every wait of later runs gives up at once (for tests of the timed-out path), 0 = normal.
- * Knobs 0-1 apply to chains begun afterwards, 2-3 to runs. value < 0 only queries (knobs 0-2 also ignore 0);
+ * knob 3: 1 = every wait of later runs gives up at once (for tests of the timed-out path), 0 = normal; knob 4: 1 =
+ * staged ops (each workgroup copies its share of an op's weights into LDS before it waits for the previous op; the
+ * default: M = 1 chains run on the pipelined kernel, whose loader waves stream every op's weights into an LDS ring
+ * ops ahead of the arithmetic; other chains stage the ops whose share fits), 0 = every op streams its weights after
+ * the wait; knob 5: loader waves of the pipelined kernel that stream (1..4, default 2); knob 6: LDS slots each loader
+ * keeps in flight (1 or 2, default 2).
+ * Knobs 0-1 and 4-6 apply to chains begun afterwards, 2-3 to runs. value < 0 only queries (knobs 0-2 also ignore 0);
  * returns the previous value. */
 int p0_chain_tune(int knob, int value);
 

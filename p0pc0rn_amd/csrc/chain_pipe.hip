@@ -1,0 +1,359 @@
+// chain_pipe.hip - the pipelined GEMV chain for M = 1 (a decode step's GEMVs in ONE persistent launch, the analogue of
+// the reference's per-token command buffer, engine/llm/drunner.js:1-8). The planning is in gemv.hip (plan_pipe);
+// the op arithmetic, prologues and epilogues are those of gemv_kernels.hpp.
+//
+// Why a second chain kernel. A decode step is 121 dependent GEMVs of 2.6-21 MB: each op can start its arithmetic
+// only once the previous op has written all of its outputs, so the step is a chain of hand-offs, and every hand-off
+// costs memory round trips. A wave's loads complete in order, so a wave that has weight loads in flight cannot see a
+// completion flag or an activation before those loads land: a workgroup that streams its weights after the hand-off
+// puts the whole weight transfer on the chain's critical path, and one that issues them just before still puts the
+// rest of the transfer in front of its poll and its x loads. Here the roles are split by wave:
+//
+//  * 4 loader waves stream every op's weight share into a ring of 12 LDS slots with LDS-DMA loads
+//    (global_load_lds_dwordx4), ops ahead of the arithmetic, as far as the ring has room. They never touch
+//    activations or flags, so their loads delay nothing but the next slot.
+//  * 8 compute waves wait for the previous op (one wave polls its XCD's copy of the completion flags), stage x',
+//    take the slots as the loaders publish them, reduce, run the epilogue, and publish this workgroup's completion.
+//    They synchronise among themselves through an LDS counter (the hardware barrier would also wait for the
+//    loaders).
+//
+// Work split. Every op is cut into units of 16 rows (64 for a softcap, whose tile maximum needs a whole 64-row tile;
+// a geglu unit also holds the matching up rows) x one split (kPer); unit u goes to workgroup position
+// (scur + u) mod G (consecutive positions on one XCD). A slot is 16 rows x 32 groups of one unit (10 KB): the rows'
+// codes [32 groups][16 rows][16 B] then their scale words [32][16][4 B]. Small shares (a few slots) are computed by
+// all 8 compute waves together, one (group, row) pair per lane per slot; large shares (the lm_head) by one wave per
+// unit, each lane taking 8 pairs per slot, so the waves stream independently.
+#include "gemv_kernels.hpp"
+
+namespace p0 {
+
+constexpr int kPL = 4;                       // loader waves
+constexpr int kPC = 8;                       // compute waves
+constexpr int kPW = kPL + kPC;
+constexpr int kSlotB = kStageRows * 32 * 20; // 10240: one slot
+constexpr int kRing = 12;                    // slots in the ring
+constexpr int kPipeKL = 3072;                // largest split (gemv: kch <= 3072)
+constexpr int kPipeRedRp = 16;               // spread shares: most 16-row parts per workgroup
+// chain state words (in the first 128-byte line, after the tag) that the host sets from p0_chain_tune knob 5
+constexpr int kCfgLoaders = 4, kCfgDepth = 5;
+
+// LDS layout (bytes)
+constexpr int kOffXs = kRing * kSlotB;                         // x' [kPipeKL] (odd k scaled 1/16)
+constexpr int kOffXsum = kOffXs + kPipeKL * 4;                 // group sums [kPipeKL / 32]
+constexpr int kOffRed = kOffXsum + (kPipeKL / 32) * 4;         // spread: [part][compute wave][16 rows]
+constexpr int kOffWred = kOffRed + kPipeRedRp * kPC * 16 * 4;  // per wave: [compute wave][2][64 rows]
+constexpr int kOffCtl = kOffWred + kPC * 2 * 64 * 4;           // control words
+constexpr int kCtlFull = 0, kCtlRel = kRing, kCtlBar = 2 * kRing, kCtlStop = 2 * kRing + 1,
+              kCtlGo = 2 * kRing + 2, kCtlTag = 2 * kRing + 3, kCtlWords = 2 * kRing + 4;
+constexpr int kPipeLds = kOffCtl + kCtlWords * 4;
+
+__host__ int pipe_lds_bytes() { return kPipeLds; }
+__host__ int pipe_waves() { return kPW; }
+__host__ int pipe_ring_slots() { return kRing; }
+__host__ int pipe_spread_parts() { return kPipeRedRp; }
+__host__ int pipe_cfg_word() { return kCfgLoaders; }
+
+// LDS words seen by the loader waves through inline assembly: the compiler tracks LDS-DMA loads as pending writes to
+// LDS and would otherwise wait for all of them (vmcnt(0)) before any LDS access in the loader code, which would
+// drain the loads in flight at every ring check.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ unsigned asm_lds_ld(unsigned a) {
+  unsigned v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+  return v;
+}
+__device__ __forceinline__ void asm_lds_st(unsigned a, unsigned v) {
+  asm volatile("ds_write_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : : "v"(a), "v"(v) : "memory");
+}
+
+// a workgroup's share of one op
+struct Share {
+  int nu, first, nrb, parts, nh, ngs, split, gA, nslot, spread;
+};
+__device__ __forceinline__ Share share_of(const GemvP& p, int b, int G) {
+  Share s;
+  const int pos = stage_pos(b, G);
+  s.first = pos >= p.scur ? pos - p.scur : pos - p.scur + G;
+  s.nu = s.first < p.su ? (p.su - s.first + G - 1) / G : 0;
+  s.nrb = p.snrb;
+  s.parts = p.epi == P0_EPI_GEGLU ? 2 : 1;
+  s.split = s.first % p.nsplit;   // every unit of a share has this split (the host checks)
+  s.gA = s.split * (p.kPer >> 5);
+  s.ngs = (min(p.K, (s.split + 1) * p.kPer) >> 5) - s.gA;
+  s.nh = (s.ngs + 31) >> 5;
+  s.nslot = s.nu * s.nrb * s.parts * s.nh;
+  s.spread = p.sngp;   // the host's choice: 1 = all compute waves on every slot, 0 = one wave per unit
+  return s;
+}
+// Slot order of a share. Spread shares: unit-major, then block, part, half. Per-wave shares: units in rounds of kPC
+// (unit j = kPC R + c goes to compute wave c), and inside a round the waves' slots interleave (slot s of every unit,
+// then slot s + 1, ...), so the ring's consecutive slots feed all waves at once.
+__device__ __forceinline__ void slot_of(const Share& s, int k, int& j, int& si) {
+  if (s.spread) {
+    const int S = s.nrb * s.parts * s.nh;
+    j = k / S;
+    si = k - j * S;
+    return;
+  }
+  const int S = s.nrb * s.parts * s.nh, R = min(k / (kPC * S), (s.nu - 1) / kPC);
+  const int nw = min(kPC, s.nu - kPC * R), kr = k - R * kPC * S;
+  si = kr / nw;
+  j = kPC * R + (kr - si * nw);
+}
+__device__ __forceinline__ int slot_index(const Share& s, int j, int si) {   // inverse of slot_of
+  const int S = s.nrb * s.parts * s.nh;
+  if (s.spread) return j * S + si;
+  const int R = j / kPC, nw = min(kPC, s.nu - kPC * R);
+  return R * kPC * S + si * nw + (j - kPC * R);
+}
+// first weight row of part (unit j, block r, part pt) of a share
+__device__ __forceinline__ int share_row(const GemvP& p, const Share& s, int G, int j, int r, int pt) {
+  return ((s.first + j * G) / p.nsplit * s.nrb + r) * kStageRows + (pt ? p.N : 0);
+}
+
+__global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __restrict__ ops, int n_ops,
+                                                                 unsigned* __restrict__ st, int spin_limit) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  uint8_t* const lds = (uint8_t*)smem;
+  unsigned* const ctl = (unsigned*)(lds + kOffCtl);
+  const int tid = threadIdx.x, lane = tid & 63, G = gridDim.x, b = blockIdx.x;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int Gp = chain_flag_stride(G);
+  unsigned* const timed_out = st + kCtrStride;
+  unsigned* const flags = st + 2 * kCtrStride;
+  if (tid < kCtlWords) ctl[tid] = 0;
+  if (tid == 0) {
+    ctl[kCtlTag] = ld_coh(st) + 1;
+    ctl[kCtlGo] = ld_coh(timed_out) == 0u;   // an earlier run gave up: do nothing until p0_chain_status resets it
+  }
+  __syncthreads();
+  const unsigned tag = ctl[kCtlTag];
+  if (!ctl[kCtlGo]) return;
+
+  if (wv < kPL) {
+    // ------------------------------------------------------------------ loader waves
+    // st[kCfgLoaders]: loader waves that stream (1 .. kPL), st[kCfgDepth]: slots in flight per loader (1 or 2)
+    const int nl = min(kPL, max(1, (int)st[kCfgLoaders])), depth2 = st[kCfgDepth] >= 2;
+    if (wv >= nl) return;
+    const unsigned a_full = lds_addr(ctl + kCtlFull), a_rel = lds_addr(ctl + kCtlRel), a_stop = lds_addr(ctl + kCtlStop);
+    int q0 = 0, pend = -1;
+    auto publish = [&](int q) { asm_lds_st(a_full + (q % kRing) * 4, (unsigned)q + 1); };
+    for (int i = 0; i < n_ops; ++i) {
+      const GemvP& p = ops[i];
+      const Share s = share_of(p, b, G);
+      const int k0 = ((wv - q0) % nl + nl) % nl;
+      for (int k = k0; k < s.nslot; k += nl) {
+        const int q = q0 + k, pos = q % kRing;
+        if ((int)asm_lds_ld(a_rel + pos * 4) < q / kRing) {   // the position still holds slot q - kRing
+          if (pend >= 0) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            publish(pend);
+            pend = -1;
+          }
+          while ((int)asm_lds_ld(a_rel + pos * 4) < q / kRing) {
+            if (asm_lds_ld(a_stop)) {   // the compute waves gave up: leave, with no load in flight
+              asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+              return;
+            }
+            __builtin_amdgcn_s_sleep(1);
+          }
+        }
+        // slot k of the share: unit j, its slot si = (block r, part pt, half h of 32 groups)
+        int j, si;
+        slot_of(s, k, j, si);
+        const int h = si % s.nh, rest = si / s.nh, pt = rest % s.parts, r = rest / s.parts;
+        const int n = share_row(p, s, G, j, r, pt);
+        const uint8_t* tb = p.w + ((int64_t)(n >> 6) * p.wG + s.gA) * 1280;
+        const int r0 = n & 63, glast = s.ngs - 1;
+        uint8_t* const slot = lds + pos * kSlotB;
+#pragma unroll
+        for (int ci = 0; ci < 8; ++ci) {   // codes: 4 groups per load (lane: group 4 ci + lane / 16, row lane % 16)
+          const int g = min(32 * h + 4 * ci + (lane >> 4), glast);
+          const uint8_t* src = tb + (int64_t)g * 1280 + (r0 + (lane & 15)) * 16;
+          __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(slot + ci * 1024),
+                                           16, 0, 0);
+        }
+#pragma unroll
+        for (int si = 0; si < 2; ++si) {   // scale words: 16 groups per load (lane: group 16 si + lane / 4, 4 rows)
+          const int g = min(32 * h + 16 * si + (lane >> 2), glast);
+          const uint8_t* src = tb + (int64_t)g * 1280 + 1024 + (r0 + 4 * (lane & 3)) * 4;
+          __builtin_amdgcn_global_load_lds((const void*)src,
+                                           (__attribute__((address_space(3))) void*)(slot + 8192 + si * 1024), 16, 0, 0);
+        }
+        if (!depth2) {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          publish(q);
+          continue;
+        }
+        if (pend >= 0) {   // the previous slot's 10 loads are older than this slot's 10
+          asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+          publish(pend);
+        }
+        pend = q;
+      }
+      q0 += s.nslot;
+    }
+    if (pend >= 0) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      publish(pend);
+    }
+    return;
+  }
+
+  // -------------------------------------------------------------------- compute waves
+  const int c = wv - kPL, tc = tid - 64 * kPL;
+  volatile unsigned* const vctl = ctl;
+  float* const xs = (float*)(lds + kOffXs);
+  float* const xsum = (float*)(lds + kOffXsum);
+  float* const red = (float*)(lds + kOffRed);
+  float* const wred = (float*)(lds + kOffWred) + c * 128;
+  unsigned gen = 0;
+  // barrier of the compute waves: a monotonic LDS counter (every compute wave adds 1 per barrier)
+  auto cbar = [&]() {
+    gen += kPC;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // this wave's LDS writes are done
+    if (lane == 0) __hip_atomic_fetch_add(ctl + kCtlBar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    while (vctl[kCtlBar] < gen) __builtin_amdgcn_s_sleep(0);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  };
+  auto wait_slot = [&](int q) {
+    while (vctl[kCtlFull + q % kRing] != (unsigned)q + 1) __builtin_amdgcn_s_sleep(0);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  };
+  // the G flags at f hold this run's tag (wave c == 0 polls); false in every compute thread if the wait gave up
+  auto wait_flags = [&](const unsigned* f) -> bool {
+    if (c == 0) {
+      int go = spin_limit >= 0;   // spin_limit < 0: every wait gives up at once (tests of the timed-out path)
+      for (int spins = 0; go && !flags_set(f, G, tag, lane); ++spins) {
+        if (spins >= spin_limit || (spins % 64 == 63 && ld_coh(timed_out))) go = 0;
+        else __builtin_amdgcn_s_sleep(1);
+      }
+      if (lane == 0) {
+        if (!go) {
+          atomicOr(timed_out, 1u);
+          vctl[kCtlStop] = 1;   // the loaders leave their waits
+        }
+        vctl[kCtlGo] = go;
+      }
+    }
+    cbar();
+    return vctl[kCtlGo] != 0;
+  };
+  const unsigned* const mine = flags + (size_t)(b % kFlagCopies) * n_ops * Gp;   // this XCD's copy
+  int q0 = 0;
+  bool abandon = false;
+  for (int i = 0; i < n_ops; ++i) {
+    const GemvP& p = ops[i];
+    const Share s = share_of(p, b, G);
+    if (s.nu > 0) {
+      if (i > 0 && !wait_flags(mine + (size_t)(i - 1) * Gp)) {
+        abandon = true;
+        break;
+      }
+      // op i - 1's outputs are read with coherent loads: no L2 invalidate
+      if (p.coh & 1) stage_x<1, true>(p, s.gA, s.gA + s.ngs, s.nh * 32, xs, xsum, tc, 64 * kPC);
+      else stage_x<1, false>(p, s.gA, s.gA + s.ngs, s.nh * 32, xs, xsum, tc, 64 * kPC);
+      cbar();
+      const int nrp = s.nu * s.nrb * s.parts;
+      if (s.spread) {
+        // every compute lane takes pair tc = 16 group + row of each slot; a part's slots are its halves
+        const int gi = tc >> 4;
+        for (int rp = 0; rp < nrp; ++rp) {
+          float acc = 0.0f;
+          for (int h = 0; h < s.nh; ++h) {
+            const int q = q0 + rp * s.nh + h;
+            wait_slot(q);
+            const uint8_t* slot = lds + (q % kRing) * kSlotB;
+            const int g = 32 * h + gi;
+            const u32x4 qv = *(const u32x4l*)(slot + tc * 16);
+            const uint32_t sm = *(const uint32_t*)(slot + 8192 + tc * 4);
+            if (g < s.ngs) {
+              const float d = dot32(qv, xs + g * 32);
+              acc = __builtin_fmaf(h2f_lo(sm) * 16777216.0f, d, __builtin_fmaf(h2f_hi(sm), xsum[g], acc));
+            }
+          }
+          acc += __shfl_xor(acc, 16, 64);
+          acc += __shfl_xor(acc, 32, 64);
+          if (lane < 16) red[(rp * kPC + c) * 16 + lane] = acc;
+        }
+        cbar();   // every slot of the share is read, every wave's row sums are in
+        if (tc < s.nslot) __hip_atomic_fetch_add(ctl + kCtlRel + (q0 + tc) % kRing, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+        // epilogue: compute thread t -> row t of the share (a softcap unit is one whole wave)
+        const int rows = s.nu * s.nrb * kStageRows;
+        if (tc - lane < rows) {
+          const int t = min(tc, rows - 1);
+          const int j = t / (s.nrb * kStageRows), rr = t - j * (s.nrb * kStageRows);
+          const int rpg = (j * s.nrb + rr / kStageRows) * s.parts, r16 = rr & 15;
+          float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+          for (int w = 0; w < kPC; ++w) v0 += red[(rpg * kPC + w) * 16 + r16];
+          if (s.parts == 2) {
+#pragma unroll
+            for (int w = 0; w < kPC; ++w) v1 += red[((rpg + 1) * kPC + w) * 16 + r16];
+          }
+          const int n = share_row(p, s, G, j, 0, 0) + rr;
+          if (tc < rows) {
+            if (p.coh & 2) epilogue<true>(p, s.split, 0, n >> 6, n & 63, v0, v1);
+            else epilogue<false>(p, s.split, 0, n >> 6, n & 63, v0, v1);
+          }
+        }
+      } else {
+        // one wave per unit: lane takes pairs lane + 64 kk of each slot (group 4 kk + lane / 16, row lane % 16)
+        for (int j = c; j < s.nu; j += kPC) {
+          for (int r = 0; r < s.nrb; ++r) {
+            for (int pt = 0; pt < s.parts; ++pt) {
+              float acc = 0.0f;
+              for (int h = 0; h < s.nh; ++h) {
+                const int q = q0 + slot_index(s, j, (r * s.parts + pt) * s.nh + h);
+                wait_slot(q);
+                const uint8_t* slot = lds + (q % kRing) * kSlotB;
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk) {
+                  const int pp = kk * 64 + lane, g = 32 * h + (pp >> 4);
+                  const u32x4 qv = *(const u32x4l*)(slot + pp * 16);
+                  const uint32_t sm = *(const uint32_t*)(slot + 8192 + pp * 4);
+                  if (g < s.ngs) {
+                    const float d = dot32(qv, xs + g * 32);
+                    acc = __builtin_fmaf(h2f_lo(sm) * 16777216.0f, d, __builtin_fmaf(h2f_hi(sm), xsum[g], acc));
+                  }
+                }
+                __builtin_amdgcn_s_waitcnt(0xC07F);   // this wave's reads of the slot are done
+                if (lane == 0) __hip_atomic_fetch_add(ctl + kCtlRel + q % kRing, 1u, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_WORKGROUP);
+              }
+              acc += __shfl_xor(acc, 16, 64);
+              acc += __shfl_xor(acc, 32, 64);
+              if (lane < 16) wred[pt * 64 + r * 16 + lane] = acc;
+            }
+          }
+          __builtin_amdgcn_s_waitcnt(0xC07F);
+          __builtin_amdgcn_wave_barrier();
+          const int rows = s.nrb * kStageRows;   // 16, or 64 for a softcap unit (the whole wave)
+          const float v0 = wred[min(lane, rows - 1)], v1 = s.parts == 2 ? wred[64 + min(lane, rows - 1)] : 0.0f;
+          const int n = share_row(p, s, G, j, 0, 0) + lane;
+          if (lane < rows || p.epi == P0_EPI_SOFTCAP) {
+            if (p.coh & 2) epilogue<true>(p, s.split, 0, n >> 6, n & 63, v0, v1);
+            else epilogue<false>(p, s.split, 0, n >> 6, n & 63, v0, v1);
+          }
+          __builtin_amdgcn_s_waitcnt(0xC07F);
+          __builtin_amdgcn_wave_barrier();   // wred is rewritten by this wave's next unit
+        }
+      }
+      // every compute wave's output stores are acknowledged before the flag: no L2 writeback
+      __builtin_amdgcn_s_waitcnt(0);
+      cbar();
+    }
+    if (c == 0 && lane < kFlagCopies) st_coh(flags + ((size_t)lane * n_ops + i) * Gp + b, tag);
+    q0 += s.nslot;
+  }
+  if (abandon) return;
+  // every workgroup has read this run's tag once all have published op 0: store it back for the next run
+  if (b == 0 && wait_flags(flags + 0) && tc == 0) st_coh(st, tag);
+}
+
+chain_kernel_t pipe_chain_kernel() { return q4_chain_pipe_kernel; }
+
+}  // namespace p0

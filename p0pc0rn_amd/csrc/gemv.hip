@@ -109,7 +109,11 @@ static int g_chain_waves = 16;          // waves per chain workgroup for M = 1 (
 static int g_chain_split_gpw = 16;      // a wave share above this many groups splits K across workgroups
 static int g_chain_spin = 1 << 22;      // polls before a chain wait gives up (about 0.3 s)
 static int g_chain_force_give_up = 0;   // tests: every wait gives up at once
+static int g_chain_stage = 1;           // staged ops (weights copied to LDS before the wait) where they fit
+static int g_pipe_loaders = 2;          // pipelined chain: loader waves that stream
+static int g_pipe_depth = 2;            // pipelined chain: slots in flight per loader wave
 static constexpr size_t kChainLds = 64 * 1024;
+static constexpr size_t kChainLdsMax = 160 * 1024 - 256;   // gfx950: LDS per CU, less the kernel's static LDS
 
 struct ChainBuild {
   int M = 0, W = 0, G = 0;
@@ -118,6 +122,7 @@ struct ChainBuild {
   std::string error;   // the first failed append (reported again by p0_chain_end)
 };
 struct ChainExec {
+  int pipe_cfg[2];   // pipelined chains: loader waves, slots in flight per loader (0: another kernel)
   GemvP* ops;
   unsigned* st;
   size_t st_words;
@@ -199,6 +204,61 @@ static Plan plan_chain(int M, int NT, int epi, int nsplit, int kPer, int W, int 
   pl.nks = (Gs + gps - 1) / gps;
   pl.lds = (size_t)M * gps * 33 * sizeof(float) + red;
   return pl;
+}
+
+// Staged plan of a chain op (mode 3, staged_op in gemv_kernels.hpp) on G workgroups of W waves: units of 16 rows (64
+// for a softcap, whose tile maximum needs a whole tile; a geglu unit also holds the up rows) x one split, dealt to
+// workgroup positions from `cur` on. Returns the LDS bytes the op needs, or 0 (the op stays a streamed op) when a
+// workgroup's share does not fit the LDS, the weights are not 16-byte aligned (LDS-DMA loads), or a workgroup would
+// get units of two splits.
+static size_t plan_staged(GemvP& p, int M, int W, int G, int& cur) {
+  if ((uintptr_t)p.w & 15) return 0;
+  const int nrb = p.epi == P0_EPI_SOFTCAP ? 4 : 1, parts = p.epi == P0_EPI_GEGLU ? 2 : 1;
+  const int64_t U = (int64_t)(p.N / (kStageRows * nrb)) * p.nsplit;
+  if (U > G && G % p.nsplit) return 0;
+  const int numax = (int)((U + G - 1) / G);
+  const int ngp = (p.kPer / 32 + 15) / 16 * 16;
+  const int64_t nrp = (int64_t)numax * nrb * parts;
+  const size_t xs = (size_t)M * ngp * 33;                      // floats: x' and its group sums
+  const size_t red = (size_t)nrp * M * W * 16;                 // floats: the per-wave row sums
+  const size_t woff = ((xs + red) * sizeof(float) + 1023) & ~(size_t)1023;
+  const size_t need = woff + (size_t)nrp * ngp * 320;
+  if (need > kChainLdsMax) return 0;
+  p.mode = 3;
+  p.su = (int)U;
+  p.scur = cur;
+  p.snrb = nrb;
+  p.sngp = ngp;
+  p.sred = (int)xs;
+  p.swoff = (int)woff;
+  cur = (int)((cur + U) % G);
+  return need;
+}
+
+// Plan of an M = 1 chain for the pipelined kernel (chain_pipe.hip) on G workgroups: every op's rows are dealt as
+// units of 16 rows (64 for a softcap, a geglu unit with its up rows) x one split to workgroup positions, continuing
+// where the previous op stopped so each workgroup streams about the same bytes over a step. A share of at most a
+// ring's worth of slots (and few enough rows) is computed by all compute waves together, a larger one by one wave per
+// unit. Returns false (the chain then runs on q4_gemv_chain_kernel) when the weights are not 16-byte aligned
+// (LDS-DMA loads) or a workgroup would get units of two splits.
+static bool plan_pipe(std::vector<GemvP>& ops, int G) {
+  int cur = 0;
+  for (GemvP& p : ops) {
+    if ((uintptr_t)p.w & 15) return false;
+    const int nrb = p.epi == P0_EPI_SOFTCAP ? 4 : 1, parts = p.epi == P0_EPI_GEGLU ? 2 : 1;
+    const int64_t U = (int64_t)(p.N / (kStageRows * nrb)) * p.nsplit;
+    if (U > G && G % p.nsplit) return false;
+    const int64_t numax = (U + G - 1) / G;
+    const int nh = (p.kPer / 32 + 31) / 32;
+    const int64_t nrp = numax * nrb * parts;
+    const bool spread = nrp * nh <= pipe_ring_slots() && nrp <= pipe_spread_parts() && numax * nrb * kStageRows <= 512;
+    p.su = (int)U;
+    p.scur = cur;
+    p.snrb = nrb;
+    p.sngp = spread ? 1 : 0;
+    cur = (int)((cur + U) % G);
+  }
+  return true;
 }
 
 static int launch(GemvP& p, int M, const char* op) {
@@ -383,14 +443,63 @@ extern "C" int p0_chain_end(void** out) {
   int grid = ctx().cu_count * per_cu;
   if (grid > cb->G) grid = cb->G;   // the plans were made for G workgroups; never more than are resident
   if (grid > kChainMaxGrid) grid = kChainMaxGrid;
+  size_t lds = cb->lds;
+  if (g_chain_stage && cb->M != 1) {
+    // staged ops are dealt over exactly `grid` workgroups, so the grid must stay resident with their LDS: plan, check
+    // the occupancy, and plan again on a smaller grid if it shrank
+    std::vector<GemvP> staged;
+    for (int pass = 0; pass < 3; ++pass) {
+      staged = cb->ops;
+      int cur = 0;
+      size_t need = 0;
+      for (GemvP& p : staged) {
+        const size_t b = plan_staged(p, cb->M, cb->W, grid, cur);
+        if (b > need) need = b;
+      }
+      if (need == 0) break;
+      const size_t tot = need > cb->lds ? need : cb->lds;
+      P0_HIP(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kChainLdsMax),
+             "p0_chain_end");
+      int pc = 0;
+      P0_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, (const void*)k, 64 * cb->W, tot), "p0_chain_end");
+      if (pc >= 1 && ctx().cu_count * pc >= grid) {
+        cb->ops = staged;
+        lds = tot;
+        break;
+      }
+      if (pc < 1) break;
+      grid = ctx().cu_count * pc;
+    }
+  }
+  // M = 1: the pipelined kernel, one workgroup per CU, when every op can be planned for it
+  if (cb->M == 1 && g_chain_stage) {
+    chain_kernel_t pk = pipe_chain_kernel();
+    P0_HIP(hipFuncSetAttribute((const void*)pk, hipFuncAttributeMaxDynamicSharedMemorySize, pipe_lds_bytes()),
+           "p0_chain_end");
+    int pc = 0;
+    P0_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, (const void*)pk, 64 * pipe_waves(), pipe_lds_bytes()),
+           "p0_chain_end");
+    std::vector<GemvP> planned = cb->ops;
+    if (pc >= 1 && plan_pipe(planned, ctx().cu_count)) {
+      cb->ops = planned;
+      k = pk;
+      cb->W = pipe_waves();
+      grid = ctx().cu_count;
+      lds = pipe_lds_bytes();
+    }
+  }
   mark_coherence(cb->ops, cb->M);
   auto* ex = new ChainExec{};
   ex->n_ops = (int)cb->ops.size();
   ex->M = cb->M;
   ex->W = cb->W;
   ex->grid = grid;
-  ex->lds = cb->lds;
+  ex->lds = lds;
   ex->kernel = k;
+  if (k == pipe_chain_kernel()) {
+    ex->pipe_cfg[0] = g_pipe_loaders;
+    ex->pipe_cfg[1] = g_pipe_depth;
+  }
   // chain state: last tag, timed out, the workgroups' lines and the completion counters (one 128-byte line each)
   const size_t words = chain_state_words((int)cb->ops.size(), grid);
   const size_t ob = cb->ops.size() * sizeof(GemvP), sb = words * sizeof(unsigned);
@@ -399,6 +508,8 @@ extern "C" int p0_chain_end(void** out) {
   if (e == hipSuccess) e = hipMalloc((void**)&ex->st, sb);
   if (e == hipSuccess) e = hipMemcpy(ex->ops, cb->ops.data(), ob, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemset(ex->st, 0, sb);
+  if (e == hipSuccess && ex->pipe_cfg[0])
+    e = hipMemcpy(ex->st + pipe_cfg_word(), ex->pipe_cfg, sizeof ex->pipe_cfg, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
     hipFree(ex->ops);
     hipFree(ex->st);
@@ -430,6 +541,9 @@ extern "C" int p0_chain_status(void* chain, int32_t* timed_out) {
   if (v) {
     // an abandoned run can leave split-K arrival counters mid-way: clear them, and the chain state with them
     P0_HIP(hipMemset(ex->st, 0, ex->st_words * sizeof(unsigned)), "p0_chain_status");
+    if (ex->pipe_cfg[0])
+      P0_HIP(hipMemcpy(ex->st + pipe_cfg_word(), ex->pipe_cfg, sizeof ex->pipe_cfg, hipMemcpyHostToDevice),
+             "p0_chain_status");
     P0_HIP(hipMemset(ctx().counters, 0, ctx().n_counters * sizeof(unsigned)), "p0_chain_status");
     P0_HIP(hipDeviceSynchronize(), "p0_chain_status");
   }
@@ -459,12 +573,23 @@ extern "C" int p0_chain_free(void* chain) {
 }
 
 // chain knobs: 0 = waves per workgroup for M = 1 (8 or 16), 1 = largest wave share (groups) before K is split
-// across workgroups, 2 = polls before a wait gives up, 3 = 1: every wait gives up at once (tests). Returns the
-// previous value; a value < 0 only reads (knob 3 also takes 0).
+// across workgroups, 2 = polls before a wait gives up, 3 = 1: every wait gives up at once (tests), 4 = staged ops
+// (1, the default) or none (0). Returns the previous value; a value < 0 only reads (knobs 3 and 4 also take 0).
 extern "C" int p0_chain_tune(int knob, int value) {
   if (knob == 3) {
     const int old = g_chain_force_give_up;
     if (value >= 0) g_chain_force_give_up = value ? 1 : 0;
+    return old;
+  }
+  if (knob == 4) {
+    const int old = g_chain_stage;
+    if (value >= 0) g_chain_stage = value ? 1 : 0;
+    return old;
+  }
+  if (knob == 5 || knob == 6) {
+    int* t = knob == 5 ? &g_pipe_loaders : &g_pipe_depth;
+    const int old = *t;
+    if (value > 0) *t = knob == 5 ? (value > 4 ? 4 : value) : (value >= 2 ? 2 : 1);
     return old;
   }
   int* t = knob == 0 ? &g_chain_waves : knob == 1 ? &g_chain_split_gpw : knob == 2 ? &g_chain_spin : nullptr;

@@ -30,6 +30,7 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 // 4-byte alignment is all a record base guarantees (weight offsets are multiples of 4, engine/llm/lops.js:124);
 // global_load_dwordx4 needs only dword alignment, so one 16-byte load per lane serves both cases
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x4l __attribute__((ext_vector_type(4)));   // 16-byte aligned (LDS)
 // Global-memory view of a pointer. Pointers read from memory (a chain's op table) are generic to the compiler, which
 // then emits flat instructions; flat loads also count on the LDS wait counter, so every LDS wait would wait for the
 // weight stream too. The cast makes them global loads / stores / atomics again.
@@ -59,6 +60,11 @@ struct GemvP {
   // 1 = write the outputs with device-coherent stores (a later op reads them, or another op writes the same lines)
   int coh;
   float* part; unsigned* cnt;
+  // staged chain ops (mode 3, q4_gemv_chain_kernel): the op's rows are dealt as units of 16 snrb rows (a geglu's unit
+  // also holds the matching up rows) x one split, unit u to workgroup position (scur + u) mod grid
+  int su, scur, snrb, sngp;   // units, first position, 16-row blocks per unit, groups per split rounded up to 16
+  int sred;                   // LDS float offset of the reduction area (after x' and its group sums)
+  int swoff;                  // LDS byte offset of the staged weights
 };
 
 __device__ __forceinline__ float gelu_tanh(float v) {   // engine/llm/lops.js:26
@@ -152,6 +158,41 @@ __device__ __forceinline__ float sum32(float v) {
   v += dpp_f<0x141>(v);   // row_half_mirror
   v += dpp_f<0x140>(v);   // row_mirror
   return v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));   // lane ^ 16
+}
+
+// x'[m][k] of the groups [g0, g1) -> LDS xs[m * 32 gps + k - 32 g0] (odd k scaled 1/16), and the per-group sums of
+// x' -> xsum[m * gps + group - g0]; entries of the gps groups past g1 are zero. Thread tid takes elements u * blockDim +
+// tid of each batch of U: the 32 lanes of a 32-aligned lane group hold one group's 32 k (the slice length and the
+// block size are multiples of 32), which they sum with cross-lane adds. Every thread runs the same number of
+// batches, so all lanes take part in the cross-lane adds.
+// tid / nt: the calling thread's index among the nt threads that stage (whole waves; every one of them calls).
+template <int M, bool COH>
+__device__ __forceinline__ void stage_x(const GemvP& p, int g0, int g1, int gps, float* xs, float* xsum,
+                                        int tid = threadIdx.x, int nt = blockDim.x) {
+  constexpr int U = M == 1 ? 4 : 8;
+  const int lane = tid & 63, wv = tid >> 6;
+  const int KL = gps * 32, kb = g0 * 32, ke = g1 * 32, nx = M * KL;
+  for (int i0 = 0; i0 < nx; i0 += U * nt) {
+    int mm[U], kl[U];
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int idx = i0 + u * nt + tid;
+      mm[u] = M == 1 ? 0 : min(idx / KL, M - 1);
+      kl[u] = idx - mm[u] * KL;   // >= KL (so past ke) for idx >= nx
+    }
+    // batches of this wave that hold elements (u * nt + the wave's first thread < nx - i0)
+    const int nu = ke > kb ? min(U, max(0, (nx - i0 - (wv << 6) + nt - 1) / nt)) : 0;
+    prologue_batch<COH, U, M>(p, nu, mm, kb, ke, kl, v);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float gs = sum32(v[u]);
+      if (i0 + u * nt + tid < nx) {
+        xs[mm[u] * KL + kl[u]] = (kl[u] & 1) ? v[u] * 0.0625f : v[u];   // kb is even: k and kl share parity
+        if ((lane & 31) == 0) xsum[mm[u] * gps + (kl[u] >> 5)] = gs;
+      }
+    }
+  }
 }
 
 struct Rec {
@@ -302,36 +343,9 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
   }
   if (!ready()) return false;
 
-  // ---- prologue: x'[m][k] for the workgroup's K-slice -> LDS (odd k scaled 1/16), and the per-group sums of x'.
-  // Thread tid takes elements u * blockDim + tid of each batch of U: the 32 lanes of a 32-aligned lane group hold one
-  // group's 32 k (KL and the block size are multiples of 32), which they sum with cross-lane adds. Every thread runs
-  // the same number of batches, so all lanes take part in the cross-lane adds.
-  {
-    constexpr int U = M == 1 ? 4 : 8;
-    const int kb = g0 * 32, ke = g1 * 32, nx = M * KL, nt = blockDim.x;
-    for (int i0 = 0; i0 < nx; i0 += U * nt) {
-      int mm[U], kl[U];
-      float v[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int idx = i0 + u * nt + tid;
-        mm[u] = M == 1 ? 0 : min(idx / KL, M - 1);
-        kl[u] = idx - mm[u] * KL;   // >= KL (so past ke) for idx >= nx
-      }
-      // batches of this wave that hold elements (u * nt + the wave's first thread < nx - i0)
-      const int nu = ke > kb ? min(U, max(0, (nx - i0 - (wv << 6) + nt - 1) / nt)) : 0;
-      if (coh_in) prologue_batch<true, U, M>(p, nu, mm, kb, ke, kl, v);
-      else prologue_batch<false, U, M>(p, nu, mm, kb, ke, kl, v);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const float gs = sum32(v[u]);
-        if (i0 + u * nt + tid < nx) {
-          xs[mm[u] * KL + kl[u]] = (kl[u] & 1) ? v[u] * 0.0625f : v[u];   // kb is even: k and kl share parity
-          if ((lane & 31) == 0) xsum[mm[u] * p.gps + (kl[u] >> 5)] = gs;
-        }
-      }
-    }
-  }
+  // ---- prologue: x'[m][k] for the workgroup's K-slice -> LDS (odd k scaled 1/16), and the per-group sums of x'
+  if (coh_in) stage_x<M, true>(p, g0, g1, p.gps, xs, xsum);
+  else stage_x<M, false>(p, g0, g1, p.gps, xs, xsum);
   __syncthreads();
 
   // ---- stream the records of the wave's share
@@ -477,6 +491,130 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
   return true;
 }
 
+// ---- staged chain ops (mode 3). A workgroup's share of the op is a few units of 16-row blocks; it copies their
+// records into LDS with LDS-DMA loads (global_load_lds_dwordx4: no registers, no ALU) BEFORE it waits for the
+// producing op, so the weights stream while the chain's previous op finishes, and after the wait only x' is read
+// from memory. Every unit holds whole rows of one split, so no partial sum leaves the workgroup.
+//
+// LDS per 16-row part (16 rows of one weight tile, the split's groups, padded to ngp, a multiple of 16):
+//   codes  [ngp][16 rows][16 B] (ngp 256 B)  then  scale/min  [ngp][16 rows][4 B] (ngp 64 B)
+// One 1-KB DMA instruction moves the codes of 4 groups (lane l: group 4 i + l / 16, row l % 16) or the scale words of
+// 16 groups (lane l: group 16 j + l / 4, rows 4 (l % 4) .. + 3). The arithmetic maps thread t to the (group, row)
+// pairs t, t + 64 W, ... of a part (pair p = group 16 + row, so a row's lanes sit 16 apart): dot32 against the
+// group's x', scaled, summed over the wave's 4 groups with two cross-lane adds, then over the waves in wave order.
+constexpr int kStageRows = 16;
+
+// position of workgroup b in the dealing order: consecutive positions on one XCD (workgroups are dispatched to the 8
+// XCDs round-robin), so units that share records' cache lines share an L2
+__device__ __forceinline__ int stage_pos(int b, int G) { return (G & 7) ? b : (b & 7) * (G >> 3) + (b >> 3); }
+
+template <int M, int W, class Ready>
+__device__ __forceinline__ void staged_op(const GemvP& p, int b, int G, float* smem, Ready&& ready) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int pos = stage_pos(b, G);
+  const int first = pos >= p.scur ? pos - p.scur : pos - p.scur + G;   // this workgroup's first unit
+  if (first >= p.su) return;
+  const int nu = (p.su - first + G - 1) / G;
+  const int parts = p.epi == P0_EPI_GEGLU ? 2 : 1, nrb = p.snrb, ngp = p.sngp;
+  const int nrp = nu * nrb * parts;
+  // every unit of a workgroup has the same split (the host deals split-minor units only when the split count
+  // divides the grid)
+  const int split = first % p.nsplit;
+  const int gA = split * (p.kPer >> 5);
+  const int ngs = (min(p.K, (split + 1) * p.kPer) >> 5) - gA;
+  const int RPB = ngp * 320, IPR = ngp / 4 + ngp / 16;
+  uint8_t* const wl = (uint8_t*)smem + p.swoff;
+  float* const xs = smem;                  // [M][32 ngp]
+  float* const xsum = smem + M * ngp * 32; // [M][ngp]
+  float* const red = smem + p.sred;        // [nrp][M][W][16]
+
+  // rows of part rp: unit j = rp / (nrb parts), block r, part (0 gate / plain, 1 up)
+  auto part_row = [&](int rp) -> int {
+    const int j = rp / (nrb * parts), rem = rp - j * (nrb * parts), r = rem / parts, pt = rem - r * parts;
+    const int rb = (first + j * G) / p.nsplit;
+    return (rb * nrb + r) * kStageRows + (pt ? p.N : 0);
+  };
+
+  __syncthreads();   // the previous op of this workgroup is done with the LDS
+  for (int k = wv; k < nrp * IPR; k += W) {
+    const int rp = k / IPR, i = k - rp * IPR;
+    const int n = part_row(rp);
+    const uint8_t* tb = p.w + ((int64_t)(n >> 6) * p.wG + gA) * 1280;
+    const int r0 = n & 63;
+    const uint8_t* src;
+    uint8_t* dst;
+    if (i < ngp / 4) {
+      const int gi = min(4 * i + (lane >> 4), ngs - 1);   // padding groups re-read the last group (in bounds)
+      src = tb + (int64_t)gi * 1280 + (r0 + (lane & 15)) * 16;
+      dst = wl + rp * RPB + i * 1024;
+    } else {
+      const int j = i - ngp / 4;
+      const int gi = min(16 * j + (lane >> 2), ngs - 1);
+      src = tb + (int64_t)gi * 1280 + 1024 + (r0 + 4 * (lane & 3)) * 4;
+      dst = wl + rp * RPB + ngp * 256 + j * 1024;
+    }
+    __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+  }
+  if (!ready()) return;
+  if (p.coh & 1) stage_x<M, true>(p, gA, gA + ngs, ngp, xs, xsum);
+  else stage_x<M, false>(p, gA, gA + ngs, ngp, xs, xsum);
+  __builtin_amdgcn_s_waitcnt(0);   // this wave's DMA loads have landed in LDS
+  __syncthreads();
+
+  const int npairs = ngs * kStageRows;
+  for (int rp = 0; rp < nrp; ++rp) {
+    const uint8_t* cb = wl + rp * RPB;
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+    for (int pp = tid; pp < npairs; pp += 64 * W) {
+      const u32x4 q = *(const u32x4l*)(cb + pp * 16);
+      const uint32_t sm = *(const uint32_t*)(cb + ngp * 256 + pp * 4);
+      const int gi = pp >> 4;
+      const float s24 = h2f_lo(sm) * 16777216.0f, mn = h2f_hi(sm);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float d = dot32(q, xs + m * ngp * 32 + gi * 32);
+        acc[m] = __builtin_fmaf(s24, d, __builtin_fmaf(mn, xsum[m * ngp + gi], acc[m]));
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float v = acc[m];
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      if (lane < 16) red[((rp * M + m) * W + wv) * 16 + lane] = v;
+    }
+  }
+  __syncthreads();
+
+  // epilogue: thread t -> row t of the workgroup's share (a whole 64-row tile per wave for a softcap unit)
+  const int rows = nu * nrb * kStageRows;
+  for (int t0 = 0; t0 < rows; t0 += 64 * W) {
+    const int t = t0 + tid;
+    if (t0 + (tid & ~63) >= rows) break;   // whole waves leave together (softcap's wave argmax needs all 64 lanes)
+    const int tt = min(t, rows - 1);
+    const int j = tt / (nrb * kStageRows), rr = tt - j * (nrb * kStageRows);
+    const int rpg = (j * nrb + rr / kStageRows) * parts, r16 = rr & 15;
+    const int n = (first + j * G) / p.nsplit * nrb * kStageRows + rr;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) v0 += red[((rpg * M + m) * W + w) * 16 + r16];
+      if (parts == 2) {
+#pragma unroll
+        for (int w = 0; w < W; ++w) v1 += red[(((rpg + 1) * M + m) * W + w) * 16 + r16];
+      }
+      if (t < rows) {
+        if (p.coh & 2) epilogue<true>(p, split, m, n >> 6, n & 63, v0, v1);
+        else epilogue<false>(p, split, m, n >> 6, n & 63, v0, v1);
+      }
+    }
+  }
+}
+
 // One op, one launch: grid (tile blocks, splits x K-slices). Up to 16 waves per workgroup for M <= 2; 8 for larger
 // M, whose accumulators need the registers (128 VGPRs per lane at 16 waves would spill).
 template <int M, int MODE>
@@ -494,20 +632,20 @@ __global__ __launch_bounds__(M <= 2 ? 1024 : 512) void q4_gemv_kernel(GemvP p) {
 // is also bounded: past `spin_limit` polls it sets the timed-out word, and every workgroup abandons the rest of the
 // chain at its next wait, so a launch always finishes (its results are then invalid and reported as such).
 //
-// Completion travels in three hops, each free of contention on one address:
-//  1. a workgroup done with its items of op i (or with none) adds 1 to its group's counter (16 workgroups a group);
-//  2. the add that completes a group adds 1 to the op's counter (one add per group);
-//  3. the add that completes the op writes tag << 16 | (i + 1) into every workgroup's own 128-byte line, 64 lanes at
-//     once; a waiter polls only its own line with one load. (Measured on MI355X with 256 workgroups: 1.3 us from the
-//     last producer's signal to a waiter's sight of it, against 2.9 us when every waiter polls every producer's flag.)
-// Counters reset themselves (the completing add clears them). The tag is the last run's tag + 1, read from the state at
-// the start; the add completing the last op stores it back, so a chain runs any number of times with no reset
-// (capturable).
-// State, one 128-byte line per word (kCtrStride words): [0] last tag, [1] timed out (sticky until p0_chain_status
-// reads and resets it; runs started meanwhile do nothing), then G workgroup lines, then for each op its group
-// counters followed by its op counter.
+// Completion is published per workgroup: a workgroup done with its units or items of op i (or with none) waits
+// until its output stores are acknowledged, then writes the run's tag into its flag of op i. A workgroup about to
+// read op i - 1's outputs polls op i - 1's flags of all workgroups: one wave loads them (G 4-byte words, one coalesced
+// load per lane per 64 workgroups) and votes. No atomic sits on the path, and no workgroup waits for another's
+// signal to be relayed. The flags exist in kFlagCopies copies, one per XCD, every producer writing each copy: a
+// waiter polls the copy of its own XCD (workgroup b runs on XCD b % 8), so each copy's lines serve 32 pollers
+// instead of 256.
+// The tag is the last run's tag + 1, read from the state at the start; workgroup 0 stores it back once every
+// workgroup has published op 0 (so has read it), so a chain runs any number of times with no reset (capturable).
+// State (u32 words): [0] last tag, [kCtrStride] timed out (sticky until p0_chain_status reads and resets it; runs
+// started meanwhile do nothing), then from word 2 kCtrStride the flags, (copy c, op i, workgroup w) at
+// (c n_ops + i) Gp + w with Gp = G rounded up to whole 256-byte lines.
 constexpr int kCtrStride = 32;
-constexpr int kFinGroup = 16;
+constexpr int kFlagCopies = 8;
 constexpr int kChainMaxGrid = 512;
 
 __device__ __forceinline__ unsigned ld_coh(const unsigned* a) {
@@ -516,13 +654,24 @@ __device__ __forceinline__ unsigned ld_coh(const unsigned* a) {
 __device__ __forceinline__ void st_coh(unsigned* a, unsigned v) {
   __hip_atomic_store(P0_GLOBAL(unsigned, a), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ unsigned add_coh(unsigned* a, unsigned v) {
-  return __hip_atomic_fetch_add(P0_GLOBAL(unsigned, a), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
+__host__ __device__ constexpr int chain_flag_stride(int G) { return (G + 63) & ~63; }
 // words of chain state for n_ops ops on G workgroups
 __host__ __device__ constexpr size_t chain_state_words(int n_ops, int G) {
-  return ((size_t)2 + G + (size_t)n_ops * ((G + kFinGroup - 1) / kFinGroup + 1)) * kCtrStride;
+  return (size_t)2 * kCtrStride + (size_t)kFlagCopies * n_ops * chain_flag_stride(G);
+}
+
+// true once every one of the G flags at f holds tag: one wave, four loads per lane issued before any is compared
+__device__ __forceinline__ bool flags_set(const unsigned* f, int G, unsigned tag, int lane) {
+  bool ok = true;
+  for (int j0 = 0; j0 < G; j0 += 256) {
+    unsigned v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = ld_coh(f + min(j0 + j * 64 + lane, G - 1));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ok = ok && v[j] == tag;
+  }
+  return __builtin_amdgcn_ballot_w64(!ok) == 0;
 }
 
 template <int M, int W>
@@ -532,72 +681,66 @@ __global__ __launch_bounds__(64 * W) void q4_gemv_chain_kernel(const GemvP* __re
   __shared__ int s_last, s_go;
   __shared__ unsigned s_tag;
   const int tid = threadIdx.x, lane = tid & 63, G = gridDim.x, b = blockIdx.x;
-  const int nsub = (G + kFinGroup - 1) / kFinGroup;
+  const int Gp = chain_flag_stride(G);
   unsigned* const timed_out = st + kCtrStride;
-  unsigned* const box = st + 2 * kCtrStride;                  // workgroup w's line: box + w * kCtrStride
-  unsigned* const ctrs = st + (2 + (size_t)G) * kCtrStride;   // op i: nsub group counters, then the op counter
+  unsigned* const flags = st + 2 * kCtrStride;
+  const unsigned* const mine = flags + (size_t)(b % kFlagCopies) * n_ops * Gp;   // this XCD's copy
   if (tid == 0) {
     s_tag = ld_coh(st) + 1;
     s_go = ld_coh(timed_out) == 0u;   // an earlier run gave up: do nothing until p0_chain_status resets the state
   }
   __syncthreads();
   const unsigned tag = s_tag;
-  bool abandon = s_go == 0;
+  const bool started = s_go != 0;
+  bool abandon = !started;
+  // wave 0 waits until the G flags at f hold this run's tag; false (in every thread) when the wait gave up
+  auto wait_flags = [&](const unsigned* f) -> bool {
+    if (tid < 64) {
+      // spin_limit < 0: the host asks every wait to give up at once (tests of the timed-out path)
+      int go = spin_limit >= 0;
+      for (int spins = 0; go && !flags_set(f, G, tag, lane); ++spins) {
+        if (spins >= spin_limit || (spins % 64 == 63 && ld_coh(timed_out))) go = 0;
+        else __builtin_amdgcn_s_sleep(1);
+      }
+      if (lane == 0) {
+        if (!go) atomicOr(timed_out, 1u);
+        s_go = go;
+      }
+    }
+    __syncthreads();
+    return s_go != 0;
+  };
   for (int i = 0; i < n_ops && !abandon; ++i) {
     const GemvP& p = ops[i];
-    const int items = p.ntb * p.nsplit * p.nks;
     bool waited = i == 0;
-    for (int it = b; it < items; it += G) {
-      const int bx = it % p.ntb, by = it / p.ntb;
-      auto ready = [&]() -> bool {
-        if (waited) return true;   // only the workgroup's first item of op i waits for op i - 1
-        if (tid == 0) {
-          const unsigned want = (tag << 16) | (unsigned)i;   // op i - 1 complete
-          // spin_limit < 0: the host asks every wait to give up at once (tests of the timed-out path)
-          int go = spin_limit >= 0;
-          for (int spins = 0; go && ld_coh(box + (size_t)b * kCtrStride) != want; ++spins) {
-            if (spins >= spin_limit || (spins % 64 == 63 && ld_coh(timed_out))) go = 0;
-            else __builtin_amdgcn_s_sleep(1);
-          }
-          if (!go) atomicOr(timed_out, 1u);
-          s_go = go;   // op i - 1's outputs are read with coherent loads: no L2 invalidate
-        }
-        __syncthreads();
-        waited = true;
-        abandon = s_go == 0;
-        return !abandon;
-      };
-      if (p.mode == 0) gemv_item<M, 0, true>(p, bx, by, smem, &s_last, ready);
-      else if (p.mode == 1) gemv_item<M, 1, true>(p, bx, by, smem, &s_last, ready);
-      else gemv_item<M, 2, true>(p, bx, by, smem, &s_last, ready);
-      if (abandon) break;
+    auto ready = [&]() -> bool {
+      if (waited) return true;   // only the workgroup's first item of op i waits for op i - 1
+      // op i - 1's outputs are read with coherent loads: no L2 invalidate
+      abandon = !wait_flags(mine + (size_t)(i - 1) * Gp);
+      waited = true;
+      return !abandon;
+    };
+    if (p.mode == 3) {
+      staged_op<M, W>(p, b, G, smem, ready);
+    } else {
+      const int items = p.ntb * p.nsplit * p.nks;
+      for (int it = b; it < items; it += G) {
+        const int bx = it % p.ntb, by = it / p.ntb;
+        if (p.mode == 0) gemv_item<M, 0, true>(p, bx, by, smem, &s_last, ready);
+        else if (p.mode == 1) gemv_item<M, 1, true>(p, bx, by, smem, &s_last, ready);
+        else gemv_item<M, 2, true>(p, bx, by, smem, &s_last, ready);
+        if (abandon) break;
+      }
     }
     if (abandon) break;
-    // every wave's coherent output stores are complete (acknowledged) before the signal: no L2 writeback
+    // every wave's coherent output stores are complete (acknowledged) before the flag: no L2 writeback
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (tid < 64) {
-      unsigned last = 0;
-      if (lane == 0) {
-        const int grp = b / kFinGroup;
-        const unsigned gsize = (unsigned)min(kFinGroup, G - grp * kFinGroup);
-        unsigned* gc = ctrs + ((size_t)i * (nsub + 1) + grp) * kCtrStride;
-        if (add_coh(gc, 1u) == gsize - 1) {
-          st_coh(gc, 0u);   // every add of this group is in: reset for the next run
-          unsigned* oc = ctrs + ((size_t)i * (nsub + 1) + nsub) * kCtrStride;
-          if (add_coh(oc, 1u) == (unsigned)nsub - 1) {
-            st_coh(oc, 0u);
-            last = 1;
-          }
-        }
-      }
-      if (__builtin_amdgcn_readfirstlane(last)) {   // op i is complete: tell every workgroup
-        const unsigned v = (tag << 16) | (unsigned)(i + 1);
-        for (int w = lane; w < G; w += 64) st_coh(box + (size_t)w * kCtrStride, v);
-        if (i == n_ops - 1 && lane == 0) st_coh(st, tag);   // every workgroup has read this run's tag
-      }
-    }
+    if (tid < kFlagCopies) st_coh(flags + ((size_t)tid * n_ops + i) * Gp + b, tag);
   }
+  // every workgroup has read this run's tag once all have published op 0: store it back for the next run
+  if (b == 0 && !abandon && wait_flags(flags + 0) && tid == 0) st_coh(st, tag);
+  __builtin_amdgcn_s_waitcnt(0);   // an abandoned staged op may still have LDS-DMA loads in flight
 }
 
 // ---- kernel tables: each M's kernels are instantiated in one of the gemv_m*.hip units (parallel compilation)
@@ -616,6 +759,14 @@ chain_kernel_t pick_chain_m(int W) {   // 16-wave chain workgroups for M = 1, 8-
   if (M == 1 && W == 16) return q4_gemv_chain_kernel<M, (M == 1 ? 16 : 8)>;
   return q4_gemv_chain_kernel<M, 8>;
 }
+
+// the pipelined M = 1 chain (chain_pipe.hip): its kernel and its fixed shape
+chain_kernel_t pipe_chain_kernel();
+int pipe_lds_bytes();
+int pipe_waves();
+int pipe_ring_slots();
+int pipe_spread_parts();
+int pipe_cfg_word();   // state word of the loader count (the next word: slots in flight per loader)
 
 #define P0_GEMV_EXTERN(M) \
   extern template gemv_kernel_t pick_m<M>(int); \

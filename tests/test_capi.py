@@ -146,3 +146,7 @@ def test_chain_tune_knobs_round_trip():
     assert capi.chain_tune(0, 16) == 8 and capi.chain_tune(0, -1) == 16
     capi.chain_tune(0, old)
     assert capi.chain_tune(3, -1) == 0 and capi.chain_tune(9, 1) == -1
+    assert capi.chain_tune(4, -1) == 1 and capi.chain_tune(4, 0) == 1 and capi.chain_tune(4, -1) == 0
+    assert capi.chain_tune(4, 1) == 0 and capi.chain_tune(4, -1) == 1
+    assert capi.chain_tune(5, -1) == 2 and capi.chain_tune(5, 9) == 2 and capi.chain_tune(5, 2) == 4
+    assert capi.chain_tune(6, -1) == 2 and capi.chain_tune(6, 1) == 2 and capi.chain_tune(6, 2) == 1

@@ -235,21 +235,23 @@ def test_chain_layers_reuse_buffers(dev):
         buf.free()
 
 
-@pytest.mark.parametrize("knob,value", [(0, 8), (1, 2)])
-def test_chain_other_plans(dev, knob, value):
-    """8-wave workgroups; and K split across workgroups inside the chain (cross-workgroup reduction + counts)"""
-    old = capi.chain_tune(knob, value)
+@pytest.mark.parametrize("knobs", [{0: 8}, {4: 0}, {1: 2, 4: 0}, {0: 8, 4: 0}])
+def test_chain_other_plans(dev, knobs):
+    """8-wave workgroups; every op streamed (no LDS staging); and streamed ops with K split across workgroups inside
+    the chain (cross-workgroup reduction + counts)"""
+    old = {k: capi.chain_tune(k, v) for k, v in knobs.items()}
     try:
-        s = MiniStep(seed=41 + knob)
+        s = MiniStep(seed=41 + sum(knobs))
         ch = s.make_chain()
     finally:
-        capi.chain_tune(knob, old)
+        for k, v in old.items():
+            capi.chain_tune(k, v)
     print("chain", ch.info(), flush=True)
     for _ in range(2):
         s.reset_outputs()
         ch.run()
         assert not ch.status()
-        s.check_against_oracle(s.read(), f"chain knob {knob}={value}")
+        s.check_against_oracle(s.read(), f"chain knobs {knobs}")
     ch.free()
     s.free()
 
