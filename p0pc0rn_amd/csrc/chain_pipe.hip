@@ -20,9 +20,9 @@
 // Work split. Every op is cut into units of 16 rows (64 for a softcap, whose tile maximum needs a whole 64-row tile;
 // a geglu unit also holds the matching up rows) x one split (kPer); unit u goes to workgroup position
 // (scur + u) mod G (consecutive positions on one XCD). A slot is 16 rows x 32 groups of one unit (10 KB): the rows'
-// codes [32 groups][16 rows][16 B] then their scale words [32][16][4 B]. Small shares (a few slots) are computed by
-// all 8 compute waves together, one (group, row) pair per lane per slot; large shares (the lm_head) by one wave per
-// unit, each lane taking 8 pairs per slot, so the waves stream independently.
+// codes [32 groups][16 rows][16 B] then their scale words [32][16][4 B]. A small share (at most a ring of slots) is
+// computed by all 8 compute waves together, one (group, row) pair per lane per slot, and reduced once; a large one
+// (the lm_head) by one wave per unit, each lane taking 8 pairs per slot, so the waves stream independently.
 #include "gemv_kernels.hpp"
 
 namespace p0 {
@@ -68,6 +68,15 @@ __device__ __forceinline__ void asm_lds_st(unsigned a, unsigned v) {
   asm volatile("ds_write_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : : "v"(a), "v"(v) : "memory");
 }
 
+// The compute waves' control words, through an LDS-typed pointer: a volatile access through a generic pointer
+// compiles to a flat load, which also waits for every outstanding global access of the wave (vmcnt(0)).
+typedef __attribute__((address_space(3))) unsigned lds_u32;
+__device__ __forceinline__ unsigned ctl_ld(lds_u32* a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+__device__ __forceinline__ void ctl_st(lds_u32* a, unsigned v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+__device__ __forceinline__ void ctl_add(lds_u32* a, unsigned v) {
+  __hip_atomic_fetch_add(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 // a workgroup's share of one op
 struct Share {
   int nu, first, nrb, parts, nh, ngs, split, gA, nslot, spread;
@@ -84,20 +93,20 @@ __device__ __forceinline__ Share share_of(const GemvP& p, int b, int G) {
   s.ngs = (min(p.K, (s.split + 1) * p.kPer) >> 5) - s.gA;
   s.nh = (s.ngs + 31) >> 5;
   s.nslot = s.nu * s.nrb * s.parts * s.nh;
-  s.spread = p.sngp;   // the host's choice: 1 = all compute waves on every slot, 0 = one wave per unit
+  s.spread = p.sngp;   // the host's choice: 1 = all compute waves on every slot (the share fits the ring), 0 = a wave per unit
   return s;
 }
-// Slot order of a share. Spread shares: unit-major, then block, part, half. Per-wave shares: units in rounds of kPC
-// (unit j = kPC R + c goes to compute wave c), and inside a round the waves' slots interleave (slot s of every unit,
-// then slot s + 1, ...), so the ring's consecutive slots feed all waves at once.
+// Slot order of a share. Small shares: unit-major, then block, part, half. Large shares: units in rounds of kPC (unit
+// j = kPC R + c goes to compute wave c), and inside a round the waves' slots interleave (slot s of every unit, then
+// slot s + 1, ...), so the ring's consecutive slots feed all waves at once.
 __device__ __forceinline__ void slot_of(const Share& s, int k, int& j, int& si) {
+  const int S = s.nrb * s.parts * s.nh;
   if (s.spread) {
-    const int S = s.nrb * s.parts * s.nh;
     j = k / S;
     si = k - j * S;
     return;
   }
-  const int S = s.nrb * s.parts * s.nh, R = min(k / (kPC * S), (s.nu - 1) / kPC);
+  const int R = min(k / (kPC * S), (s.nu - 1) / kPC);
   const int nw = min(kPC, s.nu - kPC * R), kr = k - R * kPC * S;
   si = kr / nw;
   j = kPC * R + (kr - si * nw);
@@ -134,16 +143,27 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
 
   if (wv < kPL) {
     // ------------------------------------------------------------------ loader waves
-    // st[kCfgLoaders]: loader waves that stream (1 .. kPL), st[kCfgDepth]: slots in flight per loader (1 or 2)
-    const int nl = min(kPL, max(1, (int)st[kCfgLoaders])), depth2 = st[kCfgDepth] >= 2;
-    if (wv >= nl) return;
+    // st[kCfgLoaders]: loader waves that stream a small share (1 .. kPL; a large share takes all kPL),
+    // st[kCfgDepth]: slots in flight per loader (1 or 2)
+    const int nls = min(kPL, max(1, (int)st[kCfgLoaders])), depth2 = st[kCfgDepth] >= 2;
     const unsigned a_full = lds_addr(ctl + kCtlFull), a_rel = lds_addr(ctl + kCtlRel), a_stop = lds_addr(ctl + kCtlStop);
     int q0 = 0, pend = -1;
     auto publish = [&](int q) { asm_lds_st(a_full + (q % kRing) * 4, (unsigned)q + 1); };
     for (int i = 0; i < n_ops; ++i) {
       const GemvP& p = ops[i];
+      // Touch every 64-byte line of the op's parameters: the op table would otherwise be fetched from memory (the
+      // weight stream evicts it from L2 every run) by the compute waves' scalar loads, one miss after another, on the
+      // chain's critical path; the loaders run ops ahead, so the lines are in the CU's scalar cache by then.
+      {
+        const uint32_t* pw = (const uint32_t*)&p;
+        uint32_t t = 0;
+#pragma unroll
+        for (int k = 0; k < (int)(sizeof(GemvP) / 4); k += 16) t ^= pw[k];
+        asm volatile("" : : "s"(t));
+      }
       const Share s = share_of(p, b, G);
-      const int k0 = ((wv - q0) % nl + nl) % nl;
+      const int nl = s.spread ? nls : kPL;
+      const int k0 = wv < nl ? ((wv - q0) % nl + nl) % nl : s.nslot;
       for (int k = k0; k < s.nslot; k += nl) {
         const int q = q0 + k, pos = q % kRing;
         if ((int)asm_lds_ld(a_rel + pos * 4) < q / kRing) {   // the position still holds slot q - kRing
@@ -204,7 +224,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
 
   // -------------------------------------------------------------------- compute waves
   const int c = wv - kPL, tc = tid - 64 * kPL;
-  volatile unsigned* const vctl = ctl;
+  lds_u32* const lctl = (lds_u32*)ctl;
   float* const xs = (float*)(lds + kOffXs);
   float* const xsum = (float*)(lds + kOffXsum);
   float* const red = (float*)(lds + kOffRed);
@@ -213,14 +233,13 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
   // barrier of the compute waves: a monotonic LDS counter (every compute wave adds 1 per barrier)
   auto cbar = [&]() {
     gen += kPC;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // this wave's LDS writes are done
-    if (lane == 0) __hip_atomic_fetch_add(ctl + kCtlBar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    while (vctl[kCtlBar] < gen) __builtin_amdgcn_s_sleep(0);
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's LDS writes are done
+    if (lane == 0) ctl_add(lctl + kCtlBar, 1u);
+    while (ctl_ld(lctl + kCtlBar) < gen) __builtin_amdgcn_s_sleep(0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
   };
   auto wait_slot = [&](int q) {
-    while (vctl[kCtlFull + q % kRing] != (unsigned)q + 1) __builtin_amdgcn_s_sleep(0);
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    while (ctl_ld(lctl + kCtlFull + q % kRing) != (unsigned)q + 1) __builtin_amdgcn_s_sleep(0);
   };
   // the G flags at f hold this run's tag (wave c == 0 polls); false in every compute thread if the wait gave up
   auto wait_flags = [&](const unsigned* f) -> bool {
@@ -233,13 +252,13 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
       if (lane == 0) {
         if (!go) {
           atomicOr(timed_out, 1u);
-          vctl[kCtlStop] = 1;   // the loaders leave their waits
+          ctl_st(lctl + kCtlStop, 1u);   // the loaders leave their waits
         }
-        vctl[kCtlGo] = go;
+        ctl_st(lctl + kCtlGo, (unsigned)go);
       }
     }
     cbar();
-    return vctl[kCtlGo] != 0;
+    return ctl_ld(lctl + kCtlGo) != 0;
   };
   const unsigned* const mine = flags + (size_t)(b % kFlagCopies) * n_ops * Gp;   // this XCD's copy
   int q0 = 0;
@@ -279,8 +298,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
           if (lane < 16) red[(rp * kPC + c) * 16 + lane] = acc;
         }
         cbar();   // every slot of the share is read, every wave's row sums are in
-        if (tc < s.nslot) __hip_atomic_fetch_add(ctl + kCtlRel + (q0 + tc) % kRing, 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (tc < s.nslot) ctl_add(lctl + kCtlRel + (q0 + tc) % kRing, 1u);
         // epilogue: compute thread t -> row t of the share (a softcap unit is one whole wave)
         const int rows = s.nu * s.nrb * kStageRows;
         if (tc - lane < rows) {
@@ -301,7 +319,9 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
           }
         }
       } else {
-        // one wave per unit: lane takes pairs lane + 64 kk of each slot (group 4 kk + lane / 16, row lane % 16)
+        // a large share (the lm_head), one wave per unit: lane takes pairs lane + 64 kk of each slot (group
+        // 4 kk + lane / 16, row lane % 16); it copies them to registers and hands the slot back to the loaders before
+        // the arithmetic, so the ring's slots spend their time in flight rather than held
         for (int j = c; j < s.nu; j += kPC) {
           for (int r = 0; r < s.nrb; ++r) {
             for (int pt = 0; pt < s.parts; ++pt) {
@@ -310,19 +330,23 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
                 const int q = q0 + slot_index(s, j, (r * s.parts + pt) * s.nh + h);
                 wait_slot(q);
                 const uint8_t* slot = lds + (q % kRing) * kSlotB;
+                u32x4 qv[8];
+                uint32_t sm[8];
 #pragma unroll
                 for (int kk = 0; kk < 8; ++kk) {
-                  const int pp = kk * 64 + lane, g = 32 * h + (pp >> 4);
-                  const u32x4 qv = *(const u32x4l*)(slot + pp * 16);
-                  const uint32_t sm = *(const uint32_t*)(slot + 8192 + pp * 4);
-                  if (g < s.ngs) {
-                    const float d = dot32(qv, xs + g * 32);
-                    acc = __builtin_fmaf(h2f_lo(sm) * 16777216.0f, d, __builtin_fmaf(h2f_hi(sm), xsum[g], acc));
-                  }
+                  qv[kk] = *(const u32x4l*)(slot + (kk * 64 + lane) * 16);
+                  sm[kk] = *(const uint32_t*)(slot + 8192 + (kk * 64 + lane) * 4);
                 }
                 __builtin_amdgcn_s_waitcnt(0xC07F);   // this wave's reads of the slot are done
-                if (lane == 0) __hip_atomic_fetch_add(ctl + kCtlRel + q % kRing, 1u, __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_WORKGROUP);
+                if (lane == 0) ctl_add(lctl + kCtlRel + q % kRing, 1u);
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk) {
+                  const int g = 32 * h + 4 * kk + (lane >> 4);
+                  if (g < s.ngs) {
+                    const float d = dot32(qv[kk], xs + g * 32);
+                    acc = __builtin_fmaf(h2f_lo(sm[kk]) * 16777216.0f, d, __builtin_fmaf(h2f_hi(sm[kk]), xsum[g], acc));
+                  }
+                }
               }
               acc += __shfl_xor(acc, 16, 64);
               acc += __shfl_xor(acc, 32, 64);

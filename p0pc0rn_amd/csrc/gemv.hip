@@ -6,6 +6,7 @@
 // The kernels and their mapping onto MI355X are described in gemv_kernels.hpp.
 #include "gemv_kernels.hpp"
 
+#include <map>
 #include <memory>
 #include <string>
 #include <vector>
@@ -131,6 +132,32 @@ struct ChainExec {
   chain_kernel_t kernel;
 };
 static ChainBuild* g_chain = nullptr;
+static std::map<unsigned*, size_t> g_state_bytes;   // sizes of the uncached state blocks
+
+// Chain state (completion flags and the run tag) lives in uncached device memory: a flag store and the polls of
+// other workgroups then go straight to memory, which halves the hand-off latency against cached device memory
+// (measured on MI355X, cross-XCD round trip 0.69 us vs 1.14 us). Uncached memory that a kernel has read is never
+// freed while the process runs (allocations made after such a free have been seen holding wrong values), so freed
+// chains return their state blocks to this pool, which later chains reuse.
+static std::vector<std::pair<unsigned*, size_t>> g_state_pool;   // free blocks (pointer, bytes)
+static hipError_t state_alloc(unsigned** out, size_t bytes) {
+  size_t best = (size_t)-1;
+  for (size_t i = 0; i < g_state_pool.size(); ++i)
+    if (g_state_pool[i].second >= bytes && (best == (size_t)-1 || g_state_pool[i].second < g_state_pool[best].second))
+      best = i;
+  if (best != (size_t)-1) {
+    *out = g_state_pool[best].first;
+    g_state_pool.erase(g_state_pool.begin() + (long)best);
+    return hipSuccess;
+  }
+  bytes = (bytes + 65535) & ~(size_t)65535;
+  hipError_t e = hipExtMallocWithFlags((void**)out, bytes, hipDeviceMallocUncached);
+  if (e == hipSuccess) g_state_bytes[*out] = bytes;
+  return e;
+}
+static void state_free(unsigned* p) {
+  if (p) g_state_pool.emplace_back(p, g_state_bytes[p]);
+}
 
 // Device-coherent accesses of the ops of a chain (GemvP::coh). Op i reads its inputs with coherent loads when an
 // earlier op writes into them, and writes its outputs with coherent stores when a later op reads them or another op
@@ -505,14 +532,14 @@ extern "C" int p0_chain_end(void** out) {
   const size_t ob = cb->ops.size() * sizeof(GemvP), sb = words * sizeof(unsigned);
   ex->st_words = words;
   hipError_t e = hipMalloc((void**)&ex->ops, ob);
-  if (e == hipSuccess) e = hipMalloc((void**)&ex->st, sb);
+  if (e == hipSuccess) e = state_alloc(&ex->st, sb);
   if (e == hipSuccess) e = hipMemcpy(ex->ops, cb->ops.data(), ob, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemset(ex->st, 0, sb);
   if (e == hipSuccess && ex->pipe_cfg[0])
     e = hipMemcpy(ex->st + pipe_cfg_word(), ex->pipe_cfg, sizeof ex->pipe_cfg, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
     hipFree(ex->ops);
-    hipFree(ex->st);
+    state_free(ex->st);
     delete ex;
     return fail_hip(e, "p0_chain_end");
   }
@@ -567,7 +594,7 @@ extern "C" int p0_chain_free(void* chain) {
   auto* ex = (ChainExec*)chain;
   if (ctx().device >= 0) hipStreamSynchronize(ctx().cur);
   hipFree(ex->ops);
-  hipFree(ex->st);
+  state_free(ex->st);
   delete ex;
   return P0_OK;
 }
