@@ -266,16 +266,18 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmP p) {
                                                            __builtin_bit_cast(half8, bv[h][j]), acc[i][j], 0, 0, 0);
   };
   // one steady-state step (all four k-steps; the next stage exists). Step j's W records live in register set j & 1:
-  // on entry SET = (it + 1) & 1 holds step it + 1 (dequantised now) and the other set holds step it + 2; SET is then
-  // refilled with step it + 3.
+  // on entry SET = (it + 1) & 1 holds step it + 1 (dequantised now) and the other set, free since the last step's
+  // dequant, is refilled with step it + 2 first of all: the loads then have the whole step's MFMAs to land before the
+  // wait that closes the step.
   auto step = [&](int it, int set) {
     const int buf = it & 1, k0 = it * BK;
     const uint8_t* st = lds + buf * kStage;
+    w_load(min(k0 + 2 * BK, (p.K - 1) / BK * BK), set ^ 1);   // step it + 2's records (clamped: the last is re-read)
+    __builtin_amdgcn_sched_barrier(0);
     frag(st, 0, 0);
     x_load(k0 + BK, buf ^ 1);   // the next step's X streams into the other stage meanwhile
     w_stage_fast(k0 + BK, buf ^ 1, set);   // W of the next step (spread amid the MFMAs by the scheduler)
     w_stage_fix(k0 + BK, buf ^ 1, set);
-    w_load(min(k0 + 3 * BK, (p.K - 1) / BK * BK), set);   // step it + 3's records (clamped: the last is re-read)
     frag(st, 1, 1);
     mfmas(0);
     frag(st, 2, 0);
@@ -301,7 +303,6 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmP p) {
   if (nk > 1) w_load(BK, 1);
   w_stage_fast(0, 0, 0);
   w_stage_fix(0, 0, 0);
-  if (nk > 2) w_load(2 * BK, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   int it = 0;
