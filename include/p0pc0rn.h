@@ -17,6 +17,10 @@
  *   p0_q4_gemm                           <- gemm(gpu, a)                          engine/ops/gemm.js:255-322
  *   p0_q4_dequant                        <- the q4g32a.t64 unpacking of            engine/kcheck.js:22-38 (packQ4 deq),
  *                                           engine/ops/gemm.js:139-149 (fp16 tile) and engine/core/store.js:276-301
+ *   p0_rowstats                          <- rowstats(gpu, a)                      engine/ops/misc.js:13-40
+ *   p0_normadd                           <- normadd(g, a)                         engine/llm/lops.js:143-178
+ *   p0_argmax / p0_argmaxM               <- argmax(g, a) / argmaxM(g, a)          engine/llm/lops.js:416-436,
+ *                                                                                 engine/llm/lops_spec.js:327-348
  *
  * Error behaviour: every function returns P0_OK (0) or a nonzero status. On failure, p0_last_error() returns the
  * message of the calling thread's last failure. Argument errors carry the reference's own text (for example
@@ -214,6 +218,43 @@ int p0_chain_free(void* chain);
  * Knobs 0-1 and 4-6 apply to chains begun afterwards, 2-3 to runs. value < 0 only queries (knobs 0-2 also ignore 0);
  * returns the previous value. */
 int p0_chain_tune(int knob, int value);
+
+/* ---- the GEMV's producer and consumers: row statistics, split-K sum + residual RMS, argmax over tile maxima ------- */
+/* rowstats (engine/ops/misc.js:13-40): for each row r < rows of X (floats x[r * x_ld + x_c0 + c], c < cols, from byte
+ * offset x_off), st[(st_off + r) * 2] = mean (0 for mode 1, rms) and st[(st_off + r) * 2 + 1] = 1 / sqrt(var + eps),
+ * var = mean of (x - mean)^2. x_ld 0 = cols. The sums follow the reference's order: 256 strided partial sums, then a
+ * halving tree. */
+typedef struct {
+  const void* x; int64_t x_off;   /* bytes */
+  int64_t x_ld, x_c0;             /* floats */
+  int64_t rows, cols;
+  int32_t mode;                   /* 0 = LayerNorm (mean and variance), 1 = RMSNorm */
+  float eps;
+  float* st; int64_t st_off;      /* in rows: pairs (mean, rstd) */
+} p0_rowstats_args_t;
+int p0_rowstats(const p0_rowstats_args_t* a);
+
+/* normadd (engine/llm/lops.js:143-178): for each row m < M of D floats, t = sum over the t_n split partials
+ * t[j * t_ld + m D + i] (in j order); mode 0: x = (x + t / rms(t) * w[w_off + i]) * scale, rms(t) =
+ * sqrt(mean(t^2) + eps); mode 1: x = t; then st[st_off + m] = 1 / sqrt(mean(x^2) + eps). The reference's defaults:
+ * t_n 0 = 1, t_ld 0 = D M, M 0 = 1, eps 0 = 1e-6 (the caller passes scale; the reference's own default is 1). */
+typedef struct {
+  const float* t; int64_t t_n, t_ld;
+  const float* w; int64_t w_off;  /* mode 0 only */
+  float* x;                       /* [M][D], read and written */
+  float* st; int64_t st_off;
+  int64_t D, M;
+  float eps, scale;
+  int32_t mode;
+} p0_normadd_args_t;
+int p0_normadd(const p0_normadd_args_t* a);
+
+/* argmax (engine/llm/lops.js:416-436): over the n pairs mx[2 i] = max, mx[2 i + 1] = bitcast(u32 index) that a
+ * softcap GEMV writes per 64-row tile, out[0] = the index of the largest value (ties: the lowest index), out[1] = the
+ * bits of that value; n = 0 leaves (0xFFFFFFFF, bits of -3.4e38). argmaxM (engine/llm/lops_spec.js:327-348): the same
+ * for each of M rows of n pairs, out[2 m], out[2 m + 1]. out is device memory. */
+int p0_argmax(const float* mx, int64_t n, uint32_t* out);
+int p0_argmaxM(const float* mx, int64_t n, int64_t M, uint32_t* out);
 
 /* ---- synthetic weights on the device (the reference's GPU filler, engine/tune/autotune.js:73-87) ----------------- */
 /* Symmetric BASELINE records: codes uniform in [0,16) (= q + 8 for q uniform in [-8, 8)), scale = fl16(|N(0, sigma)|),

@@ -5,7 +5,7 @@ import os
 
 import numpy as np
 
-from p0pc0rn_amd.capi import GemmArgs, GemvArgs, GemvMArgs
+from p0pc0rn_amd.capi import GemmArgs, GemvArgs, GemvMArgs, NormaddArgs, RowstatsArgs
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 PATH = os.path.join(HERE, "libq4oracle.so")
@@ -36,6 +36,9 @@ def lib():
         o.p0o_lgemv_f32.argtypes = [vp, i64, vp, i64, i64, vp, C.c_int]
         o.p0o_gemm_f32.argtypes = [vp, i64, vp, i64, i64, i64, vp, C.c_int]
         o.p0o_max_threads.restype = C.c_int
+        o.p0o_rowstats.argtypes = [C.POINTER(RowstatsArgs)]
+        o.p0o_normadd.argtypes = [C.POINTER(NormaddArgs)]
+        o.p0o_argmaxM.argtypes = [vp, i64, i64, vp]
         _o = o
     return _o
 
@@ -127,3 +130,21 @@ def gemm_f32(w, x16, M, N, K, threads=0):
 
 def max_threads():
     return lib().p0o_max_threads()
+
+
+def rowstats(args):
+    """engine/ops/misc.js:13-40 on host pointers (RowstatsArgs)"""
+    lib().p0o_rowstats(C.byref(args))
+
+
+def normadd(args):
+    """engine/llm/lops.js:143-178 on host pointers (NormaddArgs)"""
+    lib().p0o_normadd(C.byref(args))
+
+
+def argmaxM(mx, n, M):
+    """engine/llm/lops_spec.js:327-348 (M = 1: engine/llm/lops.js:416-436); returns uint32 [M][2]"""
+    mx = np.ascontiguousarray(mx, np.float32)
+    out = np.zeros(2 * M, np.uint32)
+    lib().p0o_argmaxM(mx.ctypes.data, n, M, out.ctypes.data)
+    return out

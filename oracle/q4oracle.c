@@ -432,3 +432,103 @@ void p0o_gemm_f32(const uint8_t* w, int64_t wG, const uint16_t* x16, int64_t M, 
   }
   free(wt);
 }
+
+/* ---- rowstats / normadd / argmax --------------------------------------------------------------------------------- */
+/* the reference's 256-lane reduction: lane t sums elements t, t + 256, ... in turn (engine/ops/misc.js:26-27), then
+ * level s = 128, 64, ..., 1 adds lane t + s into lane t (engine/ops/misc.js:20-23) */
+static float tree256(const float* part) {
+  float red[256];
+  memcpy(red, part, sizeof red);
+  for (int s = 128; s > 0; s >>= 1)
+    for (int t = 0; t < s; ++t) red[t] = red[t] + red[t + s];
+  return red[0];
+}
+static float rsqrt_cr(float v) { return 1.0f / sqrtf(v); }
+
+void p0o_rowstats(const p0_rowstats_args_t* a) {   /* engine/ops/misc.js:17-30 */
+  const int64_t ld = a->x_ld ? a->x_ld : a->cols;
+  const float* x = (const float*)((const uint8_t*)a->x + a->x_off);
+  for (int64_t r = 0; r < a->rows; ++r) {
+    const float* xr = x + r * ld + a->x_c0;
+    float part[256], mean = 0.0f;
+    if (a->mode == 0) {
+      for (int t = 0; t < 256; ++t) {
+        float s = 0.0f;
+        for (int64_t i = t; i < a->cols; i += 256) s = s + xr[i];
+        part[t] = s;
+      }
+      mean = tree256(part) / (float)a->cols;
+    }
+    for (int t = 0; t < 256; ++t) {
+      float q = 0.0f;
+      for (int64_t i = t; i < a->cols; i += 256) {
+        const float d = xr[i] - mean;
+        q = q + d * d;
+      }
+      part[t] = q;
+    }
+    const float var = tree256(part) / (float)a->cols;
+    a->st[(a->st_off + r) * 2] = mean;
+    a->st[(a->st_off + r) * 2 + 1] = rsqrt_cr(var + a->eps);
+  }
+}
+
+void p0o_normadd(const p0_normadd_args_t* a) {   /* engine/llm/lops.js:153-170, defaults of :175-177 */
+  const int64_t D = a->D, M = a->M ? a->M : 1, nsrc = a->t_n ? a->t_n : 1, ldp = a->t_ld ? a->t_ld : D * M;
+  const float eps = a->eps != 0.0f ? a->eps : 1e-6f;
+  float* tv = (float*)malloc((size_t)D * sizeof(float));
+  float part[256];
+  for (int64_t m = 0; m < M; ++m) {
+    const int64_t xb = m * D;
+    for (int t = 0; t < 256; ++t) {
+      float s = 0.0f;
+      for (int64_t i = t; i < D; i += 256) {
+        float v = 0.0f;
+        for (int64_t j = 0; j < nsrc; ++j) v = v + a->t[j * ldp + xb + i];
+        tv[i] = v;
+        s = s + v * v;
+      }
+      part[t] = s;
+    }
+    const float rs = rsqrt_cr(tree256(part) / (float)D + eps);
+    for (int t = 0; t < 256; ++t) {
+      float s2 = 0.0f;
+      for (int64_t i = t; i < D; i += 256) {
+        float x = a->x[xb + i];
+        if (a->mode == 0) x = (x + tv[i] * rs * a->w[a->w_off + i]) * a->scale;
+        else x = tv[i];
+        a->x[xb + i] = x;
+        s2 = s2 + x * x;
+      }
+      part[t] = s2;
+    }
+    a->st[a->st_off + m] = rsqrt_cr(tree256(part) / (float)D + eps);
+  }
+  free(tv);
+}
+
+/* engine/llm/lops_spec.js:333-343 (argmax is the M = 1 case, engine/llm/lops.js:422-432): lane t keeps the best of
+ * pairs t, t + 256, ..., then the halving tree; larger value wins, ties go to the lower index */
+void p0o_argmaxM(const float* mx, int64_t n, int64_t M, uint32_t* out) {
+  for (int64_t m = 0; m < M; ++m) {
+    float rv[256];
+    uint32_t ri[256];
+    for (int t = 0; t < 256; ++t) {
+      float bv = -3.4e38f;
+      uint32_t bi = 0xFFFFFFFFu;
+      for (int64_t i = t; i < n; i += 256) {
+        const float v = mx[2 * (m * n + i)];
+        uint32_t id;
+        memcpy(&id, &mx[2 * (m * n + i) + 1], 4);
+        if (v > bv || (v == bv && id < bi)) { bv = v; bi = id; }
+      }
+      rv[t] = bv;
+      ri[t] = bi;
+    }
+    for (int s = 128; s > 0; s >>= 1)
+      for (int t = 0; t < s; ++t)
+        if (rv[t + s] > rv[t] || (rv[t + s] == rv[t] && ri[t + s] < ri[t])) { rv[t] = rv[t + s]; ri[t] = ri[t + s]; }
+    out[2 * m] = ri[0];
+    memcpy(&out[2 * m + 1], &rv[0], 4);
+  }
+}

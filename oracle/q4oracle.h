@@ -45,6 +45,13 @@ void p0o_gemm_f32(const uint8_t* w, int64_t wG, const uint16_t* x16, int64_t M, 
                   int threads);
 int p0o_max_threads(void);
 
+/* the GEMV's producer and consumers, in the reference's own fp32 summation order (256 strided partial sums, then a
+ * halving tree): rowstats (engine/ops/misc.js:13-40), normadd (engine/llm/lops.js:143-178), argmax / argmaxM
+ * (engine/llm/lops.js:416-436, engine/llm/lops_spec.js:327-348). Host pointers, the C ABI's argument structs. */
+void p0o_rowstats(const p0_rowstats_args_t* a);
+void p0o_normadd(const p0_normadd_args_t* a);
+void p0o_argmaxM(const float* mx, int64_t n, int64_t M, uint32_t* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -27,7 +27,7 @@ HEADER_SYMBOLS = [
     "p0_q4_gemv", "p0_q4_gemvM", "p0_q4_gemm", "p0_q4_dequant", "p0_fill_q4_sym", "p0_fill_randn", "p0_gemv_tune",
     "p0_record_begin", "p0_record_end", "p0_replay", "p0_record_free",
     "p0_chain_begin", "p0_chain_end", "p0_chain_run", "p0_chain_status", "p0_chain_info", "p0_chain_free",
-    "p0_chain_tune",
+    "p0_chain_tune", "p0_rowstats", "p0_normadd", "p0_argmax", "p0_argmaxM",
 ]
 
 i64, i32, f32, vp = C.c_int64, C.c_int32, C.c_float, C.c_void_p
@@ -66,6 +66,16 @@ class GemmArgs(C.Structure):
                 ("bv", vp), ("bv_off", i64), ("bv_up", i64), ("act", i32), ("store", i32), ("res", i32)]
 
 
+class RowstatsArgs(C.Structure):
+    _fields_ = [("x", vp), ("x_off", i64), ("x_ld", i64), ("x_c0", i64), ("rows", i64), ("cols", i64), ("mode", i32),
+                ("eps", f32), ("st", vp), ("st_off", i64)]
+
+
+class NormaddArgs(C.Structure):
+    _fields_ = [("t", vp), ("t_n", i64), ("t_ld", i64), ("w", vp), ("w_off", i64), ("x", vp), ("st", vp),
+                ("st_off", i64), ("D", i64), ("M", i64), ("eps", f32), ("scale", f32), ("mode", i32)]
+
+
 class P0Error(RuntimeError):
     def __init__(self, code, msg):
         super().__init__(msg)
@@ -99,6 +109,8 @@ def lib():
             "p0_chain_begin": [], "p0_chain_end": [C.POINTER(vp)], "p0_chain_run": [vp],
             "p0_chain_status": [vp, C.POINTER(i32)], "p0_chain_info": [vp, C.POINTER(ChainInfo)], "p0_chain_free": [vp],
             "p0_chain_tune": [C.c_int, C.c_int],
+            "p0_rowstats": [C.POINTER(RowstatsArgs)], "p0_normadd": [C.POINTER(NormaddArgs)],
+            "p0_argmax": [vp, i64, vp], "p0_argmaxM": [vp, i64, i64, vp],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -326,3 +338,35 @@ def fill_q4_sym(w, N, K, seed, sigma=0.02, w_off=0):
 
 def fill_randn(dst, n, seed, sigma=1.0, as_f16=False, off_bytes=0):
     check(lib().p0_fill_randn(_ptr(dst), off_bytes, n, seed, sigma, 1 if as_f16 else 0))
+
+
+# ------------------------------------------------------------------------------------------------ rowstats / normadd / argmax
+def rowstats_args(**kw):
+    a = RowstatsArgs()
+    for k, v in kw.items():
+        setattr(a, k, _ptr(v) if k in ("x", "st") else v)
+    return a
+
+
+def normadd_args(**kw):
+    a = NormaddArgs()
+    a.scale = 1.0
+    for k, v in kw.items():
+        setattr(a, k, _ptr(v) if k in ("t", "w", "x", "st") else v)
+    return a
+
+
+def rowstats(args):
+    check(lib().p0_rowstats(C.byref(args)))
+
+
+def normadd(args):
+    check(lib().p0_normadd(C.byref(args)))
+
+
+def argmax(mx, n, out):
+    check(lib().p0_argmax(_ptr(mx), n, _ptr(out)))
+
+
+def argmaxM(mx, n, M, out):
+    check(lib().p0_argmaxM(_ptr(mx), n, M, _ptr(out)))

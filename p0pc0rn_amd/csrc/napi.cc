@@ -252,6 +252,39 @@ napi_value Gemm(napi_env env, napi_callback_info info) {
   return make_num(env, flops);
 }
 
+napi_value Rowstats(napi_env env, napi_callback_info info) {
+  auto a = args(env, info, 1);
+  napi_value o = a[0];
+  p0_rowstats_args_t r{};
+  r.x = ptr<const void>(env, o, "x"); r.x_off = i64(env, o, "x_off"); r.x_ld = i64(env, o, "x_ld");
+  r.x_c0 = i64(env, o, "x_c0"); r.rows = i64(env, o, "rows"); r.cols = i64(env, o, "cols");
+  r.mode = i32(env, o, "mode"); r.eps = (float)field(env, o, "eps");
+  r.st = ptr<float>(env, o, "st"); r.st_off = i64(env, o, "st_off");
+  if (fail(env, p0_rowstats(&r))) return nullptr;
+  return undef(env);
+}
+
+napi_value Normadd(napi_env env, napi_callback_info info) {
+  auto a = args(env, info, 1);
+  napi_value o = a[0];
+  p0_normadd_args_t r{};
+  r.t = ptr<const float>(env, o, "t"); r.t_n = i64(env, o, "t_n"); r.t_ld = i64(env, o, "t_ld");
+  r.w = ptr<const float>(env, o, "w"); r.w_off = i64(env, o, "w_off");
+  r.x = ptr<float>(env, o, "x"); r.st = ptr<float>(env, o, "st"); r.st_off = i64(env, o, "st_off");
+  r.D = i64(env, o, "D"); r.M = i64(env, o, "M"); r.eps = (float)field(env, o, "eps");
+  r.scale = (float)field(env, o, "scale", 1.0); r.mode = i32(env, o, "mode");
+  if (fail(env, p0_normadd(&r))) return nullptr;
+  return undef(env);
+}
+
+napi_value ArgmaxM(napi_env env, napi_callback_info info) {   // argmaxM(mx, n, M, out)
+  auto a = args(env, info, 4);
+  if (fail(env, p0_argmaxM((const float*)(uintptr_t)num(env, a[0]), (int64_t)num(env, a[1]), (int64_t)num(env, a[2]),
+                           (uint32_t*)(uintptr_t)num(env, a[3]))))
+    return nullptr;
+  return undef(env);
+}
+
 napi_value Dequant(napi_env env, napi_callback_info info) {   // dequant(w, wOff, N, K, out32, out16)
   auto a = args(env, info, 6);
   if (fail(env, p0_q4_dequant((const void*)(uintptr_t)num(env, a[0]), (int64_t)num(env, a[1]), (int64_t)num(env, a[2]),
@@ -336,6 +369,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"fillRandn", FillRandn}, {"version", Version}, {"recordBegin", RecordBegin}, {"recordEnd", RecordEnd},
       {"replay", Replay}, {"recordFree", RecordFree}, {"chainBegin", ChainBegin}, {"chainEnd", ChainEnd},
       {"chainRun", ChainRun}, {"chainStatus", ChainStatus}, {"chainFree", ChainFree},
+      {"rowstats", Rowstats}, {"normadd", Normadd}, {"argmaxM", ArgmaxM},
   };
   for (auto& f : fns) {
     napi_value v;

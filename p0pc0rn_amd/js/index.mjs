@@ -1,6 +1,8 @@
-// index.mjs - the Node host's public surface: the device object and the three q4 ops, as the reference names them.
+// index.mjs - the Node host's public surface: the device object, the three q4 ops and the GEMV's producer and
+// consumers (rowstats, normadd, argmax, argmaxM), as the reference names them.
 export { createGpu, Gpu, GpuError, view, f2h, h2f, toF16, fromF16, MB } from './core/gpu.mjs';
-export { gemv, KCH } from './llm/lops.mjs';
-export { gemvM } from './llm/lops_spec.mjs';
+export { gemv, normadd, argmax, KCH } from './llm/lops.mjs';
+export { gemvM, argmaxM } from './llm/lops_spec.mjs';
+export { rowstats } from './ops/misc.mjs';
 export { gemm, DEFAULT_TILE } from './ops/gemm.mjs';
 export { DecodeRunner } from './llm/drunner.mjs';

@@ -43,3 +43,21 @@ export function gemv(g, a) {
     mx: a.mx ? addr(a.mx.buf) : 0, cap: a.cap || 30,
   });
 }
+
+/** per row m < M: x_m = (x_m + rms(sum_j t_j,m) * w) * scale (mode 0) or x_m = sum_j t_j,m (mode 1); ST[statOff + m] =
+ *  rstd(x_m) (engine/llm/lops.js:172-178). t: {buf, n (splits), ld (floats between splits)} rows of D;
+ *  w: {buf, off}; x: {buf}; st: {buf, off}; eps, scale, mode */
+export function normadd(g, a) {
+  native().normadd({
+    t: addr(a.t.buf), t_n: a.t.n || 1, t_ld: a.t.ld || a.D * (a.M || 1),
+    w: a.w ? addr(a.w.buf) : 0, w_off: a.w ? a.w.off || 0 : 0,
+    x: addr(a.x.buf), st: addr(a.st.buf), st_off: a.st.off || 0,
+    D: a.D, M: a.M || 1, eps: a.eps || 1e-6, scale: a.scale == null ? 1 : a.scale, mode: a.mode || 0,
+  });
+}
+
+/** argmax over the n per-tile (max, bitcast index) pairs of mx: out[0] = index, out[1] = bits of the max
+ *  (engine/llm/lops.js:434-436) */
+export function argmax(g, a) {
+  native().argmaxM(addr(a.mx.buf), a.n, 1, addr(a.out.buf));
+}

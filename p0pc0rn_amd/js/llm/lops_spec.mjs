@@ -27,3 +27,9 @@ export function gemvM(g, a) {
     mx: a.mx ? addr(a.mx.buf) : 0, cap: a.cap || 30,
   });
 }
+
+/** argmax of each of M rows of n (max, bitcast index) pairs: out[2 m] = index, out[2 m + 1] = bits of the max
+ *  (engine/llm/lops_spec.js:346-348) */
+export function argmaxM(g, a) {
+  native().argmaxM(addr(a.mx.buf), a.n, a.M, addr(a.out.buf));
+}

@@ -165,3 +165,51 @@ const tk = r.end();
     for got, want, what in ((y1, want1, "op 0"), (y2, want2, "op 1")):
         r = rel_l2(got, want)
         assert np.all(np.isfinite(got)) and r <= 2e-5, (mode, what, r)
+
+
+@pytest.mark.gpu
+def test_js_rowstats_normadd_argmax(tmp_path):
+    """rowstats(gpu, a), normadd(g, a), argmax(g, a) and argmaxM(g, a) with the reference's argument objects
+    (engine/ops/misc.js:33-40, engine/llm/lops.js:172-178 and 434-436, engine/llm/lops_spec.js:346-348), bit-exact
+    against the oracle"""
+    rows, cols, D, M, n = 3, 2048, 2048, 2, 300
+    xs = (1.0 + O.randn(rows * cols, 91)).astype(np.float32)
+    t = O.randn(4 * M * D, 92, 0.3).astype(np.float32)
+    w = (0.5 + O.rng_uniform(93, D)).astype(np.float32)
+    x0 = O.randn(M * D, 94).astype(np.float32)
+    rng = np.random.default_rng(95)
+    mx = np.zeros(2 * n * M, np.float32)
+    mx[0::2] = rng.integers(-9, 9, n * M).astype(np.float32)
+    mx[1::2] = np.tile(np.arange(n, dtype=np.uint32) * 64, M).view(np.float32)
+    _save(tmp_path, xs=xs, t=t, w=w, x0=x0, mx=mx)
+    run_node(tmp_path, r"""
+const g = await_gpu();
+const up = (name) => { const b = fs.readFileSync(name + '.bin'); return g.upload(new Uint8Array(b.buffer, b.byteOffset, b.length)); };
+const [xs, t, w, x0, mx] = ['xs', 't', 'w', 'x0', 'mx'].map(up);
+const st = g.buffer(2 * 3 * 4), sn = g.buffer(2 * 4), o1 = g.buffer(8), oM = g.buffer(16);
+P.rowstats(g, { x: { buf: xs, off: 0, ld: 2048 }, rows: 3, cols: 2048, mode: 'ln', eps: 1e-5, st: { buf: st, off: 0 } });
+P.normadd(g, { t: { buf: t, n: 4, ld: 2 * 2048 }, w: { buf: w, off: 0 }, x: { buf: x0 }, st: { buf: sn, off: 0 },
+               D: 2048, M: 2, scale: 0.5 });
+P.argmax(g, { mx: { buf: mx }, n: 300, out: { buf: o1 } });
+P.argmaxM(g, { mx: { buf: mx }, n: 300, M: 2, out: { buf: oM } });
+(async () => {
+  await g.done();
+  for (const [name, b] of [['st', st], ['x', x0], ['sn', sn], ['o1', o1], ['oM', oM]])
+    fs.writeFileSync(name + '.out', Buffer.from(await g.read(b)));
+  console.log('ok');
+  g.freeAll(); g.device.destroy();
+})();
+""")
+    # buffers are rounded up to 16 bytes (Gpu.buffer): read back only the values
+    rd = lambda name, dt, k: np.fromfile(str(tmp_path / (name + ".out")), dt)[:k]
+    want_st = np.zeros(6, np.float32)
+    O.rowstats(capi.rowstats_args(x=xs.ctypes.data, x_ld=cols, rows=rows, cols=cols, mode=0, eps=1e-5,
+                                  st=want_st.ctypes.data))
+    assert np.array_equal(rd("st", np.uint32, 6), want_st.view(np.uint32))
+    xw, sw = x0.copy(), np.zeros(M, np.float32)
+    O.normadd(capi.normadd_args(t=t.ctypes.data, t_n=4, t_ld=M * D, w=w.ctypes.data, x=xw.ctypes.data,
+                                st=sw.ctypes.data, D=D, M=M, eps=1e-6, scale=0.5, mode=0))
+    assert np.array_equal(rd("x", np.uint32, M * D), xw.view(np.uint32))
+    assert np.array_equal(rd("sn", np.uint32, M), sw.view(np.uint32))
+    assert np.array_equal(rd("o1", np.uint32, 2), O.argmaxM(mx, n, 1))
+    assert np.array_equal(rd("oM", np.uint32, 2 * M), O.argmaxM(mx, n, M))
