@@ -27,6 +27,8 @@ def lib():
         o.p0o_randn.argtypes = [C.c_uint32, C.c_double, vp, i64]
         o.p0o_pack_q4.argtypes = [vp, i64, i64, vp, vp]
         o.p0o_dequant_q4.argtypes = [vp, i64, i64, i64, vp, vp]
+        o.p0o_pack_q8.argtypes = [vp, i64, i64, vp, vp]
+        o.p0o_dequant_q8.argtypes = [vp, i64, i64, i64, vp]
         o.p0o_hash.argtypes, o.p0o_hash.restype = [C.c_uint32], C.c_uint32
         o.p0o_fill_q4_sym.argtypes = [vp, i64, i64, C.c_uint32, C.c_float]
         o.p0o_fill_randn.argtypes = [vp, vp, i64, C.c_uint32, C.c_float]
@@ -147,4 +149,19 @@ def argmaxM(mx, n, M):
     mx = np.ascontiguousarray(mx, np.float32)
     out = np.zeros(2 * M, np.uint32)
     lib().p0o_argmaxM(mx.ctypes.data, n, M, out.ctypes.data)
+    return out
+
+
+def pack_q8(W, N, K):
+    """packQ8 (engine/kcheck.js:39-52): (record bytes uint8, exact dequantized f32 [N][K])"""
+    W = np.ascontiguousarray(W, np.float32)
+    out = np.zeros(N // 64 * K // 64 * 4224, np.uint8)
+    deq = np.zeros(N * K, np.float32)
+    lib().p0o_pack_q8(W.ctypes.data, N, K, out.ctypes.data, deq.ctypes.data)
+    return out, deq
+
+
+def dequant_q8(w, N, K, wG=None):
+    out = np.zeros(N * K, np.float32)
+    lib().p0o_dequant_q8(np.ascontiguousarray(w).ctypes.data, N, K, wG or K // 64, out.ctypes.data)
     return out

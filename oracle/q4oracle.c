@@ -123,6 +123,31 @@ void p0o_pack_q4(const float* W, int64_t N, int64_t K, uint8_t* out, float* deq)
     }
 }
 
+/* packQ8 (engine/kcheck.js:39-52): per (row, 64-group) s = fl16(absmax / 127) (1 if 0), q = clamp(rhe(w / s), -128, 127);
+ * record (tile, group) = 4224 bytes: row r's 64 int8 codes at 64 r (k order), fp16 scales at 4096 + 2 r */
+void p0o_pack_q8(const float* W, int64_t N, int64_t K, uint8_t* out, float* deq) {
+  const int64_t NT = N / 64, G = K / 64;
+  for (int64_t t = 0; t < NT; t++)
+    for (int64_t g = 0; g < G; g++) {
+      uint8_t* rec = out + (t * G + g) * 4224;
+      for (int r = 0; r < 64; r++) {
+        const int64_t n = t * 64 + r, base = n * K + g * 64;
+        double am = 0;
+        for (int i = 0; i < 64; i++) am = fmax(am, fabs((double)W[base + i]));
+        float s = rf16(am / 127.0);
+        if (s == 0.0f) s = 1.0f;
+        for (int i = 0; i < 64; i++) {
+          double q = rhe((double)W[base + i] / (double)s);
+          q = q < -128 ? -128 : q > 127 ? 127 : q;
+          rec[r * 64 + i] = (uint8_t)((int)q & 255);
+          if (deq) deq[base + i] = (float)(q * s);
+        }
+        const uint16_t h = p0o_f2h(s);
+        memcpy(rec + 4096 + r * 2, &h, 2);
+      }
+    }
+}
+
 /* ------------------------------------------------------------------------------------------------ dequant */
 static inline uint32_t rd32(const uint8_t* p) { uint32_t v; memcpy(&v, p, 4); return v; }
 
@@ -136,6 +161,21 @@ static inline float deq_one(const uint8_t* w, int64_t wG, int64_t n, int64_t k) 
   float s = p0o_h2f((uint16_t)(sm & 0xffffu)), m = p0o_h2f((uint16_t)(sm >> 16));
   volatile float qs = q * s;   /* exact (4-bit times 11-bit significands) */
   return qs + m;               /* one f32 rounding */
+}
+
+/* engine/llm/lops.js:74-80: q8g64s.t64 record (tile, k / 64); byte (r, k % 64) is a signed code; word 1024 + r / 2
+ * holds the fp16 scales of rows 2j (low half) and 2j + 1; the weight is q s, exact in f32 (8 x 11 bits) */
+static inline float deq_one_q8(const uint8_t* w, int64_t wG, int64_t n, int64_t k) {
+  const uint8_t* rec = w + (((n >> 6) * wG + (k >> 6)) * 4224);
+  const int r = (int)(n & 63);
+  const int8_t q = (int8_t)rec[r * 64 + (k & 63)];
+  uint16_t h;
+  memcpy(&h, rec + 4096 + r * 2, 2);
+  return (float)q * p0o_h2f(h);
+}
+void p0o_dequant_q8(const uint8_t* w, int64_t N, int64_t K, int64_t wG, float* out32) {
+  for (int64_t n = 0; n < N; n++)
+    for (int64_t k = 0; k < K; k++) out32[n * K + k] = deq_one_q8(w, wG, n, k);
 }
 
 void p0o_dequant_q4(const uint8_t* w, int64_t N, int64_t K, int64_t wG, float* out32, uint16_t* out16) {
@@ -204,15 +244,18 @@ static inline float softcap_f(double v, float cap) {   /* engine/llm/lops.js:96 
   return (float)((double)cap * tanh(fmin(15.0, fmax(-15.0, v / (double)cap))));
 }
 
-static double dot_row(const uint8_t* w, int64_t wG, int64_t n, const float* xp, int64_t k0, int64_t k1) {
+static double dot_row(const uint8_t* w, int enc, int64_t wG, int64_t n, const float* xp, int64_t k0, int64_t k1) {
   double acc = 0;
-  for (int64_t k = k0; k < k1; k++) acc += (double)deq_one(w, wG, n, k) * (double)xp[k - k0];
+  if (enc == P0_ENC_Q8G64S_T64)
+    for (int64_t k = k0; k < k1; k++) acc += (double)deq_one_q8(w, wG, n, k) * (double)xp[k - k0];
+  else
+    for (int64_t k = k0; k < k1; k++) acc += (double)deq_one(w, wG, n, k) * (double)xp[k - k0];
   return acc;
 }
 
 /* one GEMV-M pass; gemv is M = 1 with its own argument defaults (engine/llm/lops.js:111-141 vs lops_spec.js:163-191) */
 typedef struct {
-  const uint8_t* w; int64_t wG;
+  const uint8_t* w; int enc; int64_t wG;
   const float* X; int64_t ldx, rowB;
   int64_t M, N, K, kPer;
   int pro, epi;
@@ -245,7 +288,7 @@ static int run_gemv(const gv_t* p) {
       }
       int64_t rows = p->epi == P0_EPI_GEGLU ? 2 * p->N : p->N;
 #pragma omp parallel for schedule(static)
-      for (int64_t n = 0; n < rows; n++) tot[n] = dot_row(p->w, p->wG, n, xp, k0, k1);
+      for (int64_t n = 0; n < rows; n++) tot[n] = dot_row(p->w, p->enc, p->wG, n, xp, k0, k1);
       /* epilogues: engine/llm/lops.js:92-103, engine/llm/lops_spec.js:130-153 */
       if (p->epi == P0_EPI_STORE) {
         for (int64_t n = 0; n < p->N; n++) p->Y[s * p->ldy + m * p->ldm + n] = (float)tot[n];
@@ -276,7 +319,9 @@ int p0o_q4_gemv(const p0_gemv_args_t* a) {   /* engine/llm/lops.js:111-141 */
   int64_t K = a->K, kch = (!a->kPer && K > 2048) ? ((K + 255) / 256) * 256 : 2048;
   int64_t kPer = a->kPer ? a->kPer : K;
   if (kPer > kch) kPer = kch;
-  gv_t p = {(const uint8_t*)a->w + a->w_off, a->w_cols / 32, a->x, 0, a->x_rowB, 1, a->N, K, kPer, a->pro, a->epi, a->y,
+  const int enc = a->w_enc == P0_ENC_Q8G64S_T64 ? P0_ENC_Q8G64S_T64 : P0_ENC_Q4G32A_T64;
+  gv_t p = {(const uint8_t*)a->w + a->w_off, enc, a->w_cols / (enc == P0_ENC_Q8G64S_T64 ? 64 : 32), a->x, 0, a->x_rowB, 1,
+            a->N, K, kPer, a->pro, a->epi, a->y,
             a->ldy ? a->ldy : a->N, 0, a->epi == P0_EPI_SOFTCAP ? a->mx : a->stat, a->stat_off, 0, a->norm, a->norm_off,
             a->src_n, a->src_ld, a->ev, a->ev_off, 0, a->mx, a->cap != 0.f ? a->cap : 30.f};
   return run_gemv(&p);
@@ -285,7 +330,9 @@ int p0o_q4_gemv(const p0_gemv_args_t* a) {   /* engine/llm/lops.js:111-141 */
 int p0o_q4_gemvM(const p0_gemvm_args_t* a) {   /* engine/llm/lops_spec.js:163-191 */
   int64_t K = a->K, kPer = a->kPer ? (a->kPer < 2048 ? a->kPer : 2048) : K;
   int64_t ldm = a->y_ldm ? a->y_ldm : a->N, ldy = a->y_ldy ? a->y_ldy : a->M * ldm;
-  gv_t p = {(const uint8_t*)a->w + a->w_off, a->w_cols / 32, a->x, a->x_ldx ? a->x_ldx : K, a->x_rowB, a->M, a->N, K, kPer,
+  const int enc = a->w_enc == P0_ENC_Q8G64S_T64 ? P0_ENC_Q8G64S_T64 : P0_ENC_Q4G32A_T64;
+  gv_t p = {(const uint8_t*)a->w + a->w_off, enc, a->w_cols / (enc == P0_ENC_Q8G64S_T64 ? 64 : 32), a->x,
+            a->x_ldx ? a->x_ldx : K, a->x_rowB, a->M, a->N, K, kPer,
             a->pro, a->epi, a->y, ldy, ldm, a->stat, a->stat_off, a->stat_ld ? a->stat_ld : 2, a->norm, a->norm_off,
             a->src_n ? a->src_n : 1, a->src_ld, a->ev, a->ev_off, a->ev_ld, a->mx, a->cap != 0.f ? a->cap : 30.f};
   return run_gemv(&p);

@@ -24,6 +24,10 @@ void p0o_randn(uint32_t seed, double scale, float* out, int64_t n);
 
 /* packQ4 (engine/kcheck.js:22-38): W [N][K] f32 -> records (N/64 * K/32 * 1280 B) + the exact dequantized f32 */
 void p0o_pack_q4(const float* W, int64_t N, int64_t K, uint8_t* bytes, float* deq);
+/* packQ8 (engine/kcheck.js:39-52): W [N][K] f32 -> q8g64s.t64 records (N/64 * K/64 * 4224 B) + the exact dequant */
+void p0o_pack_q8(const float* W, int64_t N, int64_t K, uint8_t* bytes, float* deq);
+/* q8g64s.t64 record reader (engine/llm/lops.js:74-80): q * s, [N][K] */
+void p0o_dequant_q8(const uint8_t* w, int64_t N, int64_t K, int64_t wG, float* out32);
 /* record reader (engine/llm/lops.js:67-71, engine/ops/gemm.js:139-149): fl32(q*s+m) and fl16 of it, [N][K] */
 void p0o_dequant_q4(const uint8_t* w, int64_t N, int64_t K, int64_t wG, float* out32, uint16_t* out16);
 
@@ -32,7 +36,8 @@ uint32_t p0o_hash(uint32_t x);
 void p0o_fill_q4_sym(uint8_t* w, int64_t N, int64_t K, uint32_t seed, float sigma);
 void p0o_fill_randn(float* out32, uint16_t* out16, int64_t n, uint32_t seed, float sigma);
 
-/* reference results (float64 dot over the exact dequantized weights); returns the number of splits */
+/* reference results (float64 dot over the exact dequantized weights, of either encoding, w_enc); returns the number of
+ * splits */
 int p0o_q4_gemv(const p0_gemv_args_t* a);      /* engine/llm/lops.js:30-141 */
 int p0o_q4_gemvM(const p0_gemvm_args_t* a);    /* engine/llm/lops_spec.js:44-191 */
 int p0o_q4_gemm(const p0_gemm_args_t* a);      /* engine/ops/gemm.js:25-322 */

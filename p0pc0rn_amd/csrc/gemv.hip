@@ -288,7 +288,27 @@ static bool plan_pipe(std::vector<GemvP>& ops, int G) {
   return true;
 }
 
+// q8g64s.t64: one workgroup per (64-row tile, split), gemv_q8.hip
+static int launch_q8(GemvP& p, int M, const char* op) {
+  if (g_chain) {
+    set_error("%s: q8g64s.t64 ops cannot join a chain in this build", op);
+    if (g_chain->error.empty()) g_chain->error = p0_last_error();
+    return P0_EINVAL;
+  }
+  q8_kernel_t k = q8_kernel(M);
+  const size_t lds = q8_lds_bytes(M);
+  static bool attr[2] = {false, false};
+  if (!attr[M == 1]) {
+    P0_HIP(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)q8_lds_bytes(16)), op);
+    attr[M == 1] = true;
+  }
+  hipLaunchKernelGGL(k, dim3((unsigned)p.NT, (unsigned)p.nsplit), dim3(256), lds, ctx().cur, p);
+  P0_LAUNCHED(op);
+  return P0_OK;
+}
+
 static int launch(GemvP& p, int M, const char* op) {
+  if (p.enc == P0_ENC_Q8G64S_T64) return launch_q8(p, M, op);
   ChainBuild* cb = g_chain;
   if (cb && cb->ops.empty()) {   // the chain's first op fixes M and the workgroup shape
     cb->M = M;
@@ -333,10 +353,10 @@ static int launch(GemvP& p, int M, const char* op) {
   return P0_OK;
 }
 
+// engine/llm/lops.js:113-114: q4g32a.t64 (groups of 32 k) and q8g64s.t64 (groups of 64 k)
 static int check_enc(int32_t enc, const char* op) {
-  if (enc == P0_ENC_Q4G32A_T64) return P0_OK;
-  if (enc == P0_ENC_Q8G64S_T64) set_error("%s: encoding q8g64s.t64 is not supported by this build", op);
-  else set_error("%s: encoding %d", op, (int)enc);
+  if (enc == P0_ENC_Q4G32A_T64 || enc == P0_ENC_Q8G64S_T64) return P0_OK;
+  set_error("%s: encoding %d", op, (int)enc);
   return P0_EINVAL;
 }
 
@@ -354,13 +374,14 @@ extern "C" int p0_q4_gemv(const p0_gemv_args_t* a, int32_t* nsplit_out) {
   const int64_t kch = (!a->kPer && K > 2048) ? (K + 255) / 256 * 256 : 2048;
   if (kch > 3072) { set_error("gemv: K %lld needs a kPer", (long long)K); return P0_EINVAL; }
   const int64_t kPer = a->kPer ? (a->kPer < kch ? a->kPer : kch) : (K < kch ? K : kch);
-  if (kPer <= 0 || kPer % 32) { set_error("gemv: kPer must be a multiple of 32"); return P0_EINVAL; }
+  const int64_t G = a->w_enc == P0_ENC_Q8G64S_T64 ? 64 : 32;
+  if (kPer <= 0 || kPer % G) { set_error("gemv: kPer must be a multiple of %lld", (long long)G); return P0_EINVAL; }
   const int64_t nsplit = (K + kPer - 1) / kPer;
   if (a->epi != P0_EPI_STORE && nsplit > 1) { set_error("gemv: %s needs one split", epi_name(a->epi)); return P0_EINVAL; }
   if (N % 64) { set_error("gemv: N %% 64"); return P0_EINVAL; }
   if (a->w_off % 4) { set_error("gemv: weight offset"); return P0_EINVAL; }
   // this build's additional guards (the reference would read undefined memory here)
-  if (K <= 0 || K % 32) { set_error("gemv: K must be a multiple of 32"); return P0_EINVAL; }
+  if (K <= 0 || K % G) { set_error("gemv: K must be a multiple of %lld", (long long)G); return P0_EINVAL; }
   if (N <= 0) { set_error("gemv: N must be positive"); return P0_EINVAL; }
   if (a->w_cols < K) { set_error("gemv: weight has %lld columns < K %lld", (long long)a->w_cols, (long long)K); return P0_EINVAL; }
   if (a->pro < P0_PRO_RAW || a->pro > P0_PRO_PLEG) { set_error("gemv: prologue %d", a->pro); return P0_EINVAL; }
@@ -375,7 +396,8 @@ extern "C" int p0_q4_gemv(const p0_gemv_args_t* a, int32_t* nsplit_out) {
 
   GemvP p{};
   p.w = (const uint8_t*)a->w + a->w_off;
-  p.wG = a->w_cols / 32;
+  p.wG = a->w_cols / G;
+  p.enc = a->w_enc;
   p.N = (int)N; p.K = (int)K; p.kPer = (int)kPer; p.nsplit = (int)nsplit; p.NT = (int)(N / 64);
   p.pro = a->pro; p.epi = a->epi;
   p.X = a->x; p.ldx = 0; p.rowB = a->x_rowB;
@@ -386,6 +408,7 @@ extern "C" int p0_q4_gemv(const p0_gemv_args_t* a, int32_t* nsplit_out) {
   p.EV = a->ev; p.evOff = a->ev_off; p.evLd = 0;
   p.Y = a->y; p.ldy = a->ldy ? a->ldy : N; p.ldm = 0;
   p.MX = a->mx; p.cap = a->cap != 0.0f ? a->cap : 30.0f;
+  p.mrows = 1;
   if (int r = launch(p, 1, "gemv")) return r;
   if (nsplit_out) *nsplit_out = (int32_t)nsplit;
   return P0_OK;
@@ -401,12 +424,13 @@ extern "C" int p0_q4_gemvM(const p0_gemvm_args_t* a, int32_t* nsplit_out) {
   if (M < 1 || M > 16) { set_error("gemvM: M %lld (this build: 1..16)", (long long)M); return P0_EINVAL; }
   // engine/llm/lops_spec.js:170-173, in the reference's order
   const int64_t kPer = a->kPer ? (a->kPer < 2048 ? a->kPer : 2048) : K;
-  if (kPer <= 0 || kPer % 32) { set_error("gemvM: kPer must be a multiple of 32"); return P0_EINVAL; }
+  const int64_t G = a->w_enc == P0_ENC_Q8G64S_T64 ? 64 : 32;
+  if (kPer <= 0 || kPer % G) { set_error("gemvM: kPer must be a multiple of %lld", (long long)G); return P0_EINVAL; }
   const int64_t nsplit = (K + kPer - 1) / kPer;
   if (a->epi != P0_EPI_STORE && nsplit > 1) { set_error("gemvM: %s needs one split", epi_name(a->epi)); return P0_EINVAL; }
   if (N % 64) { set_error("gemvM: N %% 64"); return P0_EINVAL; }
   if (a->w_off % 4) { set_error("gemvM: weight offset"); return P0_EINVAL; }
-  if (K <= 0 || K % 32) { set_error("gemvM: K must be a multiple of 32"); return P0_EINVAL; }
+  if (K <= 0 || K % G) { set_error("gemvM: K must be a multiple of %lld", (long long)G); return P0_EINVAL; }
   if (N <= 0) { set_error("gemvM: N must be positive"); return P0_EINVAL; }
   if (a->w_cols < K) { set_error("gemvM: weight has %lld columns < K %lld", (long long)a->w_cols, (long long)K); return P0_EINVAL; }
   if (a->epi < P0_EPI_STORE || a->epi > P0_EPI_SOFTCAP) { set_error("gemvM: epilogue %d", a->epi); return P0_EINVAL; }
@@ -418,7 +442,8 @@ extern "C" int p0_q4_gemvM(const p0_gemvm_args_t* a, int32_t* nsplit_out) {
 
   GemvP p{};
   p.w = (const uint8_t*)a->w + a->w_off;
-  p.wG = a->w_cols / 32;
+  p.wG = a->w_cols / G;
+  p.enc = a->w_enc;
   p.N = (int)N; p.K = (int)K; p.kPer = (int)kPer; p.nsplit = (int)nsplit; p.NT = (int)(N / 64);
   p.pro = a->pro; p.epi = a->epi;
   p.X = a->x; p.ldx = a->x_ldx ? a->x_ldx : K; p.rowB = a->x_rowB;
@@ -429,6 +454,7 @@ extern "C" int p0_q4_gemvM(const p0_gemvm_args_t* a, int32_t* nsplit_out) {
   p.ldm = a->y_ldm ? a->y_ldm : N;
   p.Y = a->y; p.ldy = a->y_ldy ? a->y_ldy : M * p.ldm;
   p.MX = a->mx; p.cap = a->cap != 0.0f ? a->cap : 30.0f;
+  p.mrows = (int)M;
   if (int r = launch(p, (int)M, "gemvM")) return r;
   if (nsplit_out) *nsplit_out = (int32_t)nsplit;
   return P0_OK;

@@ -65,6 +65,8 @@ struct GemvP {
   int su, scur, snrb, sngp;   // units, first position, 16-row blocks per unit, groups per split rounded up to 16
   int sred;                   // LDS float offset of the reduction area (after x' and its group sums)
   int swoff;                  // LDS byte offset of the staged weights
+  int enc;                    // P0_ENC_Q4G32A_T64, or P0_ENC_Q8G64S_T64 (gemv_q8.hip)
+  int mrows;                  // rows of x (M)
 };
 
 __device__ __forceinline__ float gelu_tanh(float v) {   // engine/llm/lops.js:26
@@ -759,6 +761,11 @@ chain_kernel_t pick_chain_m(int W) {   // 16-wave chain workgroups for M = 1, 8-
   if (M == 1 && W == 16) return q4_gemv_chain_kernel<M, (M == 1 ? 16 : 8)>;
   return q4_gemv_chain_kernel<M, 8>;
 }
+
+// the q8g64s.t64 GEMV (gemv_q8.hip): the kernel for M rows and its LDS bytes
+typedef void (*q8_kernel_t)(GemvP);
+q8_kernel_t q8_kernel(int M);
+size_t q8_lds_bytes(int M);
 
 // the pipelined M = 1 chain (chain_pipe.hip): its kernel and its fixed shape
 chain_kernel_t pipe_chain_kernel();

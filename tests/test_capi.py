@@ -59,7 +59,8 @@ def gemv_err(**kw):
     (dict(K=4096, w_cols=4096, kPer=2048, epi=1), "gemv: geglu needs one split"),
     (dict(K=4096, w_cols=4096, kPer=2048, epi=2, mx=16), "gemv: softcap needs one split"),
     (dict(w_off=2), "gemv: weight offset"),
-    (dict(w_enc=2), "gemv: encoding q8g64s.t64 is not supported by this build"),
+    (dict(w_enc=2, K=4096, w_cols=4096, kPer=2016), "gemv: kPer must be a multiple of 64"),   # q8: groups of 64
+    (dict(w_enc=2, K=96, w_cols=96), "gemv: kPer must be a multiple of 64"),
     (dict(w_enc=7), "gemv: encoding 7"),
     (dict(K=48, w_cols=48), "gemv: kPer must be a multiple of 32"),
 ])
