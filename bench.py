@@ -221,8 +221,9 @@ def bench_config_a(c, reps=8):
 
 
 def bench_gemm(c, M, shapes, reps=5):
-    """the dequant-GEMMs of one DiT block at M tokens: bf16 N(0,1) activations (converted to fp16 in-kernel, exact
-    for |x| >= 2^-17), fp16 output"""
+    """the dequant-GEMMs of one DiT block at M tokens: bf16 N(0,1) activations (converted to fp16 by a staging pass,
+    exact for |x| >= 2^-17), fp16 output. The block figure times the block's GEMMs (each with its staging pass)
+    recorded back to back and replayed; per_gemm times each GEMM replayed alone."""
     Kmax = max(k for (_, n, k) in shapes)
     Nmax = max(n for (_, n, k) in shapes)
     xf = np.random.default_rng(3).standard_normal(M * Kmax, dtype=np.float32)
@@ -234,17 +235,22 @@ def bench_gemm(c, M, shapes, reps=5):
         b = c.Buffer(n // 64 * k // 32 * 1280)
         c.fill_q4_sym(b, n, k, 100 + i, 0.02)
         ws.append((name, b, n, k))
-    res, tot_fl, tot_ms = {}, 0.0, 0.0
+    res, tot_fl, all_args = {}, 0.0, []
     for name, b, n, k in ws:
         args = c.gemm_args(w=b, w_rows=n, w_cols=k, x=x, x_ld=k, x_mode=c.XMODE["bf16"], M=M, N=n, K=k,
                            epi=c.GEPI["f16"], y=y)
         c.q4_gemm(args)   # once eagerly: sizes the activation staging workspace outside the recording
         c.done()
-        ms = time_recording(c, lambda: c.q4_gemm(args), 2, reps)
+        ms = time_recording(c, lambda: c.q4_gemm(args), 2, reps)   # one GEMM per replay (launch latency included)
         fl = 2.0 * M * n * k
         res[name] = {"ms": round(ms, 4), "TFLOPS": round(fl / (ms * 1e-3) / 1e12, 1)}
         tot_fl += fl
-        tot_ms += ms
+        all_args.append(args)
+
+    def block():   # the block's linears back to back, as a DiT block runs them: one recording per block
+        for a in all_args:
+            c.q4_gemm(a)
+    tot_ms = time_recording(c, block, 2, reps)
     for (_, b, _, _) in ws:
         b.free()
     x.free()
@@ -364,8 +370,10 @@ def main():
     if dec["mode"] == "chain":
         roofline = {"bound": "hbm", "achieved": round(step_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                     "frac": round(step_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                    "kernel": "q4_gemv_chain_kernel<1,%d> (the whole M=1 decode step: 121 GEMV ops, one launch)"
-                              % dec["chain"]["waves_per_workgroup"],
+                    "kernel": ("q4_chain_pipe_kernel (the whole M=1 decode step: 121 GEMV ops, one launch)"
+                               if dec["chain"]["waves_per_workgroup"] == 12 else
+                               "q4_gemv_chain_kernel<1,%d> (the whole M=1 decode step: 121 GEMV ops, one launch)"
+                               % dec["chain"]["waves_per_workgroup"]),
                     "bytes_per_launch": int(dec["bytes"]), "us_per_launch": round(ms * 1e3, 2)}
         traffic_key = "decode_chain_bytes_per_launch"
     elif not dec["by_kind"]:
