@@ -21,6 +21,7 @@
  *   p0_normadd                           <- normadd(g, a)                         engine/llm/lops.js:143-178
  *   p0_argmax / p0_argmaxM               <- argmax(g, a) / argmaxM(g, a)          engine/llm/lops.js:416-436,
  *                                                                                 engine/llm/lops_spec.js:327-348
+ *   p0_upload_file                       <- PackStore.upload's shard streaming    engine/core/store.js:221-244
  *
  * Error behaviour: every function returns P0_OK (0) or a nonzero status. On failure, p0_last_error() returns the
  * message of the calling thread's last failure. Argument errors carry the reference's own text (for example
@@ -255,6 +256,12 @@ int p0_normadd(const p0_normadd_args_t* a);
  * for each of M rows of n pairs, out[2 m], out[2 m + 1]. out is device memory. */
 int p0_argmax(const float* mx, int64_t n, uint32_t* out);
 int p0_argmaxM(const float* mx, int64_t n, int64_t M, uint32_t* out);
+
+/* ---- the pack reader's I/O (engine/core/store.js:221-244) ---------------------------------------------------------- */
+/* bytes [offset, offset + bytes) of the file at path -> device memory dst + dst_off, streamed in 16 MB chunks through
+ * two pinned host buffers (file reads overlap the host-to-device copies on the library's stream); returns when the
+ * copies are done. The pack manifest (shards, tensors, encodings) is read by the host (p0pc0rn_amd/js/core/store.mjs). */
+int p0_upload_file(const char* path, int64_t offset, int64_t bytes, void* dst, int64_t dst_off);
 
 /* ---- synthetic weights on the device (the reference's GPU filler, engine/tune/autotune.js:73-87) ----------------- */
 /* Symmetric BASELINE records: codes uniform in [0,16) (= q + 8 for q uniform in [-8, 8)), scale = fl16(|N(0, sigma)|),

@@ -24,7 +24,7 @@ ORACLE_DIR = os.path.join(ROOT, "oracle")
 ORACLE = os.path.join(ORACLE_DIR, "libq4oracle.so")
 
 HIP_SOURCES = ["runtime.hip", "gemv.hip", "chain_pipe.hip", "gemv_m01_04.hip", "gemv_m05_08.hip", "gemv_m09_12.hip",
-               "gemv_m13_16.hip", "gemm.hip", "util.hip", "misc.hip", "gemv_q8.hip"]
+               "gemv_m13_16.hip", "gemm.hip", "util.hip", "misc.hip", "gemv_q8.hip", "pack.hip"]
 # packed-fp32 instructions are disabled on purpose: hipcc -O3 would otherwise pair fp32 ops into v_pk_*_f32
 HIPCC_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]

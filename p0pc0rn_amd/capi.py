@@ -27,7 +27,7 @@ HEADER_SYMBOLS = [
     "p0_q4_gemv", "p0_q4_gemvM", "p0_q4_gemm", "p0_q4_dequant", "p0_fill_q4_sym", "p0_fill_randn", "p0_gemv_tune",
     "p0_record_begin", "p0_record_end", "p0_replay", "p0_record_free",
     "p0_chain_begin", "p0_chain_end", "p0_chain_run", "p0_chain_status", "p0_chain_info", "p0_chain_free",
-    "p0_chain_tune", "p0_rowstats", "p0_normadd", "p0_argmax", "p0_argmaxM",
+    "p0_chain_tune", "p0_rowstats", "p0_normadd", "p0_argmax", "p0_argmaxM", "p0_upload_file",
 ]
 
 i64, i32, f32, vp = C.c_int64, C.c_int32, C.c_float, C.c_void_p
@@ -111,6 +111,7 @@ def lib():
             "p0_chain_tune": [C.c_int, C.c_int],
             "p0_rowstats": [C.POINTER(RowstatsArgs)], "p0_normadd": [C.POINTER(NormaddArgs)],
             "p0_argmax": [vp, i64, vp], "p0_argmaxM": [vp, i64, i64, vp],
+            "p0_upload_file": [C.c_char_p, i64, i64, vp, i64],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -370,3 +371,8 @@ def argmax(mx, n, out):
 
 def argmaxM(mx, n, M, out):
     check(lib().p0_argmaxM(_ptr(mx), n, M, _ptr(out)))
+
+
+def upload_file(path, offset, nbytes, dst, dst_off=0):
+    """bytes [offset, offset + nbytes) of a file -> device memory (the pack reader's I/O, engine/core/store.js:221-244)"""
+    check(lib().p0_upload_file(os.fsencode(path), offset, nbytes, _ptr(dst), dst_off))

@@ -285,6 +285,18 @@ napi_value ArgmaxM(napi_env env, napi_callback_info info) {   // argmaxM(mx, n, 
   return undef(env);
 }
 
+napi_value UploadFile(napi_env env, napi_callback_info info) {   // uploadFile(path, offset, bytes, dst, dstOff)
+  auto a = args(env, info, 5);
+  size_t len = 0;
+  napi_get_value_string_utf8(env, a[0], nullptr, 0, &len);
+  std::string path(len, '\0');
+  napi_get_value_string_utf8(env, a[0], &path[0], len + 1, &len);
+  if (fail(env, p0_upload_file(path.c_str(), (int64_t)num(env, a[1]), (int64_t)num(env, a[2]),
+                               (void*)(uintptr_t)num(env, a[3]), (int64_t)num(env, a[4]))))
+    return nullptr;
+  return undef(env);
+}
+
 napi_value Dequant(napi_env env, napi_callback_info info) {   // dequant(w, wOff, N, K, out32, out16)
   auto a = args(env, info, 6);
   if (fail(env, p0_q4_dequant((const void*)(uintptr_t)num(env, a[0]), (int64_t)num(env, a[1]), (int64_t)num(env, a[2]),
@@ -369,7 +381,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"fillRandn", FillRandn}, {"version", Version}, {"recordBegin", RecordBegin}, {"recordEnd", RecordEnd},
       {"replay", Replay}, {"recordFree", RecordFree}, {"chainBegin", ChainBegin}, {"chainEnd", ChainEnd},
       {"chainRun", ChainRun}, {"chainStatus", ChainStatus}, {"chainFree", ChainFree},
-      {"rowstats", Rowstats}, {"normadd", Normadd}, {"argmaxM", ArgmaxM},
+      {"rowstats", Rowstats}, {"normadd", Normadd}, {"argmaxM", ArgmaxM}, {"uploadFile", UploadFile},
   };
   for (auto& f : fns) {
     napi_value v;

@@ -213,3 +213,119 @@ P.argmaxM(g, { mx: { buf: mx }, n: 300, M: 2, out: { buf: oM } });
     assert np.array_equal(rd("sn", np.uint32, M), sw.view(np.uint32))
     assert np.array_equal(rd("o1", np.uint32, 2), O.argmaxM(mx, n, 1))
     assert np.array_equal(rd("oM", np.uint32, 2 * M), O.argmaxM(mx, n, M))
+
+
+# ------------------------------------------------------------------------------------------------ PackStore
+def make_pack(root):
+    """A small pack directory in the reference's layout (engine/core/store.js): manifest.json + two shard files.
+    Shard "blk": a q4g32a.t64 weight [128][256] and a q8g64s.t64 weight [128][256] (the oracle's packers), each at a
+    256-aligned offset; shard "emb": a q4g32a.rows table [10][64] (per row: 32 code bytes, then 2 x (f16 scale, f16
+    min)) and a q8g64s.rows table [6][128] (per row: 128 int8 codes, then 2 f16 scales). Returns the expected
+    dequantised rows and the weight records."""
+    rng = np.random.default_rng(5)
+    wq4, _ = O.pack_q4(O.randn(128 * 256, 21, 0.05), 128, 256)
+    wq8, _ = O.pack_q8(O.randn(128 * 256, 22, 0.05), 128, 256)
+    blk = bytearray(wq4.tobytes())
+    blk += b"\0" * ((-len(blk)) % 256)
+    off8 = len(blk)
+    blk += wq8.tobytes()
+    # q4 rows: codes in [0, 16), fp16 scale > 0 and min; the value is fl32(q s + m)
+    q4c = rng.integers(0, 16, (10, 64)).astype(np.uint8)
+    q4s = np.abs(rng.standard_normal((10, 2))).astype(np.float16) * np.float16(0.05)
+    q4m = (-8 * q4s.astype(np.float32)).astype(np.float16)
+    rows4 = bytearray()
+    want4 = np.zeros((10, 64), np.float32)
+    for r in range(10):
+        rows4 += (q4c[r, 0::2] | (q4c[r, 1::2] << 4)).astype(np.uint8).tobytes()
+        for g in range(2):
+            rows4 += q4s[r, g].tobytes() + q4m[r, g].tobytes()
+            want4[r, 32 * g:32 * g + 32] = (q4c[r, 32 * g:32 * g + 32].astype(np.float64) * float(q4s[r, g])
+                                            + float(q4m[r, g])).astype(np.float32)
+    q8c = rng.integers(-128, 128, (6, 128)).astype(np.int8)
+    q8s = np.abs(rng.standard_normal((6, 2))).astype(np.float16) * np.float16(0.01)
+    rows8 = bytearray()
+    want8 = np.zeros((6, 128), np.float32)
+    for r in range(6):
+        rows8 += q8c[r].tobytes() + q8s[r].tobytes()
+        for g in range(2):
+            want8[r, 64 * g:64 * g + 64] = (q8c[r, 64 * g:64 * g + 64].astype(np.float64) * float(q8s[r, g])).astype(np.float32)
+    emb = bytes(rows4) + bytes(rows8)
+    (root / "blk.bin").write_bytes(bytes(blk))
+    (root / "emb.bin").write_bytes(emb)
+    manifest = {
+        "pack_version": "test-1",
+        "shards": [{"name": "blk", "file": "blk.bin", "bytes": len(blk)}, {"name": "emb", "file": "emb.bin", "bytes": len(emb)}],
+        "tensors": {
+            "w.q4": {"shard": "blk", "offset": 0, "bytes": wq4.nbytes, "enc": "q4g32a.t64", "shape": [128, 256]},
+            "w.q8": {"shard": "blk", "offset": off8, "bytes": wq8.nbytes, "enc": "q8g64s.t64", "shape": [128, 256]},
+            "emb.q4": {"shard": "emb", "offset": 0, "bytes": len(rows4), "enc": "q4g32a.rows", "shape": [10, 64]},
+            "emb.q8": {"shard": "emb", "offset": len(rows4), "bytes": len(rows8), "enc": "q8g64s.rows", "shape": [6, 128]},
+        },
+    }
+    (root / "manifest.json").write_text(json.dumps(manifest))
+    return {"want4": want4, "want8": want8, "wq4": wq4, "wq8": wq8}
+
+
+def test_js_packstore_rows_files_and_errors(tmp_path):
+    """PackStore on the CPU: manifest, readRows of both row encodings (engine/core/store.js:275-301), readFile, and
+    the reference's error texts"""
+    pk = tmp_path / "pack"
+    pk.mkdir()
+    exp = make_pack(pk)
+    out = run_node(tmp_path, r"""
+const st = new P.PackStore({}, { dir: 'pack' });
+(async () => {
+  await st.init();
+  const r4 = await st.readRows('emb.q4', [3, 0, 9]), r8 = await st.readRows('emb.q8', [5, 1]);
+  fs.writeFileSync('r4.bin', Buffer.from(r4.buffer)); fs.writeFileSync('r8.bin', Buffer.from(r8.buffer));
+  const f = await st.readFile('emb');
+  const res = [f.byteLength];
+  const t = async (fn) => { try { await fn(); res.push('no error'); } catch (e) { res.push(e.message); } };
+  await t(() => st.upload('nope'));
+  await t(() => st.readRows('w.q4', [0]));
+  await t(() => st.uploadPart('emb', ['w.q4']));
+  console.log(JSON.stringify(res));
+})();
+""")
+    res = json.loads(out.strip().splitlines()[-1])
+    r4 = np.fromfile(str(tmp_path / "r4.bin"), np.float32).reshape(3, 64)
+    r8 = np.fromfile(str(tmp_path / "r8.bin"), np.float32).reshape(2, 128)
+    assert np.array_equal(r4, exp["want4"][[3, 0, 9]]) and np.array_equal(r8, exp["want8"][[5, 1]])
+    assert res[0] == (pk / "emb.bin").stat().st_size
+    assert res[1] == "unknown shard nope"
+    assert res[2] == "readRows: q4g32a.t64"
+    assert res[3] == "tensor w.q4 not in emb"
+
+
+@pytest.mark.gpu
+def test_js_packstore_upload_feeds_the_ops(tmp_path):
+    """a shard uploaded whole and a part upload both give tensor views that gemv reads as the reference's a.w"""
+    pk = tmp_path / "pack"
+    pk.mkdir()
+    exp = make_pack(pk)
+    x = O.randn(256, 23)
+    _save(tmp_path, x=x)
+    run_node(tmp_path, r"""
+const g = await_gpu();
+const b = fs.readFileSync('x.bin'), x = g.upload(new Uint8Array(b.buffer, b.byteOffset, b.length));
+const st = new P.PackStore(g, { dir: 'pack' });
+(async () => {
+  await st.init();
+  const h = await st.upload('blk'), part = await st.uploadPart('blk', ['w.q8']);
+  const outs = { q4: g.buffer(128 * 4), q8: g.buffer(128 * 4), q8p: g.buffer(128 * 4) };
+  P.gemv(g, { w: h.t('w.q4'), x: { buf: x }, N: 128, K: 256, y: { buf: outs.q4 } });
+  P.gemv(g, { w: h.t('w.q8'), x: { buf: x }, N: 128, K: 256, y: { buf: outs.q8 } });
+  P.gemv(g, { w: part.t('w.q8'), x: { buf: x }, N: 128, K: 256, y: { buf: outs.q8p } });
+  await g.done();
+  for (const k of Object.keys(outs)) fs.writeFileSync(k + '.out', Buffer.from(await g.read(outs[k], 0, 512)));
+  st.release(h); st.release(part);
+  console.log('ok');
+  g.freeAll(); g.device.destroy();
+})();
+""")
+    for key, w, enc in (("q4", exp["wq4"], 1), ("q8", exp["wq8"], 2), ("q8p", exp["wq8"], 2)):
+        got = np.fromfile(str(tmp_path / (key + ".out")), np.float32)
+        want = np.zeros(128, np.float32)
+        O.q4_gemv(capi.gemv_args(w=w.ctypes.data, w_enc=enc, w_rows=128, w_cols=256, x=x.ctypes.data, N=128, K=256,
+                                 y=want.ctypes.data))
+        assert rel_l2(got, want) <= 2e-5, key
