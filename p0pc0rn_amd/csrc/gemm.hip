@@ -9,14 +9,14 @@
 //    workspace, once per call, when X is not already fp16 rows the MFMA kernel can stream (bf16, lnmod, rms, or fp16
 //    rows that are not 16-byte aligned). The reference applies the prologue inside its tile loads; doing it once here
 //    instead of once per output-column block costs one streaming pass over X.
-//  * q4_gemm_kernel: a workgroup of 4 waves owns a 256 x 256 output tile; per 64-k step (two q4 groups) it
+//  * q4_gemm_kernel: a workgroup of 8 waves owns a 256 x 256 output tile; per 64-k step (two q4 groups) it
 //      - streams the fp16 X tile straight from global memory into LDS (global_load_lds_dwordx4: no registers, no ALU),
 //      - dequantises the W tile from its records exactly (fl16 of the fp32 value, the reference's own tile rounding,
 //        engine/ops/gemm.js:147-148) into LDS,
-//      - runs 4 x 4 blocks of v_mfma_f32_32x32x16_f16 per wave over its 128 x 128 sub-tile (fp32 accumulators in AGPRs),
-//    with two LDS stages: the next step's X loads and W records are in flight during this step's MFMAs.
-//    LDS rows are 128 B (64 k); the 16-byte chunk c of row r sits at position c ^ (r & 7), which makes the direct-load
-//    writes, the dequant writes and the MFMA fragment reads all bank-conflict free.
+//      - runs 4 x 2 blocks of v_mfma_f32_32x32x16_f16 per wave over its 128 x 64 sub-tile (fp32 accumulators),
+//    with two LDS stages: the next step's X loads and the next-but-one step's W records are in flight during this
+//    step's MFMAs. LDS rows are 128 B (64 k); the 16-byte chunk c of row r sits at a swizzled position (swz_key), which
+//    makes the direct-load writes, the dequant writes and the MFMA fragment reads all bank-conflict free.
 #include "common.hpp"
 
 namespace p0 {
@@ -56,9 +56,12 @@ __device__ __forceinline__ _Float16 to_h(float v) { return (_Float16)v; }   // R
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
   return (uint32_t)__builtin_bit_cast(uint16_t, to_h(lo)) | ((uint32_t)__builtin_bit_cast(uint16_t, to_h(hi)) << 16);
 }
-// byte offset of the 16-byte chunk c (0..7) of tile row r. LDS serves a 16-byte access 16 lanes per pass (64 banks);
-// consecutive rows r..r+15 reading one logical chunk land in distinct banks when position = c ^ ((r >> 1) & 7)
-__device__ __forceinline__ int swz_key(int r) { return (r >> 1) & 7; }
+// byte offset of the 16-byte chunk c (0..7) of tile row r. The position c ^ key(r) puts one logical chunk of any 8
+// consecutive rows into 8 distinct positions, and of any 16 consecutive rows into distinct (row parity, position)
+// pairs, so both ways an LDS can serve a 16-byte access (8 lanes x 128 B or 16 lanes x 256 B per pass) are free of bank
+// conflicts (the SQ_LDS_BANK_CONFLICT counter reads 0 on MI355X; (r >> 1) & 7 read 20% of the LDS-active cycles). The key
+// depends on r mod 32 only: the 32-row blocks of a wave's fragments share one offset.
+__device__ __forceinline__ int swz_key(int r) { return (r ^ ((r >> 3) & 3)) & 7; }
 __device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ swz_key(r)) << 4); }
 
 // ------------------------------------------------------------------------------------------------ X staging
