@@ -201,6 +201,8 @@ int p0_gemv_tune(int knob, int value);
 typedef struct {
   int32_t n_ops, m, workgroups, waves_per_workgroup;
   int64_t lds_bytes;
+  int32_t mailboxes;   /* ops that take their input from the previous op's mailbox (p0_chain_tune knob 7) */
+  int32_t reserved;
 } p0_chain_info_t;
 int p0_chain_begin(void);
 int p0_chain_end(void** chain_out);
@@ -215,8 +217,10 @@ int p0_chain_free(void* chain);
  * default: M = 1 chains run on the pipelined kernel, whose loader waves stream every op's weights into an LDS ring
  * ops ahead of the arithmetic; other chains stage the ops whose share fits), 0 = every op streams its weights after
  * the wait; knob 5: loader waves of the pipelined kernel that stream (1..4, default 2); knob 6: LDS slots each loader
- * keeps in flight (1 or 2, default 2).
- * Knobs 0-1 and 4-6 apply to chains begun afterwards, 2-3 to runs. value < 0 only queries (knobs 0-2 also ignore 0);
+ * keeps in flight (1 or 2, default 2); knob 7: 1 = mailbox hand-offs in pipelined chains (the default: an op whose only
+ * input is the previous op's output polls that output, tagged with the run, instead of the previous op's completion
+ * flags), 0 = every op waits for the flags.
+ * Knobs 0-1 and 4-7 apply to chains begun afterwards, 2-3 to runs. value < 0 only queries (knobs 0-2 also ignore 0);
  * returns the previous value. */
 int p0_chain_tune(int knob, int value);
 

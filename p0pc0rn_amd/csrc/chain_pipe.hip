@@ -241,11 +241,12 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
   auto wait_slot = [&](int q) {
     while (ctl_ld(lctl + kCtlFull + q % kRing) != (unsigned)q + 1) __builtin_amdgcn_s_sleep(0);
   };
-  // the G flags at f hold this run's tag (wave c == 0 polls); false in every compute thread if the wait gave up
-  auto wait_flags = [&](const unsigned* f) -> bool {
+  // the G flags at f (and at f2, when not null) hold this run's tag (wave c == 0 polls); false in every compute
+  // thread if the wait gave up
+  auto wait_flags = [&](const unsigned* f, const unsigned* f2) -> bool {
     if (c == 0) {
       int go = spin_limit >= 0;   // spin_limit < 0: every wait gives up at once (tests of the timed-out path)
-      for (int spins = 0; go && !flags_set(f, G, tag, lane); ++spins) {
+      for (int spins = 0; go && !(flags_set(f, G, tag, lane) && (!f2 || flags_set(f2, G, tag, lane))); ++spins) {
         if (spins >= spin_limit || (spins % 64 == 63 && ld_coh(timed_out))) go = 0;
         else __builtin_amdgcn_s_sleep(1);
       }
@@ -260,6 +261,57 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
     cbar();
     return ctl_ld(lctl + kCtlGo) != 0;
   };
+  // x' of groups [g0, g1) from the previous op's mailbox: each compute thread polls its own elements until all of them
+  // carry this run's tag (bounded like wait_flags), then writes x' and the group sums as stage_x does (raw prologue).
+  // The poll is the load: the hand-off costs one memory round trip instead of a flag round trip and then an x load.
+  auto stage_mbx = [&](const GemvP& p, int g0, int g1, int gps) -> bool {
+    constexpr int U = 4, NT = 64 * kPC;
+    const int KL = gps * 32, kb = g0 * 32, ke = g1 * 32;
+    int go = spin_limit >= 0;
+    for (int i0 = 0; go && i0 < KL; i0 += U * NT) {
+      unsigned long long w[U];
+      for (int spins = 0;; ++spins) {
+        bool ok = true;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int k = min(kb + i0 + u * NT + tc, ke - 1);   // past the slice: its last element (in bounds, unused)
+          w[u] = __hip_atomic_load(P0_GLOBAL(unsigned long long, const_cast<unsigned long long*>(p.mbxIn + k)),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) ok = ok && (unsigned)(w[u] >> 32) == tag;
+        if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+        if (!go || spins >= spin_limit || (spins % 64 == 63 && ld_coh(timed_out))) {
+          go = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (!go) break;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int kl = i0 + u * NT + tc;
+        const float v = kb + kl < ke ? __uint_as_float((unsigned)w[u]) : 0.0f;
+        const float gsum = sum32(v);
+        if (kl < KL) {
+          xs[kl] = (kl & 1) ? v * 0.0625f : v;   // kb is even: k and kl share parity
+          if ((lane & 31) == 0) xsum[kl >> 5] = gsum;
+        }
+      }
+    }
+    if (!go && lane == 0) {
+      atomicOr(timed_out, 1u);
+      ctl_st(lctl + kCtlStop, 1u);   // the loaders leave their waits
+      ctl_st(lctl + kCtlGo, 0u);
+    }
+    cbar();
+    return ctl_ld(lctl + kCtlGo) != 0;
+  };
+  // this op's rows, with their values as stored, into its mailbox (after the epilogue's own stores)
+  auto post_mbx = [&](const GemvP& p, int n, float v) {
+    __hip_atomic_store(P0_GLOBAL(unsigned long long, p.mbxOut + n),
+                       ((unsigned long long)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
   const unsigned* const mine = flags + (size_t)(b % kFlagCopies) * n_ops * Gp;   // this XCD's copy
   int q0 = 0;
   bool abandon = false;
@@ -267,14 +319,23 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
     const GemvP& p = ops[i];
     const Share s = share_of(p, b, G);
     if (s.nu > 0) {
-      if (i > 0 && !wait_flags(mine + (size_t)(i - 1) * Gp)) {
-        abandon = true;
-        break;
+      if (p.mbxIn) {
+        // op i - 1's completion is not waited for here: its mailbox says its outputs are all written. Op i + 1 waits
+        // for op i - 1's flags with op i's (GemvP::flags2), so every later op still sees every earlier op complete.
+        if (!stage_mbx(p, s.gA, s.gA + s.ngs, s.nh * 32)) {
+          abandon = true;
+          break;
+        }
+      } else {
+        if (i > 0 && !wait_flags(mine + (size_t)(i - 1) * Gp, p.flags2 ? mine + (size_t)(i - 2) * Gp : nullptr)) {
+          abandon = true;
+          break;
+        }
+        // op i - 1's outputs are read with coherent loads: no L2 invalidate
+        if (p.coh & 1) stage_x<1, true>(p, s.gA, s.gA + s.ngs, s.nh * 32, xs, xsum, tc, 64 * kPC);
+        else stage_x<1, false>(p, s.gA, s.gA + s.ngs, s.nh * 32, xs, xsum, tc, 64 * kPC);
+        cbar();
       }
-      // op i - 1's outputs are read with coherent loads: no L2 invalidate
-      if (p.coh & 1) stage_x<1, true>(p, s.gA, s.gA + s.ngs, s.nh * 32, xs, xsum, tc, 64 * kPC);
-      else stage_x<1, false>(p, s.gA, s.gA + s.ngs, s.nh * 32, xs, xsum, tc, 64 * kPC);
-      cbar();
       const int nrp = s.nu * s.nrb * s.parts;
       if (s.spread) {
         // every compute lane takes pair tc = 16 group + row of each slot; a part's slots are its halves
@@ -314,8 +375,9 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
           }
           const int n = share_row(p, s, G, j, 0, 0) + rr;
           if (tc < rows) {
-            if (p.coh & 2) epilogue<true>(p, s.split, 0, n >> 6, n & 63, v0, v1);
-            else epilogue<false>(p, s.split, 0, n >> 6, n & 63, v0, v1);
+            const float yv = (p.coh & 2) ? epilogue<true>(p, s.split, 0, n >> 6, n & 63, v0, v1)
+                                         : epilogue<false>(p, s.split, 0, n >> 6, n & 63, v0, v1);
+            if (p.mbxOut) post_mbx(p, n, yv);
           }
         }
       } else {
@@ -359,8 +421,9 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
           const float v0 = wred[min(lane, rows - 1)], v1 = s.parts == 2 ? wred[64 + min(lane, rows - 1)] : 0.0f;
           const int n = share_row(p, s, G, j, 0, 0) + lane;
           if (lane < rows || p.epi == P0_EPI_SOFTCAP) {
-            if (p.coh & 2) epilogue<true>(p, s.split, 0, n >> 6, n & 63, v0, v1);
-            else epilogue<false>(p, s.split, 0, n >> 6, n & 63, v0, v1);
+            const float yv = (p.coh & 2) ? epilogue<true>(p, s.split, 0, n >> 6, n & 63, v0, v1)
+                                         : epilogue<false>(p, s.split, 0, n >> 6, n & 63, v0, v1);
+            if (p.mbxOut && lane < rows) post_mbx(p, n, yv);
           }
           __builtin_amdgcn_s_waitcnt(0xC07F);
           __builtin_amdgcn_wave_barrier();   // wred is rewritten by this wave's next unit
@@ -375,7 +438,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
   }
   if (abandon) return;
   // every workgroup has read this run's tag once all have published op 0: store it back for the next run
-  if (b == 0 && wait_flags(flags + 0) && tc == 0) st_coh(st, tag);
+  if (b == 0 && wait_flags(flags + 0, nullptr) && tc == 0) st_coh(st, tag);
 }
 
 chain_kernel_t pipe_chain_kernel() { return q4_chain_pipe_kernel; }

@@ -111,6 +111,7 @@ static int g_chain_split_gpw = 16;      // a wave share above this many groups s
 static int g_chain_spin = 1 << 22;      // polls before a chain wait gives up (about 0.3 s)
 static int g_chain_force_give_up = 0;   // tests: every wait gives up at once
 static int g_chain_stage = 1;           // staged ops (weights copied to LDS before the wait) where they fit
+static int g_chain_mbx = 1;             // pipelined chains: mailbox hand-offs where an op reads the previous op's output
 static int g_pipe_loaders = 2;          // pipelined chain: loader waves that stream
 static int g_pipe_depth = 2;            // pipelined chain: slots in flight per loader wave
 static constexpr size_t kChainLds = 64 * 1024;
@@ -130,6 +131,7 @@ struct ChainExec {
   int n_ops, M, W, grid;
   size_t lds;
   chain_kernel_t kernel;
+  int mailboxes;     // ops that take their input from a mailbox
 };
 static ChainBuild* g_chain = nullptr;
 static std::map<unsigned*, size_t> g_state_bytes;   // sizes of the uncached state blocks
@@ -200,6 +202,43 @@ static void mark_coherence(std::vector<GemvP>& ops, int M) {
     }
     ops[i].coh = c;
   }
+}
+
+// Mailbox hand-offs of a pipelined M = 1 chain (chain_pipe.hip). Op i takes its x from op i - 1's mailbox when
+//  * op i - 1 has one split and a store or geglu epilogue (it writes final values, all N of them), and did not take its
+//    own input from a mailbox,
+//  * op i has the raw prologue and its x[0, K) lies inside op i - 1's outputs (its only input is op i - 1's output),
+//  * op i writes nothing op i - 1 writes (no write-after-write between the two: op i does not wait for op i - 1's
+//    stores to be acknowledged, only for its mailbox).
+// Op i + 1 then waits for op i - 1's flags together with op i's. The mailboxes live in the chain state after the
+// flags, 2 words per producer row; returns the words they take and sets mb_out / mb_in (word offsets, -1: none).
+static size_t plan_mailboxes(std::vector<GemvP>& ops, std::vector<int64_t>& mb_out, std::vector<int64_t>& mb_in) {
+  const size_t n = ops.size();
+  mb_out.assign(n, -1);
+  mb_in.assign(n, -1);
+  size_t words = 0;
+  for (size_t i = 1; i < n; ++i) {
+    const GemvP& pr = ops[i - 1];
+    GemvP& c = ops[i];
+    if (mb_in[i - 1] >= 0 || pr.nsplit != 1 || (pr.epi != P0_EPI_STORE && pr.epi != P0_EPI_GEGLU)) continue;
+    if (c.pro != P0_PRO_RAW || c.enc != P0_ENC_Q4G32A_T64) continue;
+    const intptr_t d = (intptr_t)(const void*)(c.X + c.rowB) - (intptr_t)(const void*)pr.Y;
+    if (d < 0 || d % 4 || d / 4 + c.K > pr.N) continue;
+    std::vector<Span> rp, wp, rc, wc;
+    op_spans(pr, 1, rp, wp);
+    op_spans(c, 1, rc, wc);
+    bool waw = false;
+    for (const Span& a : wc)
+      for (const Span& b2 : wp) waw = waw || (a.a < b2.b && b2.a < a.b);
+    if (waw) continue;
+    if (mb_out[i - 1] < 0) {
+      mb_out[i - 1] = (int64_t)words;
+      words += 2 * (size_t)pr.N;
+    }
+    mb_in[i] = mb_out[i - 1] + 2 * (d / 4);
+    if (i + 1 < n) ops[i + 1].flags2 = 1;
+  }
+  return words;
 }
 
 // plan of one op inside a chain: all W waves of a workgroup busy (tgw = W / kw), one K-slice per split unless the op
@@ -542,6 +581,8 @@ extern "C" int p0_chain_end(void** out) {
     }
   }
   mark_coherence(cb->ops, cb->M);
+  std::vector<int64_t> mb_out, mb_in;
+  const size_t mb_words = k == pipe_chain_kernel() && g_chain_mbx ? plan_mailboxes(cb->ops, mb_out, mb_in) : 0;
   auto* ex = new ChainExec{};
   ex->n_ops = (int)cb->ops.size();
   ex->M = cb->M;
@@ -554,11 +595,19 @@ extern "C" int p0_chain_end(void** out) {
     ex->pipe_cfg[1] = g_pipe_depth;
   }
   // chain state: last tag, timed out, the workgroups' lines and the completion counters (one 128-byte line each)
-  const size_t words = chain_state_words((int)cb->ops.size(), grid);
+  const size_t mb_base = (chain_state_words((int)cb->ops.size(), grid) + 63) & ~(size_t)63;   // 256-byte aligned
+  const size_t words = mb_words ? mb_base + mb_words : chain_state_words((int)cb->ops.size(), grid);
   const size_t ob = cb->ops.size() * sizeof(GemvP), sb = words * sizeof(unsigned);
   ex->st_words = words;
   hipError_t e = hipMalloc((void**)&ex->ops, ob);
   if (e == hipSuccess) e = state_alloc(&ex->st, sb);
+  if (e == hipSuccess && mb_words) {
+    for (size_t i = 0; i < cb->ops.size(); ++i) {
+      if (mb_out[i] >= 0) cb->ops[i].mbxOut = (unsigned long long*)(ex->st + mb_base + mb_out[i]);
+      if (mb_in[i] >= 0) cb->ops[i].mbxIn = (const unsigned long long*)(ex->st + mb_base + mb_in[i]);
+      if (mb_in[i] >= 0) ++ex->mailboxes;
+    }
+  }
   if (e == hipSuccess) e = hipMemcpy(ex->ops, cb->ops.data(), ob, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemset(ex->st, 0, sb);
   if (e == hipSuccess && ex->pipe_cfg[0])
@@ -612,6 +661,8 @@ extern "C" int p0_chain_info(void* chain, p0_chain_info_t* out) {
   out->workgroups = ex->grid;
   out->waves_per_workgroup = ex->W;
   out->lds_bytes = (int64_t)ex->lds;
+  out->mailboxes = ex->mailboxes;
+  out->reserved = 0;
   return P0_OK;
 }
 
@@ -627,8 +678,15 @@ extern "C" int p0_chain_free(void* chain) {
 
 // chain knobs: 0 = waves per workgroup for M = 1 (8 or 16), 1 = largest wave share (groups) before K is split
 // across workgroups, 2 = polls before a wait gives up, 3 = 1: every wait gives up at once (tests), 4 = staged ops
-// (1, the default) or none (0). Returns the previous value; a value < 0 only reads (knobs 3 and 4 also take 0).
+// (1, the default) or none (0), 5 / 6 = loader waves / slots in flight of the pipelined kernel, 7 = mailbox hand-offs
+// in pipelined chains (1, the default) or none (0). Returns the previous value; a value < 0 only reads (knobs 3, 4
+// and 7 also take 0).
 extern "C" int p0_chain_tune(int knob, int value) {
+  if (knob == 7) {
+    const int old = g_chain_mbx;
+    if (value >= 0) g_chain_mbx = value ? 1 : 0;
+    return old;
+  }
   if (knob == 3) {
     const int old = g_chain_force_give_up;
     if (value >= 0) g_chain_force_give_up = value ? 1 : 0;

@@ -67,6 +67,12 @@ struct GemvP {
   int swoff;                  // LDS byte offset of the staged weights
   int enc;                    // P0_ENC_Q4G32A_T64, or P0_ENC_Q8G64S_T64 (gemv_q8.hip)
   int mrows;                  // rows of x (M)
+  // pipelined M = 1 chains: an op whose only input is the previous op's output takes it from that op's mailbox, one
+  // 64-bit word per output row (run tag << 32 | the value's bits) in the chain state, instead of waiting for the
+  // previous op's completion flags and then loading x: one memory round trip instead of two
+  unsigned long long* mbxOut;       // this op's mailbox (row n at n), or null
+  const unsigned long long* mbxIn;  // x[k] of this op at mbxIn[k], or null
+  int flags2;                       // 1: op i also waits for op i - 2's flags (op i - 1 took its input from a mailbox)
 };
 
 __device__ __forceinline__ float gelu_tanh(float v) {   // engine/llm/lops.js:26
@@ -258,14 +264,18 @@ __device__ __forceinline__ void wave_argmax(float& v, int& r) {
   }
 }
 
-// the epilogue of one wave for x row m: tot0 = row sums of tile0 (gate tile for a geglu), tot1 = the up tile's
+// the epilogue of one wave for x row m: tot0 = row sums of tile0 (gate tile for a geglu), tot1 = the up tile's;
+// returns the value stored at row n of y
 template <bool COH>
-__device__ __forceinline__ void epilogue(const GemvP& p, int split, int m, int tile0, int lane, float tot0, float tot1) {
+__device__ __forceinline__ float epilogue(const GemvP& p, int split, int m, int tile0, int lane, float tot0, float tot1) {
   const int n = tile0 * 64 + lane;
   if (p.epi == P0_EPI_STORE) {
     stf<COH>(&p.Y[split * p.ldy + m * p.ldm + n], tot0);
+    return tot0;
   } else if (p.epi == P0_EPI_GEGLU) {
-    stf<COH>(&p.Y[m * p.ldm + n], gelu_tanh(tot0) * tot1);
+    const float v = gelu_tanh(tot0) * tot1;
+    stf<COH>(&p.Y[m * p.ldm + n], v);
+    return v;
   } else {
     float v = p.cap * tanhf(fminf(15.0f, fmaxf(-15.0f, tot0 / p.cap)));
     stf<COH>(&p.Y[m * p.ldm + n], v);
@@ -276,6 +286,7 @@ __device__ __forceinline__ void epilogue(const GemvP& p, int split, int m, int t
       stf<COH>(&p.MX[o], v);
       stf<COH>(&p.MX[o + 1], __int_as_float(tile0 * 64 + r));
     }
+    return v;
   }
 }
 

@@ -141,6 +141,8 @@ def test_chain_matches_oracle(dev, M, gemvM):
     info = ch.info()
     print("chain", info, flush=True)
     assert info["n_ops"] == 6 and info["m"] == M
+    if M == 1 and info["waves_per_workgroup"] == 12:
+        assert info["mailboxes"] == 2   # o takes qkv's output, down the geglu output (the others: flags)
     s.reset_outputs()
     ch.run()
     assert not ch.status()
@@ -235,10 +237,10 @@ def test_chain_layers_reuse_buffers(dev):
         buf.free()
 
 
-@pytest.mark.parametrize("knobs", [{0: 8}, {4: 0}, {1: 2, 4: 0}, {0: 8, 4: 0}])
+@pytest.mark.parametrize("knobs", [{0: 8}, {4: 0}, {1: 2, 4: 0}, {0: 8, 4: 0}, {7: 0}])
 def test_chain_other_plans(dev, knobs):
-    """8-wave workgroups; every op streamed (no LDS staging); and streamed ops with K split across workgroups inside
-    the chain (cross-workgroup reduction + counts)"""
+    """8-wave workgroups; every op streamed (no LDS staging); streamed ops with K split across workgroups inside
+    the chain (cross-workgroup reduction + counts); the pipelined chain without mailbox hand-offs"""
     old = {k: capi.chain_tune(k, v) for k, v in knobs.items()}
     try:
         s = MiniStep(seed=41 + sum(knobs))
@@ -371,3 +373,78 @@ def test_chain_errors(dev):
     ch.free()
     for v in (w, x, y):
         v.free()
+
+
+def test_chain_mailboxes_match_flags(dev):
+    """Mailbox hand-offs (an op polls the previous op's tagged outputs instead of its completion flags) compute the
+    same bits as the flag hand-offs, run after run: the x values an op stages are the same floats either way. Checked
+    over the mini step (two store -> raw and geglu -> raw hand-offs, one of them into a 2-split op) and over a chain of
+    layers that read and rewrite the same two buffers (every other op a mailbox consumer, the rest wait for two ops'
+    flags)."""
+    s = MiniStep(seed=61)
+    old = capi.chain_tune(7, 1)
+    try:
+        ch_m = s.make_chain()
+        capi.chain_tune(7, 0)
+        ch_f = s.make_chain()
+    finally:
+        capi.chain_tune(7, old)
+    im, iff = ch_m.info(), ch_f.info()
+    print("mailbox chain", im, "flag chain", iff, flush=True)
+    if im["waves_per_workgroup"] != 12:
+        pytest.skip("this device plans the general chain kernel (mailboxes are a pipelined-chain feature)")
+    assert im["mailboxes"] == 2 and iff["mailboxes"] == 0
+    res = []
+    for ch in (ch_f, ch_m, ch_m, ch_f, ch_m):
+        s.reset_outputs()
+        ch.run()
+        assert not ch.status()
+        res.append(s.read())
+    s.check_against_oracle(res[1], "mailbox chain")
+    for r in res[1:]:
+        for k in res[0]:
+            assert np.array_equal(res[0][k].view(np.uint32), r[k].view(np.uint32)), k
+    ch_m.free()
+    ch_f.free()
+    s.free()
+
+    D, L = 512, 5
+    ws = [_w(D, D, 300 + i) for i in range(2 * L)]
+    wd = [capi.to_device(w) for w in ws]
+    a0 = O.randn(D, 301)
+    a, b = capi.to_device(a0), capi.Buffer(4 * D)
+
+    def enqueue():
+        for l in range(L):
+            capi.q4_gemv(capi.gemv_args(w=wd[2 * l], w_rows=D, w_cols=D, x=a, N=D, K=D, y=b))
+            capi.q4_gemv(capi.gemv_args(w=wd[2 * l + 1], w_rows=D, w_cols=D, x=b, N=D, K=D, y=a))
+
+    old = capi.chain_tune(7, 1)
+    try:
+        ch_m = capi.chain(enqueue)
+        capi.chain_tune(7, 0)
+        ch_f = capi.chain(enqueue)
+    finally:
+        capi.chain_tune(7, old)
+    assert ch_m.info()["mailboxes"] == L and ch_f.info()["mailboxes"] == 0
+    outs = []
+    for ch in (ch_f, ch_m, ch_m):
+        a.upload(a0)
+        ch.run()
+        assert not ch.status()
+        outs.append(a.read(np.float32, D))
+    want = a0.copy()
+    for i in range(2 * L):
+        y = np.zeros(D, np.float32)
+        O.q4_gemv(capi.gemv_args(w=ws[i].ctypes.data, w_rows=D, w_cols=D, x=want.ctypes.data, N=D, K=D,
+                                 y=y.ctypes.data))
+        want = y
+    r = rel_l2(outs[1], want)
+    print(f"10 dependent GEMVs through mailboxes: rel_l2 {r:.3e}", flush=True)
+    assert r <= 1e-4
+    for o in outs[1:]:
+        assert np.array_equal(outs[0].view(np.uint32), o.view(np.uint32))
+    ch_m.free()
+    ch_f.free()
+    for buf in wd + [a, b]:
+        buf.free()
