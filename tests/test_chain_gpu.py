@@ -448,3 +448,84 @@ def test_chain_mailboxes_match_flags(dev):
     ch_f.free()
     for buf in wd + [a, b]:
         buf.free()
+
+
+def _both_chains(enqueue):
+    """the same ops planned with and without mailbox hand-offs"""
+    old = capi.chain_tune(7, 1)
+    try:
+        ch_m = capi.chain(enqueue)
+        capi.chain_tune(7, 0)
+        ch_f = capi.chain(enqueue)
+    finally:
+        capi.chain_tune(7, old)
+    return ch_m, ch_f
+
+
+def _gemv(w, N, K, x, y, **kw):
+    capi.q4_gemv(capi.gemv_args(w=w, w_rows=kw.pop("w_rows", N), w_cols=K, x=x, N=N, K=K, y=y, **kw))
+
+
+def test_chain_mailbox_cases(dev):
+    """Which hand-offs take a mailbox, and that each computes what the flag hand-off computes:
+      a. op 1 reads x at an offset inside op 0's output (rows 128..383 of 384): mailbox;
+      b. op 3 writes into op 2's output (write after write): flags;
+      c. op 5, 16 K-splits, reads op 4's output, which op 4 writes with large per-workgroup shares (one wave per
+         64-row unit): mailbox;
+      d. op 7 reads x running past op 6's output (rows 64..319 of a 256-row output): flags.
+    Every output is compared bit for bit between the two chains, and (a) and (c) with the oracle."""
+    D = 256
+    ws = {"w384": _w(384, D, 401), "w256": _w(D, D, 402), "wbig": _w(32768, 2048, 403), "wback": _w(2048, 32768, 404)}
+    dv = {k: capi.to_device(v) for k, v in ws.items()}
+    x0 = O.randn(2048, 405)
+    tail = O.randn(512, 406)
+    x = capi.to_device(x0)
+    sizes = {"p384": 384, "o1": D, "bB": 512, "big": 32768, "back": 16 * 2048, "o2": 512, "o3": D}
+    b = {k: capi.Buffer(4 * n) for k, n in sizes.items()}
+
+    def enqueue():
+        _gemv(dv["w384"], 384, D, x, b["p384"])                                   # 0
+        _gemv(dv["w256"], D, D, b["p384"], b["o1"], x_rowB=128)                   # 1 (a)
+        _gemv(dv["w384"], 384, D, b["o1"], b["bB"])                               # 2
+        _gemv(dv["w256"], D, D, b["bB"], b["bB"].ptr + 4 * 256)                   # 3 (b)
+        _gemv(dv["wbig"], 32768, 2048, x, b["big"])                               # 4
+        _gemv(dv["wback"], 2048, 32768, b["big"], b["back"], kPer=2048)           # 5 (c)
+        _gemv(dv["w256"], D, D, b["o1"], b["o2"])                                 # 6
+        _gemv(dv["w256"], D, D, b["o2"].ptr + 4 * 64, b["o3"])                    # 7 (d)
+
+    ch_m, ch_f = _both_chains(enqueue)
+    im = ch_m.info()
+    print("mailbox chain", im, flush=True)
+    if im["waves_per_workgroup"] != 12:
+        pytest.skip("this device plans the general chain kernel (mailboxes are a pipelined-chain feature)")
+    assert im["mailboxes"] == 2 and ch_f.info()["mailboxes"] == 0
+    outs = []
+    for ch in (ch_f, ch_m, ch_m):
+        for k in b:
+            b[k].fill_u32(NAN)
+        b["o2"].upload(tail)   # rows 256.. of o2 are read by op 7 and written by no op
+        ch.run()
+        assert not ch.status()
+        outs.append({k: b[k].read(np.float32) for k in b})
+    for r in outs[1:]:
+        for k in b:
+            assert np.array_equal(outs[0][k].view(np.uint32), r[k].view(np.uint32)), k
+    got = outs[1]
+    for k in b:
+        assert np.all(np.isfinite(got[k])), k
+
+    def ref(w, N, K, xin, kPer=0, nsplit=1):
+        y = np.zeros(N * nsplit, np.float32)
+        xin = np.ascontiguousarray(xin, np.float32)
+        O.q4_gemv(capi.gemv_args(w=ws[w].ctypes.data, w_rows=N, w_cols=K, x=xin.ctypes.data, N=N, K=K,
+                                 y=y.ctypes.data, kPer=kPer))
+        return y
+    _check(got["p384"], ref("w384", 384, D, x0[:D]), "op 0")
+    _check(got["o1"], ref("w256", D, D, got["p384"][128:384]), "op 1 (mailbox at an offset)")
+    _check(got["big"], ref("wbig", 32768, 2048, x0), "op 4 (large shares)")
+    _check(got["back"], ref("wback", 2048, 32768, got["big"], kPer=2048, nsplit=16), "op 5 (mailbox, 16 splits)")
+    _check(got["o3"], ref("w256", D, D, got["o2"][64:320]), "op 7 (flags: x past the producer's rows)")
+    ch_m.free()
+    ch_f.free()
+    for buf in list(dv.values()) + [x] + list(b.values()):
+        buf.free()
