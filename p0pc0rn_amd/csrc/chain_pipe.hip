@@ -81,6 +81,7 @@ __device__ __forceinline__ void ctl_add(lds_u32* a, unsigned v) {
 struct Share {
   int nu, first, nrb, parts, nh, ngs, split, gA, nslot, spread;
 };
+template <bool Q8>
 __device__ __forceinline__ Share share_of(const GemvP& p, int b, int G) {
   Share s;
   const int pos = stage_pos(b, G);
@@ -89,9 +90,11 @@ __device__ __forceinline__ Share share_of(const GemvP& p, int b, int G) {
   s.nrb = p.snrb;
   s.parts = p.epi == P0_EPI_GEGLU ? 2 : 1;
   s.split = s.first % p.nsplit;   // every unit of a share has this split (the host checks)
-  s.gA = s.split * (p.kPer >> 5);
-  s.ngs = (min(p.K, (s.split + 1) * p.kPer) >> 5) - s.gA;
-  s.nh = (s.ngs + 31) >> 5;
+  // groups of the split (32 k for q4g32a.t64, 64 k for q8g64s.t64) and slots per 16-row part (32 or 8 groups each)
+  const int gsh = Q8 && p.enc == P0_ENC_Q8G64S_T64 ? 6 : 5;
+  s.gA = s.split * (p.kPer >> gsh);
+  s.ngs = (min(p.K, (s.split + 1) * p.kPer) >> gsh) - s.gA;
+  s.nh = gsh == 6 ? (s.ngs + 7) >> 3 : (s.ngs + 31) >> 5;
   s.nslot = s.nu * s.nrb * s.parts * s.nh;
   s.spread = p.sngp;   // the host's choice: 1 = all compute waves on every slot (the share fits the ring), 0 = a wave per unit
   return s;
@@ -117,11 +120,31 @@ __device__ __forceinline__ int slot_index(const Share& s, int j, int si) {   // 
   const int R = j / kPC, nw = min(kPC, s.nu - kPC * R);
   return R * kPC * S + si * nw + (j - kPC * R);
 }
+// q8g64s.t64 arithmetic: sum over 16 k of (code + 128) x' (the codes' sign bits flipped make them unsigned bytes,
+// which convert with one instruction each; the group's 128 sum x' is taken off after the quarters are added)
+__device__ __forceinline__ float dot16_q8(const u32x4 q, const float* __restrict__ x) {
+  const float4* x4 = (const float4*)x;
+  const uint32_t u[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u};
+  float da = 0.0f, db = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float4 xv = x4[w];
+    da = __builtin_fmaf((float)(u[w] & 0xFFu), xv.x, da);
+    db = __builtin_fmaf((float)((u[w] >> 8) & 0xFFu), xv.y, db);
+    da = __builtin_fmaf((float)((u[w] >> 16) & 0xFFu), xv.z, da);
+    db = __builtin_fmaf((float)(u[w] >> 24), xv.w, db);
+  }
+  return da + db;
+}
+__device__ __forceinline__ float h2f_u16(const uint8_t* p) { return (float)*(const _Float16*)p; }
+
 // first weight row of part (unit j, block r, part pt) of a share
 __device__ __forceinline__ int share_row(const GemvP& p, const Share& s, int G, int j, int r, int pt) {
   return ((s.first + j * G) / p.nsplit * s.nrb + r) * kStageRows + (pt ? p.N : 0);
 }
 
+// Q8: the instantiation for chains that hold q8g64s.t64 ops (the q4-only one carries none of their code)
+template <bool Q8>
 __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __restrict__ ops, int n_ops,
                                                                  unsigned* __restrict__ st, int spin_limit) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
@@ -161,7 +184,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
         for (int k = 0; k < (int)(sizeof(GemvP) / 4); k += 16) t ^= pw[k];
         asm volatile("" : : "s"(t));
       }
-      const Share s = share_of(p, b, G);
+      const Share s = share_of<Q8>(p, b, G);
       const int nl = s.spread ? nls : kPL;
       const int k0 = wv < nl ? ((wv - q0) % nl + nl) % nl : s.nslot;
       for (int k = k0; k < s.nslot; k += nl) {
@@ -185,9 +208,27 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
         slot_of(s, k, j, si);
         const int h = si % s.nh, rest = si / s.nh, pt = rest % s.parts, r = rest / s.parts;
         const int n = share_row(p, s, G, j, r, pt);
-        const uint8_t* tb = p.w + ((int64_t)(n >> 6) * p.wG + s.gA) * 1280;
         const int r0 = n & 63, glast = s.ngs - 1;
         uint8_t* const slot = lds + pos * kSlotB;
+        if (Q8 && p.enc == P0_ENC_Q8G64S_T64) {
+          // q8g64s.t64 slot: 16 rows x 8 groups of 64 k. Codes [8 groups][16 rows][64 B] (a group's 16 rows are 1 KB
+          // of one record), then scales [8 groups][16 rows][2 B]; the scale load is issued twice so that every slot
+          // takes 10 loads, as the vmcnt arithmetic below assumes
+          const uint8_t* tb = p.w + ((int64_t)(n >> 6) * p.wG + s.gA) * 4224;
+#pragma unroll
+          for (int ci = 0; ci < 8; ++ci) {
+            const int g = min(8 * h + ci, glast);
+            __builtin_amdgcn_global_load_lds((const void*)(tb + (int64_t)g * 4224 + r0 * 64 + lane * 16),
+                                             (__attribute__((address_space(3))) void*)(slot + ci * 1024), 16, 0, 0);
+          }
+          const int g = min(8 * h + ((lane >> 1) & 7), glast);   // lane: group (lane / 2) % 8, half lane % 2
+          const uint8_t* src = tb + (int64_t)g * 4224 + 4096 + r0 * 2 + (lane & 1) * 16;
+#pragma unroll
+          for (int rep = 0; rep < 2; ++rep)
+            __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(slot + 8192),
+                                             16, 0, 0);
+        } else {
+        const uint8_t* tb = p.w + ((int64_t)(n >> 6) * p.wG + s.gA) * 1280;
 #pragma unroll
         for (int ci = 0; ci < 8; ++ci) {   // codes: 4 groups per load (lane: group 4 ci + lane / 16, row lane % 16)
           const int g = min(32 * h + 4 * ci + (lane >> 4), glast);
@@ -201,6 +242,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
           const uint8_t* src = tb + (int64_t)g * 1280 + 1024 + (r0 + 4 * (lane & 3)) * 4;
           __builtin_amdgcn_global_load_lds((const void*)src,
                                            (__attribute__((address_space(3))) void*)(slot + 8192 + si * 1024), 16, 0, 0);
+        }
         }
         if (!depth2) {
           asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -264,7 +306,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
   // x' of groups [g0, g1) from the previous op's mailbox: each compute thread polls its own elements until all of them
   // carry this run's tag (bounded like wait_flags), then writes x' and the group sums as stage_x does (raw prologue).
   // The poll is the load: the hand-off costs one memory round trip instead of a flag round trip and then an x load.
-  auto stage_mbx = [&](const GemvP& p, int g0, int g1, int gps) -> bool {
+  auto stage_mbx = [&](const GemvP& p, int g0, int g1, int gps, float odd) -> bool {
     constexpr int U = 4, NT = 64 * kPC;
     const int KL = gps * 32, kb = g0 * 32, ke = g1 * 32;
     int go = spin_limit >= 0;
@@ -294,7 +336,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
         const float v = kb + kl < ke ? __uint_as_float((unsigned)w[u]) : 0.0f;
         const float gsum = sum32(v);
         if (kl < KL) {
-          xs[kl] = (kl & 1) ? v * 0.0625f : v;   // kb is even: k and kl share parity
+          xs[kl] = (kl & 1) ? v * odd : v;   // kb is even: k and kl share parity
           if ((lane & 31) == 0) xsum[kl >> 5] = gsum;
         }
       }
@@ -317,12 +359,17 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
   bool abandon = false;
   for (int i = 0; i < n_ops; ++i) {
     const GemvP& p = ops[i];
-    const Share s = share_of(p, b, G);
+    const Share s = share_of<Q8>(p, b, G);
     if (s.nu > 0) {
+      // x' of the split in 32-k groups; the q4 dot products take odd k pre-scaled 1/16, the q8 ones plain x'
+      const bool q8 = Q8 && p.enc == P0_ENC_Q8G64S_T64;
+      const int xg0 = q8 ? 2 * s.gA : s.gA, xg1 = q8 ? 2 * (s.gA + s.ngs) : s.gA + s.ngs;
+      const int xgps = q8 ? 16 * s.nh : 32 * s.nh;
+      const float odd = q8 ? 1.0f : 0.0625f;
       if (p.mbxIn) {
         // op i - 1's completion is not waited for here: its mailbox says its outputs are all written. Op i + 1 waits
         // for op i - 1's flags with op i's (GemvP::flags2), so every later op still sees every earlier op complete.
-        if (!stage_mbx(p, s.gA, s.gA + s.ngs, s.nh * 32)) {
+        if (!stage_mbx(p, xg0, xg1, xgps, odd)) {
           abandon = true;
           break;
         }
@@ -332,12 +379,33 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
           break;
         }
         // op i - 1's outputs are read with coherent loads: no L2 invalidate
-        if (p.coh & 1) stage_x<1, true>(p, s.gA, s.gA + s.ngs, s.nh * 32, xs, xsum, tc, 64 * kPC);
-        else stage_x<1, false>(p, s.gA, s.gA + s.ngs, s.nh * 32, xs, xsum, tc, 64 * kPC);
+        if (p.coh & 1) stage_x<1, true>(p, xg0, xg1, xgps, xs, xsum, tc, 64 * kPC, odd);
+        else stage_x<1, false>(p, xg0, xg1, xgps, xs, xsum, tc, 64 * kPC, odd);
         cbar();
       }
       const int nrp = s.nu * s.nrb * s.parts;
       if (s.spread) {
+       if (q8) {
+        // q8 slots: compute wave c takes group c of every slot, lane = (row lane / 4, quarter lane % 4 of the group's
+        // 64 k); the quarters are added across the lane quad, the groups across the waves (red), as for q4
+        const int rr = lane >> 2, qq = lane & 3;
+        for (int rp = 0; rp < nrp; ++rp) {
+          float acc = 0.0f;
+          for (int h = 0; h < s.nh; ++h) {
+            const int q = q0 + rp * s.nh + h;
+            wait_slot(q);
+            const uint8_t* slot = lds + (q % kRing) * kSlotB;
+            const int g = 8 * h + c;   // group of the split (< 8 nh: inside the staged x')
+            const u32x4 qv = *(const u32x4l*)(slot + c * 1024 + rr * 64 + qq * 16);
+            const float sc = h2f_u16(slot + 8192 + c * 32 + rr * 2);
+            float d = dot16_q8(qv, xs + g * 64 + qq * 16);
+            d += __shfl_xor(d, 1, 64);
+            d += __shfl_xor(d, 2, 64);
+            if (g < s.ngs) acc = __builtin_fmaf(sc, d - 128.0f * (xsum[2 * g] + xsum[2 * g + 1]), acc);
+          }
+          if (qq == 0) red[(rp * kPC + c) * 16 + rr] = acc;
+        }
+       } else {
         // every compute lane takes pair tc = 16 group + row of each slot; a part's slots are its halves
         const int gi = tc >> 4;
         for (int rp = 0; rp < nrp; ++rp) {
@@ -358,6 +426,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
           acc += __shfl_xor(acc, 32, 64);
           if (lane < 16) red[(rp * kPC + c) * 16 + lane] = acc;
         }
+       }
         cbar();   // every slot of the share is read, every wave's row sums are in
         if (tc < s.nslot) ctl_add(lctl + kCtlRel + (q0 + tc) % kRing, 1u);
         // epilogue: compute thread t -> row t of the share (a softcap unit is one whole wave)
@@ -392,6 +461,27 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
                 const int q = q0 + slot_index(s, j, (r * s.parts + pt) * s.nh + h);
                 wait_slot(q);
                 const uint8_t* slot = lds + (q % kRing) * kSlotB;
+                if (q8) {   // lane = (row lane / 4, quarter lane % 4) of each of the slot's 8 groups
+                  const int rr = lane >> 2, qq = lane & 3;
+                  u32x4 qv[8];
+                  float sc[8];
+#pragma unroll
+                  for (int gl = 0; gl < 8; ++gl) {
+                    qv[gl] = *(const u32x4l*)(slot + gl * 1024 + rr * 64 + qq * 16);
+                    sc[gl] = h2f_u16(slot + 8192 + gl * 32 + rr * 2);
+                  }
+                  __builtin_amdgcn_s_waitcnt(0xC07F);   // this wave's reads of the slot are done
+                  if (lane == 0) ctl_add(lctl + kCtlRel + q % kRing, 1u);
+#pragma unroll
+                  for (int gl = 0; gl < 8; ++gl) {
+                    const int g = 8 * h + gl;
+                    float d = dot16_q8(qv[gl], xs + g * 64 + qq * 16);
+                    d += __shfl_xor(d, 1, 64);
+                    d += __shfl_xor(d, 2, 64);
+                    if (g < s.ngs) acc = __builtin_fmaf(sc[gl], d - 128.0f * (xsum[2 * g] + xsum[2 * g + 1]), acc);
+                  }
+                  continue;
+                }
                 u32x4 qv[8];
                 uint32_t sm[8];
 #pragma unroll
@@ -409,6 +499,10 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
                     acc = __builtin_fmaf(h2f_lo(sm[kk]) * 16777216.0f, d, __builtin_fmaf(h2f_hi(sm[kk]), xsum[g], acc));
                   }
                 }
+              }
+              if (q8) {
+                if ((lane & 3) == 0) wred[pt * 64 + r * 16 + (lane >> 2)] = acc;
+                continue;
               }
               acc += __shfl_xor(acc, 16, 64);
               acc += __shfl_xor(acc, 32, 64);
@@ -441,6 +535,6 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
   if (b == 0 && wait_flags(flags + 0, nullptr) && tc == 0) st_coh(st, tag);
 }
 
-chain_kernel_t pipe_chain_kernel() { return q4_chain_pipe_kernel; }
+chain_kernel_t pipe_chain_kernel(bool q8) { return q8 ? q4_chain_pipe_kernel<true> : q4_chain_pipe_kernel<false>; }
 
 }  // namespace p0

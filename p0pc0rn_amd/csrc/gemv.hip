@@ -119,6 +119,7 @@ static constexpr size_t kChainLdsMax = 160 * 1024 - 256;   // gfx950: LDS per CU
 
 struct ChainBuild {
   int M = 0, W = 0, G = 0;
+  bool q8 = false;     // holds q8g64s.t64 ops (the pipelined kernel only)
   size_t lds = 0;
   std::vector<GemvP> ops;
   std::string error;   // the first failed append (reported again by p0_chain_end)
@@ -221,7 +222,7 @@ static size_t plan_mailboxes(std::vector<GemvP>& ops, std::vector<int64_t>& mb_o
     const GemvP& pr = ops[i - 1];
     GemvP& c = ops[i];
     if (mb_in[i - 1] >= 0 || pr.nsplit != 1 || (pr.epi != P0_EPI_STORE && pr.epi != P0_EPI_GEGLU)) continue;
-    if (c.pro != P0_PRO_RAW || c.enc != P0_ENC_Q4G32A_T64) continue;
+    if (c.pro != P0_PRO_RAW) continue;
     const intptr_t d = (intptr_t)(const void*)(c.X + c.rowB) - (intptr_t)(const void*)pr.Y;
     if (d < 0 || d % 4 || d / 4 + c.K > pr.N) continue;
     std::vector<Span> rp, wp, rc, wc;
@@ -315,7 +316,7 @@ static bool plan_pipe(std::vector<GemvP>& ops, int G) {
     const int64_t U = (int64_t)(p.N / (kStageRows * nrb)) * p.nsplit;
     if (U > G && G % p.nsplit) return false;
     const int64_t numax = (U + G - 1) / G;
-    const int nh = (p.kPer / 32 + 31) / 32;
+    const int nh = p.enc == P0_ENC_Q8G64S_T64 ? (p.kPer / 64 + 7) / 8 : (p.kPer / 32 + 31) / 32;   // slots per part
     const int64_t nrp = numax * nrb * parts;
     const bool spread = nrp * nh <= pipe_ring_slots() && nrp <= pipe_spread_parts() && numax * nrb * kStageRows <= 512;
     p.su = (int)U;
@@ -329,11 +330,6 @@ static bool plan_pipe(std::vector<GemvP>& ops, int G) {
 
 // q8g64s.t64: one workgroup per (64-row tile, split), gemv_q8.hip
 static int launch_q8(GemvP& p, int M, const char* op) {
-  if (g_chain) {
-    set_error("%s: q8g64s.t64 ops cannot join a chain in this build", op);
-    if (g_chain->error.empty()) g_chain->error = p0_last_error();
-    return P0_EINVAL;
-  }
   q8_kernel_t k = q8_kernel(M);
   const size_t lds = q8_lds_bytes(M);
   static bool attr[2] = {false, false};
@@ -347,8 +343,8 @@ static int launch_q8(GemvP& p, int M, const char* op) {
 }
 
 static int launch(GemvP& p, int M, const char* op) {
-  if (p.enc == P0_ENC_Q8G64S_T64) return launch_q8(p, M, op);
   ChainBuild* cb = g_chain;
+  if (p.enc == P0_ENC_Q8G64S_T64 && !cb) return launch_q8(p, M, op);
   if (cb && cb->ops.empty()) {   // the chain's first op fixes M and the workgroup shape
     cb->M = M;
     cb->W = M == 1 ? g_chain_waves : 8;
@@ -358,6 +354,13 @@ static int launch(GemvP& p, int M, const char* op) {
     set_error("%s: a chain holds ops of one M (chain M %d, this op %d)", op, cb->M, M);
     if (cb->error.empty()) cb->error = p0_last_error();
     return P0_EINVAL;
+  }
+  if (cb && p.enc == P0_ENC_Q8G64S_T64) {
+    // q8g64s.t64 ops run only on the pipelined M = 1 kernel (p0_chain_end refuses a chain that cannot take them)
+    p.coh = 0;
+    cb->ops.push_back(p);
+    cb->q8 = true;
+    return P0_OK;
   }
   const Plan pl = cb ? plan_chain(M, p.NT, p.epi, p.nsplit, p.kPer, cb->W, cb->G) : plan(M, p.NT, p.epi, p.nsplit, p.kPer);
   if (pl.nks > 1 && (size_t)p.nsplit * pl.nks * M * pl.rowsTot > ctx().part_floats) {
@@ -565,7 +568,7 @@ extern "C" int p0_chain_end(void** out) {
   }
   // M = 1: the pipelined kernel, one workgroup per CU, when every op can be planned for it
   if (cb->M == 1 && g_chain_stage) {
-    chain_kernel_t pk = pipe_chain_kernel();
+    chain_kernel_t pk = pipe_chain_kernel(cb->q8);
     P0_HIP(hipFuncSetAttribute((const void*)pk, hipFuncAttributeMaxDynamicSharedMemorySize, pipe_lds_bytes()),
            "p0_chain_end");
     int pc = 0;
@@ -580,9 +583,14 @@ extern "C" int p0_chain_end(void** out) {
       lds = pipe_lds_bytes();
     }
   }
+  const bool pipe = k == pipe_chain_kernel(false) || k == pipe_chain_kernel(true);
+  if (cb->q8 && !pipe) {
+    set_error("p0_chain_end: q8g64s.t64 ops join only pipelined chains (M = 1, 16-byte aligned weights, knob 4 on)");
+    return P0_EINVAL;
+  }
   mark_coherence(cb->ops, cb->M);
   std::vector<int64_t> mb_out, mb_in;
-  const size_t mb_words = k == pipe_chain_kernel() && g_chain_mbx ? plan_mailboxes(cb->ops, mb_out, mb_in) : 0;
+  const size_t mb_words = pipe && g_chain_mbx ? plan_mailboxes(cb->ops, mb_out, mb_in) : 0;
   auto* ex = new ChainExec{};
   ex->n_ops = (int)cb->ops.size();
   ex->M = cb->M;
@@ -590,7 +598,7 @@ extern "C" int p0_chain_end(void** out) {
   ex->grid = grid;
   ex->lds = lds;
   ex->kernel = k;
-  if (k == pipe_chain_kernel()) {
+  if (pipe) {
     ex->pipe_cfg[0] = g_pipe_loaders;
     ex->pipe_cfg[1] = g_pipe_depth;
   }

@@ -168,7 +168,8 @@ __device__ __forceinline__ float sum32(float v) {
   return v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));   // lane ^ 16
 }
 
-// x'[m][k] of the groups [g0, g1) -> LDS xs[m * 32 gps + k - 32 g0] (odd k scaled 1/16), and the per-group sums of
+// x'[m][k] of the groups [g0, g1) -> LDS xs[m * 32 gps + k - 32 g0] (odd k scaled by `odd`: 1/16 for the q4 dot
+// products, 1 for q8 ones), and the per-group sums of
 // x' -> xsum[m * gps + group - g0]; entries of the gps groups past g1 are zero. Thread tid takes elements u * blockDim +
 // tid of each batch of U: the 32 lanes of a 32-aligned lane group hold one group's 32 k (the slice length and the
 // block size are multiples of 32), which they sum with cross-lane adds. Every thread runs the same number of
@@ -176,7 +177,7 @@ __device__ __forceinline__ float sum32(float v) {
 // tid / nt: the calling thread's index among the nt threads that stage (whole waves; every one of them calls).
 template <int M, bool COH>
 __device__ __forceinline__ void stage_x(const GemvP& p, int g0, int g1, int gps, float* xs, float* xsum,
-                                        int tid = threadIdx.x, int nt = blockDim.x) {
+                                        int tid = threadIdx.x, int nt = blockDim.x, float odd = 0.0625f) {
   constexpr int U = M == 1 ? 4 : 8;
   const int lane = tid & 63, wv = tid >> 6;
   const int KL = gps * 32, kb = g0 * 32, ke = g1 * 32, nx = M * KL;
@@ -196,7 +197,7 @@ __device__ __forceinline__ void stage_x(const GemvP& p, int g0, int g1, int gps,
     for (int u = 0; u < U; ++u) {
       const float gs = sum32(v[u]);
       if (i0 + u * nt + tid < nx) {
-        xs[mm[u] * KL + kl[u]] = (kl[u] & 1) ? v[u] * 0.0625f : v[u];   // kb is even: k and kl share parity
+        xs[mm[u] * KL + kl[u]] = (kl[u] & 1) ? v[u] * odd : v[u];   // kb is even: k and kl share parity
         if ((lane & 31) == 0) xsum[mm[u] * gps + (kl[u] >> 5)] = gs;
       }
     }
@@ -779,7 +780,7 @@ q8_kernel_t q8_kernel(int M);
 size_t q8_lds_bytes(int M);
 
 // the pipelined M = 1 chain (chain_pipe.hip): its kernel and its fixed shape
-chain_kernel_t pipe_chain_kernel();
+chain_kernel_t pipe_chain_kernel(bool q8);   // q8: the instantiation that also runs q8g64s.t64 ops
 int pipe_lds_bytes();
 int pipe_waves();
 int pipe_ring_slots();

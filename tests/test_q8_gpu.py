@@ -3,8 +3,8 @@
 Every q8 shape the reference ships (engine/tune/kshipped.js:14, run as kshipped.js:17-41 runs it: 128 rows at the real
 K, its kPer rule, seeds 33 + K / 34 + K / 35 + K) under the reference's own acceptance (cos > 0.99999, the tile argmax)
 and this build's bars (relative L2 <= 1e-3 and <= 2e-5), the expected rows in float64 from numpy over the decoded
-records (tests/test_q8_oracle.py pins the packer and the decode); gemvM with M rows against the oracle; and a chain that
-holds a q8 op is refused."""
+records (tests/test_q8_oracle.py pins the packer and the decode); gemvM with M rows against the oracle; q8 ops inside a
+pipelined chain, mixed with q4 ops, against the oracle; and a gemvM chain holding a q8 op is refused."""
 import math
 
 import numpy as np
@@ -88,11 +88,104 @@ def test_q8_gemvM_matches_oracle(dev, M, epi):
         v.free()
 
 
-def test_q8_ops_cannot_join_a_chain(dev):
-    N, K = 128, 256
-    w, _ = O.pack_q8(O.randn(N * K, 5, 0.05), N, K)
-    wb, xb, yb = capi.to_device(w), capi.Buffer(K * 4), capi.Buffer(N * 4)
-    with pytest.raises(capi.P0Error, match="q8g64s.t64 ops cannot join a chain"):
-        capi.chain(lambda: capi.q4_gemv(capi.gemv_args(w=wb, w_enc=2, w_rows=N, w_cols=K, x=xb, N=N, K=K, y=yb)))
+def _q8(rows, K, seed):
+    return O.pack_q8(O.randn(rows * K, seed, 0.05), rows, K)[0]
+
+
+def _q4(rows, K, seed):
+    return O.pack_q4(O.randn(rows * K, seed, 0.05), rows, K)[0]
+
+
+def test_q8_ops_in_a_pipelined_chain(dev):
+    """A decode-like chain of q4g32a.t64 and q8g64s.t64 ops (the real E2B pack is balanced 4/8-bit) as one pipelined
+    launch: q8 ops with every prologue the chain sees (rms, raw through a mailbox, raw with 2 K-splits), a geglu, a
+    softcap and a large share per workgroup (one wave per unit). Each op is checked against the oracle run on the input
+    it read on the GPU (the previous op's output, read back), to this build's fp32 bar; every intermediate is NaN-filled
+    before the run. Two more runs reproduce the bits."""
+    D = 256
+    x0 = O.randn(2048, 501)
+    nw = nw_of(2048)
+    st = np.array([0, 0.7, 0, 0], np.float32)
+    ops = [   # (name, enc, w rows, N, K, kPer, pro, epi, input, input offset)
+        ("a", "q4", 512, 512, D, 0, "rms", "store", "x", 0),
+        ("b", "q8", D, D, 512, 0, "raw", "store", "a", 0),          # mailbox from a q4 op into a q8 op
+        ("c", "q8", 768, 384, D, 0, "rms", "geglu", "b", 0),
+        ("d", "q4", D, D, 384, 0, "rms", "store", "c", 0),
+        ("e", "q8", D, D, D, 128, "raw", "store", "d", 0),         # mailbox into a 2-split q8 op
+        ("f", "q8", 32768, 32768, 2048, 0, "rms", "store", "x", 0),  # 8 units x 4 slots per workgroup: per-wave mode
+        ("g", "q8", 4096, 4096, D, 0, "rms", "softcap", "x", 0),
+    ]
+    host = {n: (_q8 if enc == "q8" else _q4)(rows, K, 510 + i)
+            for i, (n, enc, rows, N, K, kPer, pro, epi, src, off) in enumerate(ops)}
+    dw = {n: capi.to_device(w) for n, w in host.items()}
+    x, nwb, stb = capi.to_device(x0), capi.to_device(nw), capi.to_device(st)
+    nsplit = {n: (-(-K // kPer) if kPer else 1) for (n, enc, rows, N, K, kPer, pro, epi, src, off) in ops}
+    out = {n: capi.Buffer(4 * N * nsplit[n]) for (n, enc, rows, N, K, kPer, pro, epi, src, off) in ops}
+    NTg = 4096 // 64
+    mx0 = np.zeros(NTg * 2 + 8, np.float32)
+    mx0[NTg * 2 + 1] = 0.9
+    mx = capi.to_device(mx0)
+    bufs = dict(out, x=x)
+
+    def fields(n, enc, rows, N, K, kPer, pro, epi, src, off, b):
+        f = dict(w=b["w"][n], w_enc=1 if enc == "q4" else 2, w_rows=rows, w_cols=K, x=b[src], x_rowB=off, N=N, K=K,
+                 kPer=kPer, pro=capi.PRO[pro], epi=capi.EPI[epi], y=b[n])
+        if pro == "rms":
+            f.update(norm=b["nw"], stat=b["st"], stat_off=1)
+        if epi == "softcap":
+            f.update(mx=b["mx"], stat=b["mx"], stat_off=NTg * 2 + 1)
+        return f
+
+    dev_b = dict(bufs, w=dw, nw=nwb, st=stb, mx=mx)
+
+    def enqueue():
+        for o in ops:
+            capi.q4_gemv(capi.gemv_args(**fields(*o, dev_b)))
+
+    ch = capi.chain(enqueue)
+    info = ch.info()
+    print("mixed chain", info, flush=True)
+    if info["waves_per_workgroup"] != 12:
+        pytest.skip("this device plans the general chain kernel")
+    assert info["mailboxes"] == 2
+    runs = []
+    for r in range(3):
+        for n in out:
+            out[n].fill_u32(0x7FC00000)
+        mx.upload(mx0)
+        ch.run()
+        assert not ch.status()
+        runs.append({n: out[n].read(np.float32) for n in out} | {"mx": mx.read(np.float32)})
+    for r in runs[1:]:
+        for k in r:
+            assert np.array_equal(runs[0][k].view(np.uint32), r[k].view(np.uint32)), k
+    got = runs[0]
+    mxh = mx0.copy()
+    for o in ops:
+        n, enc, rows, N, K, kPer, pro, epi, src, off = o
+        xin = np.ascontiguousarray(x0 if src == "x" else got[src], np.float32)
+        y = np.full(N * nsplit[n], np.nan, np.float32)
+        f = fields(n, enc, rows, N, K, kPer, pro, epi, "x", off,
+                   dict(w={n: host[n].ctypes.data}, x=xin.ctypes.data, nw=nw.ctypes.data, st=st.ctypes.data,
+                        mx=mxh.ctypes.data, **{n: y.ctypes.data}))
+        O.q4_gemv(capi.gemv_args(**f))
+        r = rel_l2(got[n], y)
+        print(f"op {n} ({enc} {pro}.{epi} {N}x{K} kPer {kPer}): rel_l2 {r:.3e}", flush=True)
+        assert np.all(np.isfinite(got[n])) and r <= 2e-5, n
+    gm, om = got["mx"][:2 * NTg:2], mxh[:2 * NTg:2]
+    assert np.allclose(gm, om, rtol=1e-5, atol=1e-5)
+    assert np.mean(got["mx"][1:2 * NTg:2].view(np.uint32) == mxh[1:2 * NTg:2].view(np.uint32)) > 0.99
+    ch.free()
+    for v in list(dw.values()) + [x, nwb, stb, mx] + list(out.values()):
+        v.free()
+
+
+def test_q8_ops_join_only_pipelined_chains(dev):
+    """q8 ops need the pipelined M = 1 kernel: a gemvM chain holding one is refused at p0_chain_end"""
+    N, K, M = 128, 256, 2
+    wb, xb, yb = capi.to_device(_q8(N, K, 5)), capi.Buffer(M * K * 4), capi.Buffer(M * N * 4)
+    with pytest.raises(capi.P0Error, match="q8g64s.t64 ops join only pipelined chains"):
+        capi.chain(lambda: capi.q4_gemvM(capi.gemvm_args(w=wb, w_enc=2, w_rows=N, w_cols=K, x=xb, M=M, N=N, K=K,
+                                                         y=yb)))
     for v in (wb, xb, yb):
         v.free()
