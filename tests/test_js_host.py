@@ -123,12 +123,13 @@ const fl = P.gemm(g, { w: { buf: wg, off: 0, enc: 'q4g32a.t64', rows: 128, cols:
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("mode", ["graph", "chain"])
-def test_js_decode_runner(tmp_path, mode):
-    """a token of two dependent GEMVs (y1 = W1 x; y2 = W2 y1), recorded once and submitted three times"""
+@pytest.mark.parametrize("mode,enc2", [("graph", "q4"), ("chain", "q4"), ("graph", "q8"), ("chain", "q8")])
+def test_js_decode_runner(tmp_path, mode, enc2):
+    """a token of two dependent GEMVs (y1 = W1 x; y2 = W2 y1), recorded once and submitted three times; W2 in either
+    encoding (a balanced 4/8-bit pack mixes them in one token)"""
     N1, K1, N2 = 512, 1024, 256
     w1, _ = O.pack_q4(O.randn(N1 * K1, 7, 0.05), N1, K1)
-    w2, _ = O.pack_q4(O.randn(N2 * N1, 8, 0.05), N2, N1)
+    w2, _ = (O.pack_q4 if enc2 == "q4" else O.pack_q8)(O.randn(N2 * N1, 8, 0.05), N2, N1)
     x = O.randn(K1, 9)
     _save(tmp_path, w1=w1, w2=w2, x=x)
     out = run_node(tmp_path, r"""
@@ -139,7 +140,7 @@ const y1 = g.buffer(512 * 4), y2 = g.buffer(256 * 4);
 const r = new P.DecodeRunner(g, { mode: '%s' });
 r.begin();
 P.gemv(g, { w: { buf: w1, off: 0, enc: 'q4g32a.t64', rows: 512, cols: 1024 }, x: { buf: x }, N: 512, K: 1024, y: { buf: y1 } });
-P.gemv(g, { w: { buf: w2, off: 0, enc: 'q4g32a.t64', rows: 256, cols: 512 }, x: { buf: y1 }, N: 256, K: 512, y: { buf: y2 } });
+P.gemv(g, { w: { buf: w2, off: 0, enc: '%s', rows: 256, cols: 512 }, x: { buf: y1 }, N: 256, K: 512, y: { buf: y2 } });
 const tk = r.end();
 (async () => {
   const outs = [];
@@ -153,7 +154,7 @@ const tk = r.end();
   console.log(JSON.stringify({ same: outs.every((o) => o === outs[0]), submits: r.submits }));
   r.forget(); g.freeAll(); g.device.destroy();
 })();
-""" % mode)
+""" % (mode, "q4g32a.t64" if enc2 == "q4" else "q8g64s.t64"))
     res = json.loads(out.strip().splitlines()[-1])
     assert res["same"] and res["submits"] == 3
     y1 = np.fromfile(str(tmp_path / "y1.bin"), np.float32)
@@ -161,7 +162,8 @@ const tk = r.end();
     want1 = np.zeros(N1, np.float32)
     O.q4_gemv(capi.gemv_args(w=w1.ctypes.data, w_rows=N1, w_cols=K1, x=x.ctypes.data, N=N1, K=K1, y=want1.ctypes.data))
     want2 = np.zeros(N2, np.float32)
-    O.q4_gemv(capi.gemv_args(w=w2.ctypes.data, w_rows=N2, w_cols=N1, x=y1.ctypes.data, N=N2, K=N1, y=want2.ctypes.data))
+    O.q4_gemv(capi.gemv_args(w=w2.ctypes.data, w_enc=1 if enc2 == "q4" else 2, w_rows=N2, w_cols=N1, x=y1.ctypes.data,
+                             N=N2, K=N1, y=want2.ctypes.data))
     for got, want, what in ((y1, want1, "op 0"), (y2, want2, "op 1")):
         r = rel_l2(got, want)
         assert np.all(np.isfinite(got)) and r <= 2e-5, (mode, what, r)
