@@ -529,3 +529,64 @@ def test_chain_mailbox_cases(dev):
     ch_f.free()
     for buf in list(dv.values()) + [x] + list(b.values()):
         buf.free()
+
+
+@pytest.mark.parametrize("enc", ["q4", "q8"])
+def test_chain_small_and_ragged_shapes(dev, enc):
+    """The pipelined chain at the edges of its slots: one group (K = 32 / 64), a K that leaves most of a slot empty,
+    a ragged last K-split (K = 320, kPer = 128: splits of 128, 128 and 64 k; q8: K = 384, kPer = 256: 256 and 128), the
+    fewest rows (N = 64) and a softcap on one tile, each op checked against the oracle on the input it read"""
+    G = 32 if enc == "q4" else 64
+    pack = (lambda w, r, k: O.pack_q4(w, r, k)[0]) if enc == "q4" else (lambda w, r, k: O.pack_q8(w, r, k)[0])
+    we = 1 if enc == "q4" else 2
+    Kr, kPr = (320, 128) if enc == "q4" else (384, 256)
+    ops = [   # (N, K, kPer, epi, input)
+        (64, G, 0, "store", "x"),
+        (256, 64, 0, "store", 0),
+        (192, 3 * G, 0, "store", 1),
+        (64, 192, 0, "softcap", 2),
+        (Kr, 64, 0, "store", 1),
+        (128, Kr, kPr, "store", 4),
+    ]
+    x0 = O.randn(256, 601)
+    ws = [pack(O.randn(N * K, 610 + i, 0.05), N, K) for i, (N, K, kPer, epi, src) in enumerate(ops)]
+    dw = [capi.to_device(w) for w in ws]
+    x = capi.to_device(x0)
+    nsp = [(-(-K // kPer) if kPer else 1) for (N, K, kPer, epi, src) in ops]
+    ys = [capi.Buffer(4 * N * s) for (N, K, kPer, epi, src), s in zip(ops, nsp)]
+    mx0 = np.zeros(16, np.float32)
+    mx0[3] = 0.8
+    mx = capi.to_device(mx0)
+
+    def f(i, b_in, b_out, mxp):
+        N, K, kPer, epi, src = ops[i]
+        d = dict(w=dw[i] if mxp is None else ws[i].ctypes.data, w_enc=we, w_rows=N, w_cols=K, x=b_in, N=N, K=K, kPer=kPer,
+                 epi=capi.EPI[epi], y=b_out)
+        if epi == "softcap":
+            d.update(mx=mx if mxp is None else mxp, pro=capi.PRO["rms"], stat=mx if mxp is None else mxp, stat_off=3,
+                     norm=x if mxp is None else x0.ctypes.data)
+        return d
+
+    def enqueue():
+        for i, (N, K, kPer, epi, src) in enumerate(ops):
+            capi.q4_gemv(capi.gemv_args(**f(i, x if src == "x" else ys[src], ys[i], None)))
+
+    ch = capi.chain(enqueue)
+    print("chain", ch.info(), flush=True)
+    for b in ys:
+        b.fill_u32(NAN)
+    mx.upload(mx0)
+    ch.run()
+    assert not ch.status()
+    got = [b.read(np.float32) for b in ys]
+    gmx = mx.read(np.float32)
+    mxh = mx0.copy()
+    for i, (N, K, kPer, epi, src) in enumerate(ops):
+        xin = np.ascontiguousarray(x0 if src == "x" else got[src], np.float32)
+        y = np.full(N * nsp[i], np.nan, np.float32)
+        O.q4_gemv(capi.gemv_args(**f(i, xin.ctypes.data, y.ctypes.data, mxh.ctypes.data)))
+        _check(got[i], y, f"{enc} op {i} N {N} K {K} kPer {kPer} {epi}")
+    assert np.allclose(gmx[0], mxh[0], rtol=1e-5, atol=1e-6) and gmx[1].view(np.uint32) == mxh[1].view(np.uint32)
+    ch.free()
+    for b in dw + ys + [x, mx]:
+        b.free()
