@@ -31,26 +31,37 @@ constexpr int kPL = 4;                       // loader waves
 constexpr int kPC = 8;                       // compute waves
 constexpr int kPW = kPL + kPC;
 constexpr int kSlotB = kStageRows * 32 * 20; // 10240: one slot
-constexpr int kRing = 12;                    // slots in the ring
-constexpr int kPipeKL = 3072;                // largest split (gemv: kch <= 3072)
-constexpr int kPipeRedRp = 16;               // spread shares: most 16-row parts per workgroup
 // chain state words (in the first 128-byte line, after the tag) that the host sets from p0_chain_tune knob 5
 constexpr int kCfgLoaders = 4, kCfgDepth = 5;
+constexpr int kPipeMaxM = 5;                 // x rows a pipelined chain takes (gemvM verify passes up to 5)
 
-// LDS layout (bytes)
-constexpr int kOffXs = kRing * kSlotB;                         // x' [kPipeKL] (odd k scaled 1/16)
-constexpr int kOffXsum = kOffXs + kPipeKL * 4;                 // group sums [kPipeKL / 32]
-constexpr int kOffRed = kOffXsum + (kPipeKL / 32) * 4;         // spread: [part][compute wave][16 rows]
-constexpr int kOffWred = kOffRed + kPipeRedRp * kPC * 16 * 4;  // per wave: [compute wave][2][64 rows]
-constexpr int kOffCtl = kOffWred + kPC * 2 * 64 * 4;           // control words
-constexpr int kCtlFull = 0, kCtlRel = kRing, kCtlBar = 2 * kRing, kCtlStop = 2 * kRing + 1,
-              kCtlGo = 2 * kRing + 2, kCtlTag = 2 * kRing + 3, kCtlWords = 2 * kRing + 4;
-constexpr int kPipeLds = kOffCtl + kCtlWords * 4;
+// LDS layout (bytes) for M rows of x. M = 1 takes splits of up to 3072 k (gemv: kch <= 3072), M > 1 up to 2048
+// (gemvM caps kPer at 2048); the ring gives way to the M rows of x' and of the reductions.
+template <int M>
+struct PipeL {
+  static constexpr int KL = M == 1 ? 3072 : 2048;                   // largest split
+  static constexpr int RedRp = M == 1 ? 16 : 4;                     // spread shares: most 16-row parts per workgroup
+  static constexpr int Ring = M <= 2 ? 12 : M == 3 ? 11 : M == 4 ? 10 : 8;   // slots in the ring
+  static constexpr int OffXs = Ring * kSlotB;                       // x' [M][split] (odd k scaled 1/16 for q4)
+  static constexpr int OffXsum = OffXs + M * KL * 4;                // group sums [M][split / 32]
+  static constexpr int OffRed = OffXsum + M * (KL / 32) * 4;        // spread: [part][m][compute wave][16 rows]
+  static constexpr int OffWred = OffRed + RedRp * M * kPC * 16 * 4; // per wave: [compute wave][m][2][64 rows]
+  static constexpr int OffCtl = OffWred + kPC * M * 2 * 64 * 4;     // control words
+  static constexpr int CtlFull = 0, CtlRel = Ring, CtlBar = 2 * Ring, CtlStop = 2 * Ring + 1, CtlGo = 2 * Ring + 2,
+                       CtlTag = 2 * Ring + 3, CtlWords = 2 * Ring + 4;
+  static constexpr int Lds = OffCtl + CtlWords * 4;
+  static_assert(Lds <= 160 * 1024 - 256, "pipelined chain LDS");
+};
 
-__host__ int pipe_lds_bytes() { return kPipeLds; }
+__host__ int pipe_lds_bytes(int M) {
+  return M == 1 ? PipeL<1>::Lds : M == 2 ? PipeL<2>::Lds : M == 3 ? PipeL<3>::Lds : M == 4 ? PipeL<4>::Lds : PipeL<5>::Lds;
+}
 __host__ int pipe_waves() { return kPW; }
-__host__ int pipe_ring_slots() { return kRing; }
-__host__ int pipe_spread_parts() { return kPipeRedRp; }
+__host__ int pipe_ring_slots(int M) {
+  return M == 1 ? PipeL<1>::Ring : M == 2 ? PipeL<2>::Ring : M == 3 ? PipeL<3>::Ring : M == 4 ? PipeL<4>::Ring : PipeL<5>::Ring;
+}
+__host__ int pipe_spread_parts(int M) { return M == 1 ? PipeL<1>::RedRp : PipeL<2>::RedRp; }
+__host__ int pipe_max_m() { return kPipeMaxM; }
 __host__ int pipe_cfg_word() { return kCfgLoaders; }
 
 // LDS words seen by the loader waves through inline assembly: the compiler tracks LDS-DMA loads as pending writes to
@@ -144,32 +155,34 @@ __device__ __forceinline__ int share_row(const GemvP& p, const Share& s, int G, 
 }
 
 // Q8: the instantiation for chains that hold q8g64s.t64 ops (the q4-only one carries none of their code)
-template <bool Q8>
+template <int M, bool Q8>
 __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __restrict__ ops, int n_ops,
                                                                  unsigned* __restrict__ st, int spin_limit) {
+  using L = PipeL<M>;
+  constexpr int kRing = L::Ring;
   extern __shared__ __attribute__((aligned(16))) float smem[];
   uint8_t* const lds = (uint8_t*)smem;
-  unsigned* const ctl = (unsigned*)(lds + kOffCtl);
+  unsigned* const ctl = (unsigned*)(lds + L::OffCtl);
   const int tid = threadIdx.x, lane = tid & 63, G = gridDim.x, b = blockIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int Gp = chain_flag_stride(G);
   unsigned* const timed_out = st + kCtrStride;
   unsigned* const flags = st + 2 * kCtrStride;
-  if (tid < kCtlWords) ctl[tid] = 0;
+  if (tid < L::CtlWords) ctl[tid] = 0;
   if (tid == 0) {
-    ctl[kCtlTag] = ld_coh(st) + 1;
-    ctl[kCtlGo] = ld_coh(timed_out) == 0u;   // an earlier run gave up: do nothing until p0_chain_status resets it
+    ctl[L::CtlTag] = ld_coh(st) + 1;
+    ctl[L::CtlGo] = ld_coh(timed_out) == 0u;   // an earlier run gave up: do nothing until p0_chain_status resets it
   }
   __syncthreads();
-  const unsigned tag = ctl[kCtlTag];
-  if (!ctl[kCtlGo]) return;
+  const unsigned tag = ctl[L::CtlTag];
+  if (!ctl[L::CtlGo]) return;
 
   if (wv < kPL) {
     // ------------------------------------------------------------------ loader waves
     // st[kCfgLoaders]: loader waves that stream a small share (1 .. kPL; a large share takes all kPL),
     // st[kCfgDepth]: slots in flight per loader (1 or 2)
     const int nls = min(kPL, max(1, (int)st[kCfgLoaders])), depth2 = st[kCfgDepth] >= 2;
-    const unsigned a_full = lds_addr(ctl + kCtlFull), a_rel = lds_addr(ctl + kCtlRel), a_stop = lds_addr(ctl + kCtlStop);
+    const unsigned a_full = lds_addr(ctl + L::CtlFull), a_rel = lds_addr(ctl + L::CtlRel), a_stop = lds_addr(ctl + L::CtlStop);
     int q0 = 0, pend = -1;
     auto publish = [&](int q) { asm_lds_st(a_full + (q % kRing) * 4, (unsigned)q + 1); };
     for (int i = 0; i < n_ops; ++i) {
@@ -267,21 +280,21 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
   // -------------------------------------------------------------------- compute waves
   const int c = wv - kPL, tc = tid - 64 * kPL;
   lds_u32* const lctl = (lds_u32*)ctl;
-  float* const xs = (float*)(lds + kOffXs);
-  float* const xsum = (float*)(lds + kOffXsum);
-  float* const red = (float*)(lds + kOffRed);
-  float* const wred = (float*)(lds + kOffWred) + c * 128;
+  float* const xs = (float*)(lds + L::OffXs);
+  float* const xsum = (float*)(lds + L::OffXsum);
+  float* const red = (float*)(lds + L::OffRed);
+  float* const wred = (float*)(lds + L::OffWred) + c * (M * 128);   // this wave's [m][2][64 rows]
   unsigned gen = 0;
   // barrier of the compute waves: a monotonic LDS counter (every compute wave adds 1 per barrier)
   auto cbar = [&]() {
     gen += kPC;
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's LDS writes are done
-    if (lane == 0) ctl_add(lctl + kCtlBar, 1u);
-    while (ctl_ld(lctl + kCtlBar) < gen) __builtin_amdgcn_s_sleep(0);
+    if (lane == 0) ctl_add(lctl + L::CtlBar, 1u);
+    while (ctl_ld(lctl + L::CtlBar) < gen) __builtin_amdgcn_s_sleep(0);
     __builtin_amdgcn_s_waitcnt(0xC07F);
   };
   auto wait_slot = [&](int q) {
-    while (ctl_ld(lctl + kCtlFull + q % kRing) != (unsigned)q + 1) __builtin_amdgcn_s_sleep(0);
+    while (ctl_ld(lctl + L::CtlFull + q % kRing) != (unsigned)q + 1) __builtin_amdgcn_s_sleep(0);
   };
   // the G flags at f (and at f2, when not null) hold this run's tag (wave c == 0 polls); false in every compute
   // thread if the wait gave up
@@ -295,13 +308,13 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
       if (lane == 0) {
         if (!go) {
           atomicOr(timed_out, 1u);
-          ctl_st(lctl + kCtlStop, 1u);   // the loaders leave their waits
+          ctl_st(lctl + L::CtlStop, 1u);   // the loaders leave their waits
         }
-        ctl_st(lctl + kCtlGo, (unsigned)go);
+        ctl_st(lctl + L::CtlGo, (unsigned)go);
       }
     }
     cbar();
-    return ctl_ld(lctl + kCtlGo) != 0;
+    return ctl_ld(lctl + L::CtlGo) != 0;
   };
   // x' of groups [g0, g1) from the previous op's mailbox: each compute thread polls its own elements until all of them
   // carry this run's tag (bounded like wait_flags), then writes x' and the group sums as stage_x does (raw prologue).
@@ -343,11 +356,11 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
     }
     if (!go && lane == 0) {
       atomicOr(timed_out, 1u);
-      ctl_st(lctl + kCtlStop, 1u);   // the loaders leave their waits
-      ctl_st(lctl + kCtlGo, 0u);
+      ctl_st(lctl + L::CtlStop, 1u);   // the loaders leave their waits
+      ctl_st(lctl + L::CtlGo, 0u);
     }
     cbar();
-    return ctl_ld(lctl + kCtlGo) != 0;
+    return ctl_ld(lctl + L::CtlGo) != 0;
   };
   // this op's rows, with their values as stored, into its mailbox (after the epilogue's own stores)
   auto post_mbx = [&](const GemvP& p, int n, float v) {
@@ -379,8 +392,8 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
           break;
         }
         // op i - 1's outputs are read with coherent loads: no L2 invalidate
-        if (p.coh & 1) stage_x<1, true>(p, xg0, xg1, xgps, xs, xsum, tc, 64 * kPC, odd);
-        else stage_x<1, false>(p, xg0, xg1, xgps, xs, xsum, tc, 64 * kPC, odd);
+        if (p.coh & 1) stage_x<M, true>(p, xg0, xg1, xgps, xs, xsum, tc, 64 * kPC, odd);
+        else stage_x<M, false>(p, xg0, xg1, xgps, xs, xsum, tc, 64 * kPC, odd);
         cbar();
       }
       const int nrp = s.nu * s.nrb * s.parts;
@@ -403,13 +416,16 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
             d += __shfl_xor(d, 2, 64);
             if (g < s.ngs) acc = __builtin_fmaf(sc, d - 128.0f * (xsum[2 * g] + xsum[2 * g + 1]), acc);
           }
-          if (qq == 0) red[(rp * kPC + c) * 16 + rr] = acc;
+          if (qq == 0) red[(rp * M * kPC + c) * 16 + rr] = acc;   // q8 chains have M = 1
         }
        } else {
-        // every compute lane takes pair tc = 16 group + row of each slot; a part's slots are its halves
+        // every compute lane takes pair tc = 16 group + row of each slot; a part's slots are its halves; x' row m
+        // starts at m xgps 32
         const int gi = tc >> 4;
         for (int rp = 0; rp < nrp; ++rp) {
-          float acc = 0.0f;
+          float acc[M];
+#pragma unroll
+          for (int m = 0; m < M; ++m) acc[m] = 0.0f;
           for (int h = 0; h < s.nh; ++h) {
             const int q = q0 + rp * s.nh + h;
             wait_slot(q);
@@ -418,35 +434,46 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
             const u32x4 qv = *(const u32x4l*)(slot + tc * 16);
             const uint32_t sm = *(const uint32_t*)(slot + 8192 + tc * 4);
             if (g < s.ngs) {
-              const float d = dot32(qv, xs + g * 32);
-              acc = __builtin_fmaf(h2f_lo(sm) * 16777216.0f, d, __builtin_fmaf(h2f_hi(sm), xsum[g], acc));
+              const float s24 = h2f_lo(sm) * 16777216.0f, mn = h2f_hi(sm);
+#pragma unroll
+              for (int m = 0; m < M; ++m) {
+                const float d = dot32(qv, xs + m * xgps * 32 + g * 32);
+                acc[m] = __builtin_fmaf(s24, d, __builtin_fmaf(mn, xsum[m * xgps + g], acc[m]));
+              }
             }
           }
-          acc += __shfl_xor(acc, 16, 64);
-          acc += __shfl_xor(acc, 32, 64);
-          if (lane < 16) red[(rp * kPC + c) * 16 + lane] = acc;
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            float v = acc[m];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            if (lane < 16) red[((rp * M + m) * kPC + c) * 16 + lane] = v;
+          }
         }
        }
         cbar();   // every slot of the share is read, every wave's row sums are in
-        if (tc < s.nslot) ctl_add(lctl + kCtlRel + (q0 + tc) % kRing, 1u);
+        if (tc < s.nslot) ctl_add(lctl + L::CtlRel + (q0 + tc) % kRing, 1u);
         // epilogue: compute thread t -> row t of the share (a softcap unit is one whole wave)
         const int rows = s.nu * s.nrb * kStageRows;
         if (tc - lane < rows) {
           const int t = min(tc, rows - 1);
           const int j = t / (s.nrb * kStageRows), rr = t - j * (s.nrb * kStageRows);
           const int rpg = (j * s.nrb + rr / kStageRows) * s.parts, r16 = rr & 15;
-          float v0 = 0.0f, v1 = 0.0f;
-#pragma unroll
-          for (int w = 0; w < kPC; ++w) v0 += red[(rpg * kPC + w) * 16 + r16];
-          if (s.parts == 2) {
-#pragma unroll
-            for (int w = 0; w < kPC; ++w) v1 += red[((rpg + 1) * kPC + w) * 16 + r16];
-          }
           const int n = share_row(p, s, G, j, 0, 0) + rr;
-          if (tc < rows) {
-            const float yv = (p.coh & 2) ? epilogue<true>(p, s.split, 0, n >> 6, n & 63, v0, v1)
-                                         : epilogue<false>(p, s.split, 0, n >> 6, n & 63, v0, v1);
-            if (p.mbxOut) post_mbx(p, n, yv);
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kPC; ++w) v0 += red[((rpg * M + m) * kPC + w) * 16 + r16];
+            if (s.parts == 2) {
+#pragma unroll
+              for (int w = 0; w < kPC; ++w) v1 += red[(((rpg + 1) * M + m) * kPC + w) * 16 + r16];
+            }
+            if (tc < rows) {
+              const float yv = (p.coh & 2) ? epilogue<true>(p, s.split, m, n >> 6, n & 63, v0, v1)
+                                           : epilogue<false>(p, s.split, m, n >> 6, n & 63, v0, v1);
+              if (M == 1 && p.mbxOut) post_mbx(p, n, yv);
+            }
           }
         }
       } else {
@@ -456,7 +483,9 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
         for (int j = c; j < s.nu; j += kPC) {
           for (int r = 0; r < s.nrb; ++r) {
             for (int pt = 0; pt < s.parts; ++pt) {
-              float acc = 0.0f;
+              float acc[M];
+#pragma unroll
+              for (int m = 0; m < M; ++m) acc[m] = 0.0f;
               for (int h = 0; h < s.nh; ++h) {
                 const int q = q0 + slot_index(s, j, (r * s.parts + pt) * s.nh + h);
                 wait_slot(q);
@@ -471,14 +500,14 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
                     sc[gl] = h2f_u16(slot + 8192 + gl * 32 + rr * 2);
                   }
                   __builtin_amdgcn_s_waitcnt(0xC07F);   // this wave's reads of the slot are done
-                  if (lane == 0) ctl_add(lctl + kCtlRel + q % kRing, 1u);
+                  if (lane == 0) ctl_add(lctl + L::CtlRel + q % kRing, 1u);
 #pragma unroll
                   for (int gl = 0; gl < 8; ++gl) {
                     const int g = 8 * h + gl;
                     float d = dot16_q8(qv[gl], xs + g * 64 + qq * 16);
                     d += __shfl_xor(d, 1, 64);
                     d += __shfl_xor(d, 2, 64);
-                    if (g < s.ngs) acc = __builtin_fmaf(sc[gl], d - 128.0f * (xsum[2 * g] + xsum[2 * g + 1]), acc);
+                    if (g < s.ngs) acc[0] = __builtin_fmaf(sc[gl], d - 128.0f * (xsum[2 * g] + xsum[2 * g + 1]), acc[0]);
                   }
                   continue;
                 }
@@ -490,34 +519,46 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
                   sm[kk] = *(const uint32_t*)(slot + 8192 + (kk * 64 + lane) * 4);
                 }
                 __builtin_amdgcn_s_waitcnt(0xC07F);   // this wave's reads of the slot are done
-                if (lane == 0) ctl_add(lctl + kCtlRel + q % kRing, 1u);
+                if (lane == 0) ctl_add(lctl + L::CtlRel + q % kRing, 1u);
 #pragma unroll
                 for (int kk = 0; kk < 8; ++kk) {
                   const int g = 32 * h + 4 * kk + (lane >> 4);
                   if (g < s.ngs) {
-                    const float d = dot32(qv[kk], xs + g * 32);
-                    acc = __builtin_fmaf(h2f_lo(sm[kk]) * 16777216.0f, d, __builtin_fmaf(h2f_hi(sm[kk]), xsum[g], acc));
+                    const float s24 = h2f_lo(sm[kk]) * 16777216.0f, mn = h2f_hi(sm[kk]);
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                      const float d = dot32(qv[kk], xs + m * xgps * 32 + g * 32);
+                      acc[m] = __builtin_fmaf(s24, d, __builtin_fmaf(mn, xsum[m * xgps + g], acc[m]));
+                    }
                   }
                 }
               }
               if (q8) {
-                if ((lane & 3) == 0) wred[pt * 64 + r * 16 + (lane >> 2)] = acc;
+                if ((lane & 3) == 0) wred[pt * 64 + r * 16 + (lane >> 2)] = acc[0];   // q8 chains have M = 1
                 continue;
               }
-              acc += __shfl_xor(acc, 16, 64);
-              acc += __shfl_xor(acc, 32, 64);
-              if (lane < 16) wred[pt * 64 + r * 16 + lane] = acc;
+#pragma unroll
+              for (int m = 0; m < M; ++m) {
+                float v = acc[m];
+                v += __shfl_xor(v, 16, 64);
+                v += __shfl_xor(v, 32, 64);
+                if (lane < 16) wred[(m * 2 + pt) * 64 + r * 16 + lane] = v;
+              }
             }
           }
           __builtin_amdgcn_s_waitcnt(0xC07F);
           __builtin_amdgcn_wave_barrier();
           const int rows = s.nrb * kStageRows;   // 16, or 64 for a softcap unit (the whole wave)
-          const float v0 = wred[min(lane, rows - 1)], v1 = s.parts == 2 ? wred[64 + min(lane, rows - 1)] : 0.0f;
           const int n = share_row(p, s, G, j, 0, 0) + lane;
-          if (lane < rows || p.epi == P0_EPI_SOFTCAP) {
-            const float yv = (p.coh & 2) ? epilogue<true>(p, s.split, 0, n >> 6, n & 63, v0, v1)
-                                         : epilogue<false>(p, s.split, 0, n >> 6, n & 63, v0, v1);
-            if (p.mbxOut && lane < rows) post_mbx(p, n, yv);
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            const float v0 = wred[m * 128 + min(lane, rows - 1)];
+            const float v1 = s.parts == 2 ? wred[m * 128 + 64 + min(lane, rows - 1)] : 0.0f;
+            if (lane < rows || p.epi == P0_EPI_SOFTCAP) {
+              const float yv = (p.coh & 2) ? epilogue<true>(p, s.split, m, n >> 6, n & 63, v0, v1)
+                                           : epilogue<false>(p, s.split, m, n >> 6, n & 63, v0, v1);
+              if (M == 1 && p.mbxOut && lane < rows) post_mbx(p, n, yv);
+            }
           }
           __builtin_amdgcn_s_waitcnt(0xC07F);
           __builtin_amdgcn_wave_barrier();   // wred is rewritten by this wave's next unit
@@ -535,6 +576,15 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
   if (b == 0 && wait_flags(flags + 0, nullptr) && tc == 0) st_coh(st, tag);
 }
 
-chain_kernel_t pipe_chain_kernel(bool q8) { return q8 ? q4_chain_pipe_kernel<true> : q4_chain_pipe_kernel<false>; }
+chain_kernel_t pipe_chain_kernel(int M, bool q8) {
+  switch (M) {
+    case 1: return q8 ? q4_chain_pipe_kernel<1, true> : q4_chain_pipe_kernel<1, false>;
+    case 2: return q4_chain_pipe_kernel<2, false>;
+    case 3: return q4_chain_pipe_kernel<3, false>;
+    case 4: return q4_chain_pipe_kernel<4, false>;
+    case 5: return q4_chain_pipe_kernel<5, false>;
+  }
+  return nullptr;
+}
 
 }  // namespace p0

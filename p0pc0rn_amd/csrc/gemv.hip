@@ -112,6 +112,7 @@ static int g_chain_spin = 1 << 22;      // polls before a chain wait gives up (a
 static int g_chain_force_give_up = 0;   // tests: every wait gives up at once
 static int g_chain_stage = 1;           // staged ops (weights copied to LDS before the wait) where they fit
 static int g_chain_mbx = 1;             // pipelined chains: mailbox hand-offs where an op reads the previous op's output
+static int g_chain_pipe_m = 1;          // gemvM chains (M <= 5) on the pipelined kernel (1) or the general one (0)
 static int g_pipe_loaders = 2;          // pipelined chain: loader waves that stream
 static int g_pipe_depth = 2;            // pipelined chain: slots in flight per loader wave
 static constexpr size_t kChainLds = 64 * 1024;
@@ -307,18 +308,19 @@ static size_t plan_staged(GemvP& p, int M, int W, int G, int& cur) {
 // where the previous op stopped so each workgroup streams about the same bytes over a step. A share of at most a
 // ring's worth of slots (and few enough rows) is computed by all compute waves together, a larger one by one wave per
 // unit. Returns false (the chain then runs on q4_gemv_chain_kernel) when the weights are not 16-byte aligned
-// (LDS-DMA loads) or a workgroup would get units of two splits.
-static bool plan_pipe(std::vector<GemvP>& ops, int G) {
+// (LDS-DMA loads), a workgroup would get units of two splits, or (M > 1) a split exceeds 2048 k or an op is q8.
+static bool plan_pipe(std::vector<GemvP>& ops, int G, int M) {
   int cur = 0;
   for (GemvP& p : ops) {
     if ((uintptr_t)p.w & 15) return false;
+    if (M > 1 && (p.kPer > 2048 || p.enc != P0_ENC_Q4G32A_T64)) return false;
     const int nrb = p.epi == P0_EPI_SOFTCAP ? 4 : 1, parts = p.epi == P0_EPI_GEGLU ? 2 : 1;
     const int64_t U = (int64_t)(p.N / (kStageRows * nrb)) * p.nsplit;
     if (U > G && G % p.nsplit) return false;
     const int64_t numax = (U + G - 1) / G;
     const int nh = p.enc == P0_ENC_Q8G64S_T64 ? (p.kPer / 64 + 7) / 8 : (p.kPer / 32 + 31) / 32;   // slots per part
     const int64_t nrp = numax * nrb * parts;
-    const bool spread = nrp * nh <= pipe_ring_slots() && nrp <= pipe_spread_parts() && numax * nrb * kStageRows <= 512;
+    const bool spread = nrp * nh <= pipe_ring_slots(M) && nrp <= pipe_spread_parts(M) && numax * nrb * kStageRows <= 512;
     p.su = (int)U;
     p.scur = cur;
     p.snrb = nrb;
@@ -566,31 +568,31 @@ extern "C" int p0_chain_end(void** out) {
       grid = ctx().cu_count * pc;
     }
   }
-  // M = 1: the pipelined kernel, one workgroup per CU, when every op can be planned for it
-  if (cb->M == 1 && g_chain_stage) {
-    chain_kernel_t pk = pipe_chain_kernel(cb->q8);
-    P0_HIP(hipFuncSetAttribute((const void*)pk, hipFuncAttributeMaxDynamicSharedMemorySize, pipe_lds_bytes()),
-           "p0_chain_end");
+  // M <= pipe_max_m(): the pipelined kernel, one workgroup per CU, when every op can be planned for it
+  bool pipe = false;
+  if (cb->M <= pipe_max_m() && g_chain_stage && (cb->M == 1 || g_chain_pipe_m)) {
+    chain_kernel_t pk = pipe_chain_kernel(cb->M, cb->q8);
+    const int plds = pipe_lds_bytes(cb->M);
+    P0_HIP(hipFuncSetAttribute((const void*)pk, hipFuncAttributeMaxDynamicSharedMemorySize, plds), "p0_chain_end");
     int pc = 0;
-    P0_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, (const void*)pk, 64 * pipe_waves(), pipe_lds_bytes()),
-           "p0_chain_end");
+    P0_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, (const void*)pk, 64 * pipe_waves(), plds), "p0_chain_end");
     std::vector<GemvP> planned = cb->ops;
-    if (pc >= 1 && plan_pipe(planned, ctx().cu_count)) {
+    if (pc >= 1 && plan_pipe(planned, ctx().cu_count, cb->M)) {
       cb->ops = planned;
       k = pk;
       cb->W = pipe_waves();
       grid = ctx().cu_count;
-      lds = pipe_lds_bytes();
+      lds = plds;
+      pipe = true;
     }
   }
-  const bool pipe = k == pipe_chain_kernel(false) || k == pipe_chain_kernel(true);
   if (cb->q8 && !pipe) {
     set_error("p0_chain_end: q8g64s.t64 ops join only pipelined chains (M = 1, 16-byte aligned weights, knob 4 on)");
     return P0_EINVAL;
   }
   mark_coherence(cb->ops, cb->M);
   std::vector<int64_t> mb_out, mb_in;
-  const size_t mb_words = pipe && g_chain_mbx ? plan_mailboxes(cb->ops, mb_out, mb_in) : 0;
+  const size_t mb_words = pipe && cb->M == 1 && g_chain_mbx ? plan_mailboxes(cb->ops, mb_out, mb_in) : 0;
   auto* ex = new ChainExec{};
   ex->n_ops = (int)cb->ops.size();
   ex->M = cb->M;
@@ -687,12 +689,14 @@ extern "C" int p0_chain_free(void* chain) {
 // chain knobs: 0 = waves per workgroup for M = 1 (8 or 16), 1 = largest wave share (groups) before K is split
 // across workgroups, 2 = polls before a wait gives up, 3 = 1: every wait gives up at once (tests), 4 = staged ops
 // (1, the default) or none (0), 5 / 6 = loader waves / slots in flight of the pipelined kernel, 7 = mailbox hand-offs
-// in pipelined chains (1, the default) or none (0). Returns the previous value; a value < 0 only reads (knobs 3, 4
-// and 7 also take 0).
+// in pipelined chains (1, the default) or none (0), 8 = gemvM chains of M <= 5 on the pipelined kernel (1, the
+// default) or the general one (0). Returns the previous value; a value < 0 only reads (knobs 3, 4, 7 and 8 also
+// take 0).
 extern "C" int p0_chain_tune(int knob, int value) {
-  if (knob == 7) {
-    const int old = g_chain_mbx;
-    if (value >= 0) g_chain_mbx = value ? 1 : 0;
+  if (knob == 7 || knob == 8) {
+    int* t = knob == 7 ? &g_chain_mbx : &g_chain_pipe_m;
+    const int old = *t;
+    if (value >= 0) *t = value ? 1 : 0;
     return old;
   }
   if (knob == 3) {

@@ -779,12 +779,13 @@ typedef void (*q8_kernel_t)(GemvP);
 q8_kernel_t q8_kernel(int M);
 size_t q8_lds_bytes(int M);
 
-// the pipelined M = 1 chain (chain_pipe.hip): its kernel and its fixed shape
-chain_kernel_t pipe_chain_kernel(bool q8);   // q8: the instantiation that also runs q8g64s.t64 ops
-int pipe_lds_bytes();
+// the pipelined chain (chain_pipe.hip) for M <= pipe_max_m() rows of x: its kernels and their shape
+chain_kernel_t pipe_chain_kernel(int M, bool q8);   // q8 (M = 1 only): the instantiation that also runs q8 ops
+int pipe_lds_bytes(int M);
 int pipe_waves();
-int pipe_ring_slots();
-int pipe_spread_parts();
+int pipe_ring_slots(int M);
+int pipe_spread_parts(int M);
+int pipe_max_m();
 int pipe_cfg_word();   // state word of the loader count (the next word: slots in flight per loader)
 
 #define P0_GEMV_EXTERN(M) \

@@ -153,3 +153,5 @@ def test_chain_tune_knobs_round_trip():
     assert capi.chain_tune(6, -1) == 2 and capi.chain_tune(6, 1) == 2 and capi.chain_tune(6, 2) == 1
     assert capi.chain_tune(7, -1) == 1 and capi.chain_tune(7, 0) == 1 and capi.chain_tune(7, -1) == 0
     assert capi.chain_tune(7, 1) == 0 and capi.chain_tune(7, -1) == 1
+    assert capi.chain_tune(8, -1) == 1 and capi.chain_tune(8, 0) == 1 and capi.chain_tune(8, -1) == 0
+    assert capi.chain_tune(8, 1) == 0 and capi.chain_tune(8, -1) == 1

@@ -134,13 +134,23 @@ class MiniStep:
             b.free()
 
 
-@pytest.mark.parametrize("M,gemvM", [(1, False), (1, True), (3, True), (8, True)])
-def test_chain_matches_oracle(dev, M, gemvM):
+@pytest.mark.parametrize("M,gemvM,pipe_m", [(1, False, 1), (1, True, 1), (2, True, 1), (3, True, 1), (5, True, 1),
+                                             (5, True, 0), (8, True, 1)])
+def test_chain_matches_oracle(dev, M, gemvM, pipe_m):
+    """M <= 5 rows run on the pipelined kernel (knob 8 on), M = 8 and knob 8 off on the general one"""
     s = MiniStep(M=M, gemvM=gemvM, seed=10 + M)
-    ch = s.make_chain()
+    old = capi.chain_tune(8, pipe_m)
+    try:
+        ch = s.make_chain()
+    finally:
+        capi.chain_tune(8, old)
     info = ch.info()
     print("chain", info, flush=True)
     assert info["n_ops"] == 6 and info["m"] == M
+    if M <= 5 and pipe_m:
+        assert info["waves_per_workgroup"] == 12
+    elif M > 1:
+        assert info["waves_per_workgroup"] == 8
     if M == 1 and info["waves_per_workgroup"] == 12:
         assert info["mailboxes"] == 2   # o takes qkv's output, down the geglu output (the others: flags)
     s.reset_outputs()
