@@ -184,7 +184,9 @@ int p0_q4_dequant(const void* w, int64_t w_off, int64_t N, int64_t K, float* out
 /* knob 0: waves a GEMV call aims for before it splits K (default 2048);
  * knob 1: output tiles from which a GEMV wave streams two tiles (default 1024);
  * knob 2: fewest q4 groups a wave streams when K is split (default 2);
- * knob 3: most waves sharing one tile slot's K range inside a workgroup (default 16, at most 16; 8 when M > 2).
+ * knob 3: most waves sharing one tile slot's K range inside a workgroup (default 16, at most 16; 8 when M > 2);
+ * knob 4: fewest x rows M from which a gemvM call outside a chain runs on the matrix cores (default 2, i.e. every
+ *         M > 1; 17: never, the fp32 VALU kernel).
  * value <= 0 only queries. Returns the previous value, or -1 for an unknown knob. */
 int p0_gemv_tune(int knob, int value);
 

@@ -40,6 +40,7 @@ static int g_target_waves = 2048;       // waves a call aims for before it split
 static int g_two_tiles_min_nt = 1024;   // output tiles from which a wave streams two tiles
 static int g_min_gpw = 2;               // fewest q4 groups a wave streams when K is split
 static int g_max_kw = 16;               // most waves that share one tile slot's K-slice inside a workgroup
+static int g_mf_min_m = 2;              // fewest x rows a standalone GEMV-M runs on MFMA (17: never)
 
 struct Plan {
   int mode, gps, nks, kw, tgw, ntb, rowsTot, waves;
@@ -58,16 +59,19 @@ static Plan plan(int M, int NT, int epi, int nsplit, int kPer) {
   const int kws_max = Gs / g_min_gpw > 1 ? Gs / g_min_gpw : 1;
   if (kws > kws_max) kws = kws_max;
   if (kws < 1) kws = 1;
-  const int max_kw = M <= 2 ? g_max_kw : (g_max_kw < 8 ? g_max_kw : 8);   // the kernel's launch bound
+  const bool mf = M >= 2 && M >= g_mf_min_m;   // the MFMA kernel (512 threads)
+  const int max_kw = M <= 2 && !mf ? g_max_kw : (g_max_kw < 8 ? g_max_kw : 8);   // the kernel's launch bound
   pl.kw = kws < max_kw ? kws : max_kw;
   pl.tgw = pl.kw >= 4 ? 1 : 4 / pl.kw;                 // 4 waves per workgroup unless kw is larger
   if (pl.tgw > slots) pl.tgw = slots;
   pl.waves = pl.tgw * pl.kw;
   int nks = (kws + pl.kw - 1) / pl.kw;
   int gps = (Gs + nks - 1) / nks;
-  // LDS: x' and its group sums for the slice, plus the reduction rows
+  // LDS: x' and its group sums for the slice, plus the reduction rows. M >= 2 runs on MFMA (gemv_item): its group
+  // sums take 16 entries per group (a 16-row A operand) when M < 16
   const size_t red = (size_t)pl.waves * T * 64 * sizeof(float);
-  int maxGps = (int)((48 * 1024 - red) / ((size_t)M * 33 * sizeof(float)));
+  const int XS = mf && M < 16 ? 16 : M;
+  int maxGps = (int)((48 * 1024 - red) / ((size_t)M * 32 * sizeof(float) + (size_t)XS * sizeof(float)));
   if (maxGps < 1) maxGps = 1;
   if (gps > maxGps) gps = maxGps;
   for (;;) {   // the partials must fit the workspace: coarser slices until they do
@@ -78,7 +82,7 @@ static Plan plan(int M, int NT, int epi, int nsplit, int kPer) {
   pl.gps = gps;
   pl.nks = nks;
   pl.ntb = (slots + pl.tgw - 1) / pl.tgw;
-  pl.lds = (size_t)M * gps * 33 * sizeof(float) + red;
+  pl.lds = (size_t)M * gps * 32 * sizeof(float) + (size_t)XS * gps * sizeof(float) + red;
   return pl;
 }
 
@@ -385,12 +389,13 @@ static int launch(GemvP& p, int M, const char* op) {
   p.part = ctx().part;
   p.cnt = ctx().counters;
   p.coh = 0;   // chains: set for the whole chain by p0_chain_end
+  p.mf = !cb && M >= 2 && M >= g_mf_min_m;   // must agree with plan()'s LDS layout
   if (cb) {
     cb->ops.push_back(p);
     if (pl.lds > cb->lds) cb->lds = pl.lds;
     return P0_OK;
   }
-  gemv_kernel_t k = pick(M, pl.mode);
+  gemv_kernel_t k = pick(M, pl.mode + (p.mf ? 3 : 0));
   dim3 grid((unsigned)pl.ntb, (unsigned)(p.nsplit * pl.nks));
   hipLaunchKernelGGL(k, grid, dim3(64 * pl.waves), pl.lds, ctx().cur, p);
   P0_LAUNCHED(op);
@@ -508,7 +513,7 @@ extern "C" int p0_q4_gemvM(const p0_gemvm_args_t* a, int32_t* nsplit_out) {
 // tiles, 2 = fewest groups per wave, 3 = most waves per tile slot in a workgroup. Returns the previous value.
 extern "C" int p0_gemv_tune(int knob, int value) {
   int* t = knob == 0 ? &g_target_waves : knob == 1 ? &g_two_tiles_min_nt : knob == 2 ? &g_min_gpw
-         : knob == 3 ? &g_max_kw : nullptr;
+         : knob == 3 ? &g_max_kw : knob == 4 ? &g_mf_min_m : nullptr;
   if (!t) return -1;
   const int old = *t;
   if (value > 0) *t = knob == 3 && value > 16 ? 16 : value;

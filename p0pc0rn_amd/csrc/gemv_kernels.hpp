@@ -73,6 +73,7 @@ struct GemvP {
   unsigned long long* mbxOut;       // this op's mailbox (row n at n), or null
   const unsigned long long* mbxIn;  // x[k] of this op at mbxIn[k], or null
   int flags2;                       // 1: op i also waits for op i - 2's flags (op i - 1 took its input from a mailbox)
+  int mf;             // standalone GEMV-M (M >= 2): the MFMA path (gemv_item), else the fp32 VALU path
 };
 
 __device__ __forceinline__ float gelu_tanh(float v) {   // engine/llm/lops.js:26
@@ -209,6 +210,88 @@ struct Rec {
   uint32_t sm;
 };
 
+// ---- GEMV-M on MFMA (standalone launches, M >= 2). Per q4 group and 16 weight rows, two v_mfma_f32_16x16x32_f16
+// compute D[m][n] = 2^8 sum_k x'[m][k] q[n][k]: the A operand holds 2^8 x' split into fp16 hi + lo (2^8 x' = hi + lo to
+// 2^-22), the B operand the codes as exact fp16 values q (even k) and 16 q (odd k, whose x' carry the 1/16). The matrix
+// cores flush fp16 subnormals, so every operand is kept normal: the codes come out of a code word as 1024 + q
+// (OR-ing the exponent of 1024 into masked nibbles) minus 1024, and the 2^8 keeps lo normal down to |x'| ~ 2^-11.
+// Lane l holds D[4 (l / 16) + i][l % 16]: one weight row per lane, so each lane applies its row's scale and min
+// (2^-8 s D + m sum x') in fp32.
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+constexpr float kMfScale = 256.0f;   // 2^8 x' in the A operand
+constexpr float kMfBig = 255.0f;     // |x'| from which a workgroup keeps the fp32 VALU path (fp16 hi would overflow)
+
+// x' of the slice as MFMA A operands: [group][word w][hi, lo][M rows][8 halves], the 8 halves of word w in the code
+// word's nibble order (k 8w + 0, 4, 1, 5, 2, 6, 3, 7), odd k scaled 1/16; group sums [group][16] (rows >= M zero).
+// Sets *big when some |x'| >= kMfBig (or is not finite).
+template <int M, bool COH>
+__device__ __forceinline__ void stage_x_mf(const GemvP& p, int g0, int g1, int gps, _Float16* xh, float* xsum, int* big) {
+  constexpr int U = 8;
+  const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wv = tid >> 6;
+  const int KL = gps * 32, kb = g0 * 32, ke = g1 * 32, nx = M * KL;
+  if (M < 16)
+    for (int i = tid; i < gps * (16 - M); i += nt) xsum[(i / (16 - M)) * 16 + M + i % (16 - M)] = 0.0f;
+  bool bad = false;
+  for (int i0 = 0; i0 < nx; i0 += U * nt) {
+    int mm[U], kl[U];
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int idx = i0 + u * nt + tid;
+      mm[u] = min(idx / KL, M - 1);
+      kl[u] = idx - mm[u] * KL;
+    }
+    const int nu = ke > kb ? min(U, max(0, (nx - i0 - (wv << 6) + nt - 1) / nt)) : 0;
+    prologue_batch<COH, U, M>(p, nu, mm, kb, ke, kl, v);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float gs = sum32(v[u]);
+      if (i0 + u * nt + tid < nx) {
+        const int g = kl[u] >> 5, kk = kl[u] & 31, w = kk >> 3, j = kk & 7;
+        const float x = (kl[u] & 1) ? v[u] * 0.0625f : v[u];
+        const float xs8 = x * kMfScale;
+        const _Float16 hi = (_Float16)xs8;
+        const _Float16 lo = (_Float16)(xs8 - (float)hi);
+        const int at = (((g * 4 + w) * 2) * M + mm[u]) * 8 + (((j & 3) << 1) | (j >> 2));
+        xh[at] = hi;
+        xh[at + M * 8] = lo;
+        bad = bad || !(__builtin_fabsf(x) < kMfBig);
+        if ((lane & 31) == 0) xsum[g * 16 + mm[u]] = gs;
+      }
+    }
+  }
+  if (bad) *big = 1;
+}
+
+// one group's records of one 64-row tile in the MFMA B layout: lane l holds word l / 16 of rows 16 b + l % 16, and the
+// scale/min words of those rows
+struct RecM {
+  uint32_t q[4];
+  uint32_t sm[4];
+};
+__device__ __forceinline__ RecM load_rec_mf(const GemvP& p, int64_t tile, int g, int lane) {
+  const uint8_t* rec = p.w + (int64_t)__builtin_amdgcn_readfirstlane((int)(tile * p.wG + g)) * 1280;
+  RecM r;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    r.q[b] = *P0_GLOBAL(const uint32_t, rec + (16 * b + (lane & 15)) * 16 + (lane >> 4) * 4);
+    r.sm[b] = *P0_GLOBAL(const uint32_t, rec + 1024 + (16 * b + (lane & 15)) * 4);
+  }
+  return r;
+}
+__device__ __forceinline__ half8_t codes_b(uint32_t v) {
+  const uint32_t v8 = v >> 8;
+  const h2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+  const h2_t a = __builtin_bit_cast(h2_t, (v & 0x000F000Fu) | 0x64006400u) - k1024;    // q: k 8w, 8w + 4
+  const h2_t b = __builtin_bit_cast(h2_t, (v & 0x00F000F0u) | 0x64006400u) - k1024;    // 16 q: k 8w + 1, 8w + 5
+  const h2_t c = __builtin_bit_cast(h2_t, (v8 & 0x000F000Fu) | 0x64006400u) - k1024;   // q: k 8w + 2, 8w + 6
+  const h2_t d = __builtin_bit_cast(h2_t, (v8 & 0x00F000F0u) | 0x64006400u) - k1024;   // 16 q: k 8w + 3, 8w + 7
+  const u32x4l u = {__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), __builtin_bit_cast(uint32_t, c),
+                    __builtin_bit_cast(uint32_t, d)};
+  return __builtin_bit_cast(half8_t, u);
+}
+
 // One record's lane slice: 16 bytes of the lane's row codes and its 4-byte scale/min. Nontemporal loads (STREAM) for
 // ops that stream hundreds of MB (the two-tiles-per-wave mode): they keep the cache for the activations; plain loads
 // otherwise, whose latency is lower (measured on MI355X: dependent HBM loads 280 ns plain, 330 ns nontemporal), which is
@@ -303,7 +386,7 @@ __device__ __forceinline__ float epilogue(const GemvP& p, int split, int m, int 
 // first poll then returns behind those loads (a wave's loads complete in order), which costs nothing when the wait is
 // longer than the loads' latency, and a wave that issued them after the wait would hold the whole workgroup at the
 // prologue's barrier for a full HBM latency.
-template <int M, int MODE, bool CHAIN, class Ready>
+template <int M, int MODE, bool CHAIN, class Ready, bool MFK = false>
 __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float* smem, int* s_last, Ready&& ready) {
   constexpr int T = MODE == 0 ? 1 : 2;
   constexpr int TPW = MODE == 1 ? 2 : 1;   // distinct output tiles per wave
@@ -319,9 +402,13 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kwv = wv % p.kw, tw = wv / p.kw;
   const int KL = p.gps * 32;
-  float* xs = smem;                    // [M][KL]   x' of the slice, odd k scaled 1/16
-  float* xsum = smem + M * KL;         // [M][gps]  group sums of x'
-  float* red = xsum + M * p.gps;       // [waves][T][64] in-workgroup reduction
+  // MF: GEMV-M on MFMA (stage_x_mf); the fp32 VALU path stays for a workgroup whose x' is too large for fp16
+  constexpr bool MF = MFK && !CHAIN && M >= 2;
+  constexpr bool mf = MF;
+  const int XS = mf && M < 16 ? 16 : M;   // group-sum entries per group (MF: a 16-row A operand)
+  float* xs = smem;                    // [M][KL]   x' of the slice, odd k scaled 1/16 (MF: the A operands, same size)
+  float* xsum = smem + M * KL;         // [M][gps]  group sums of x' (MF: [gps][16])
+  float* red = xsum + XS * p.gps;      // [waves][T][64] in-workgroup reduction
 
   const int split = by / p.nks, ks = by - split * p.nks;
   const int k0s = split * p.kPer, k1s = min(p.K, k0s + p.kPer);
@@ -347,7 +434,95 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
   const bool streams = active && wg0 < wg1;
 
   // ---- the share's first chunk is issued before the input is read: its latency overlaps the wait and the prologue
+  if (mf && tid == 0) *s_last = 0;   // MF: the "x' too large" flag until the split-K arrival reuses the word
   __syncthreads();   // the previous item of this workgroup is done with the LDS
+  float acc[T][M];
+  bool mfd = false;   // MF: acc filled by the MFMA path
+  if constexpr (MF) {
+    constexpr int DM = 4;   // groups per chunk of records (8 registers per group and tile)
+    RecM m0[DM][T];
+    if (streams) {
+#pragma unroll
+      for (int i = 0; i < DM; ++i)
+#pragma unroll
+        for (int t = 0; t < T; ++t) m0[i][t] = load_rec_mf(p, tl(t), min(wg0 + i, glast), lane);
+    }
+    stage_x_mf<M, false>(p, g0, g1, p.gps, (_Float16*)xs, xsum, s_last);
+    __syncthreads();
+    if (*s_last == 0) {
+      float am[T][4][4];   // [tile][16-row block][i]: rows 16 b + lane % 16, x row 4 (lane / 16) + i
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) am[t][b][i] = 0.0f;
+      const _Float16* xh = (const _Float16*)xs;
+      const int arow = min(lane & 15, M - 1), aw = lane >> 4;
+      auto consume_mf = [&](const RecM (&cur)[T], int g) {
+        const int gl = g - g0;
+        const half8_t z = {};
+        const half8_t* ap = (const half8_t*)(xh + (((gl * 4 + aw) * 2) * M + arow) * 8);
+        const half8_t ahi = (lane & 15) < M ? ap[0] : z, alo = (lane & 15) < M ? ap[M] : z;
+        const f4_t sx = *(const f4_t*)(xsum + gl * 16 + 4 * aw);
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const half8_t bq = codes_b(cur[t].q[b]);
+            f4_t d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bq, d, 0, 0, 0);
+            const float s8 = h2f_lo(cur[t].sm[b]) * (1.0f / kMfScale), mn = h2f_hi(cur[t].sm[b]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) am[t][b][i] = __builtin_fmaf(s8, d[i], __builtin_fmaf(mn, sx[i], am[t][b][i]));
+          }
+      };
+      if (streams) {
+#pragma unroll
+        for (int i = 0; i < DM; ++i)
+          if (wg0 + i < wg1) consume_mf(m0[i], wg0 + i);
+        for (int c0 = wg0 + DM; c0 < wg1; c0 += DM) {
+          RecM r[DM][T];
+#pragma unroll
+          for (int i = 0; i < DM; ++i)
+#pragma unroll
+            for (int t = 0; t < T; ++t) r[i][t] = load_rec_mf(p, tl(t), min(c0 + i, glast), lane);
+#pragma unroll
+          for (int i = 0; i < DM; ++i)
+            if (c0 + i < wg1) consume_mf(r[i], c0 + i);
+        }
+      }
+      // back to one weight row per lane (acc[t][m] at lane = row) through this wave's reduction row: x row m lives in
+      // the 16 lanes l / 16 == m / 4, element m % 4, for rows 16 b + l % 16. Lanes hand values to other lanes here, so
+      // a wavefront fence on each side keeps the compiler from moving a read above other lanes' writes (the LDS itself
+      // serves one wave's accesses in order)
+      auto wave_sync = [] {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      };
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        float* tr = red + (wv * T + t) * 64;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          wave_sync();
+          if ((lane >> 4) == (m >> 2)) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) tr[16 * b + (lane & 15)] = am[t][b][m & 3];
+          }
+          wave_sync();
+          acc[t][m] = tr[lane];
+        }
+      }
+      mfd = true;
+    } else {
+      __syncthreads();   // x' too large for fp16: this workgroup stages fp32 x' and takes the VALU path
+      stage_x<M, false>(p, g0, g1, p.gps, xs, xsum);
+      __syncthreads();
+    }
+  }
+  if (!mfd) {
   Rec r0[D][T];
   if (streams) {
 #pragma unroll
@@ -358,12 +533,13 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
   if (!ready()) return false;
 
   // ---- prologue: x'[m][k] for the workgroup's K-slice -> LDS (odd k scaled 1/16), and the per-group sums of x'
-  if (coh_in) stage_x<M, true>(p, g0, g1, p.gps, xs, xsum);
-  else stage_x<M, false>(p, g0, g1, p.gps, xs, xsum);
-  __syncthreads();
+  if (!mf) {
+    if (coh_in) stage_x<M, true>(p, g0, g1, p.gps, xs, xsum);
+    else stage_x<M, false>(p, g0, g1, p.gps, xs, xsum);
+    __syncthreads();
+  }
 
   // ---- stream the records of the wave's share
-  float acc[T][M];
 #pragma unroll
   for (int t = 0; t < T; ++t)
 #pragma unroll
@@ -404,6 +580,7 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
         if (c0 + i < wg1) consume(r[i], c0 + i);
     }
   }
+  }   // !mfd
 
   // ---- the kw waves of a slot: sum their shares in wave order into wave kwv == 0. The reads are unrolled to the
   // largest kw (the workgroup's wave count) with clamped indices, so they issue back to back and wait once; the
@@ -638,6 +815,15 @@ __global__ __launch_bounds__(M <= 2 ? 1024 : 512) void q4_gemv_kernel(GemvP p) {
   gemv_item<M, MODE, false>(p, blockIdx.x, blockIdx.y, smem, &s_last, [] { return true; });
 }
 
+// the same GEMV-M on the matrix cores (M >= 2; the host sends p.mf calls here, with at most 8 waves per workgroup)
+template <int M, int MODE>
+__global__ __launch_bounds__(512) void q4_gemv_mf_kernel(GemvP p) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  __shared__ int s_last;
+  auto ready = [] { return true; };
+  gemv_item<M, MODE, false, decltype(ready)&, true>(p, blockIdx.x, blockIdx.y, smem, &s_last, ready);
+}
+
 // ---- the chain executor: a recorded sequence of GEMV ops in ONE persistent launch (the analogue of the reference's
 // per-token command buffer, engine/llm/drunner.js:1-8). Op i may read what ops < i wrote, so its items wait until op
 // i - 1 has written all of its outputs; each workgroup issues its first item's weight loads BEFORE that wait, so the
@@ -762,7 +948,12 @@ typedef void (*gemv_kernel_t)(GemvP);
 typedef void (*chain_kernel_t)(const GemvP*, int, unsigned*, int);
 
 template <int M>
-gemv_kernel_t pick_m(int mode) {
+gemv_kernel_t pick_m(int mode) {   // modes 3..5: modes 0..2 on the matrix cores (M >= 2)
+  if constexpr (M >= 2) {
+    if (mode == 3) return q4_gemv_mf_kernel<M, 0>;
+    if (mode == 4) return q4_gemv_mf_kernel<M, 1>;
+    if (mode == 5) return q4_gemv_mf_kernel<M, 2>;
+  }
   if (mode == 0) return q4_gemv_kernel<M, 0>;
   if (mode == 1) return q4_gemv_kernel<M, 1>;
   return q4_gemv_kernel<M, 2>;

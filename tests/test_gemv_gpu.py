@@ -200,18 +200,40 @@ def test_gemv_softcap_ties_take_the_lower_row(dev):
 
 
 # ------------------------------------------------------------------------------------------------ gemvM
+@pytest.fixture(params=["valu", "mfma"])
+def mf(request):
+    """p0_gemv_tune knob 4: every M on the fp32 VALU kernel (17), or M >= 2 on the matrix-core kernel (2, the
+    default)"""
+    old = capi.gemv_tune(4, 2 if request.param == "mfma" else 17)
+    yield request.param
+    capi.gemv_tune(4, old)
+
+
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 16])
-def test_gemvM_rms_store(dev, M):
-    Case(M, 256, 1024, "rms", "store", seed=30 + M, gemvM=True).check(f"gemvM M={M} rms.store")
+def test_gemvM_rms_store(dev, mf, M):
+    Case(M, 256, 1024, "rms", "store", seed=30 + M, gemvM=True).check(f"gemvM M={M} rms.store ({mf})")
 
 
 @pytest.mark.parametrize("pro,epi", [("raw", "geglu"), ("rms", "softcap"), ("pleg", "store"), ("raw", "store")])
-def test_gemvM_verify_shapes(dev, pro, epi):
-    Case(5, 192, 512, pro, epi, seed=41, gemvM=True).check(f"gemvM M=5 {pro}.{epi}")
+def test_gemvM_verify_shapes(dev, mf, pro, epi):
+    Case(5, 192, 512, pro, epi, seed=41, gemvM=True).check(f"gemvM M=5 {pro}.{epi} ({mf})")
 
 
-def test_gemvM_splits_and_strides(dev):
-    Case(5, 128, 8192, "raw", "store", kPer=2048, ldx=8192 + 32, ldm=128 + 64, seed=43, gemvM=True).check("gemvM splits")
+@pytest.mark.parametrize("M", [9, 16])
+@pytest.mark.parametrize("pro,epi", [("raw", "geglu"), ("rms", "softcap")])
+def test_gemvM_large_M_epilogues(dev, M, pro, epi):
+    Case(M, 192, 512, pro, epi, seed=45 + M, gemvM=True).check(f"gemvM M={M} {pro}.{epi}")
+
+
+def test_gemvM_splits_and_strides(dev, mf):
+    Case(5, 128, 8192, "raw", "store", kPer=2048, ldx=8192 + 32, ldm=128 + 64, seed=43, gemvM=True).check(
+        f"gemvM splits ({mf})")
+
+
+def test_gemvM_mf_knob(dev):
+    old = capi.gemv_tune(4, 0)
+    assert old == 2, "default: the matrix-core GEMV-M for every M > 1"
+    assert capi.gemv_tune(4, 3) == 2 and capi.gemv_tune(4, old) == 3
 
 
 def test_gemvM_row_equals_gemv(dev):
@@ -225,3 +247,19 @@ def test_gemvM_row_equals_gemv(dev):
         c1.x[:K] = cm.x[m * K:(m + 1) * K]
         y1 = c1.run_gpu()[0][:N]
         assert rel_l2(ym[m * N:(m + 1) * N], y1) < 1e-6
+
+
+def test_gemvM_two_tiles_per_wave(dev, mf):
+    """1024 output tiles and more: each wave streams two tiles (the head's mode), here with the softcap epilogue"""
+    Case(3, 65536, 256, "rms", "softcap", seed=61, gemvM=True).check(f"gemvM M=3 two tiles per wave ({mf})")
+
+
+@pytest.mark.parametrize("M", [2, 5, 16])
+def test_gemvM_large_activations_keep_fp32(dev, mf, M):
+    """M >= 2 runs on MFMA with 2^8 x' split into fp16 hi + lo; a workgroup whose x' reaches 255 (fp16 would
+    overflow) takes the fp32 path instead. Large values sit in one K-slice only, so both paths run in one call, and the
+    split partials still meet the fp32 bar."""
+    c = Case(M, 128, 8192, "raw", "store", kPer=2048, seed=62 + M, gemvM=True)
+    for m in range(M):
+        c.x[m * 8192 + 4096: m * 8192 + 4096 + 7] = np.float32([400.0, -900.0, 330.0, 1.0e5, -3.5e3, 600.0, 2.0e4])
+    c.check(f"gemvM M={M} large activations ({mf})")
