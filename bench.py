@@ -313,6 +313,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="decode step only")
+    ap.add_argument("--verify-m", default="1,2,4,5,8,16",
+                    help="x rows of the verify passes timed (config C); empty: none")
+    ap.add_argument("--no-config-a", action="store_true", help="skip the single-GEMV ring (config A)")
     ap.add_argument("--no-breakdown", action="store_true",
                     help="skip the per-projection timings (short runs under PMC counters)")
     ap.add_argument("--calibrate", action="store_true",
@@ -345,10 +348,13 @@ def main():
                              "ms_graph": round(dec["ms_graph"], 4), "chain": dec["chain"],
                              "by_projection": dec["by_kind"]}}
     if not args.no_extra:
-        extra["config_a_gemv"] = bench_config_a(c)
-        log("config A", extra["config_a_gemv"])
-        extra["verify_sweep"] = bench_verify(c, step)
-        log("verify sweep", extra["verify_sweep"])
+        if not args.no_config_a:
+            extra["config_a_gemv"] = bench_config_a(c)
+            log("config A", extra["config_a_gemv"])
+        vm = tuple(int(v) for v in args.verify_m.split(",") if v.strip())
+        if vm:
+            extra["verify_sweep"] = bench_verify(c, step, vm)
+            log("verify sweep", extra["verify_sweep"])
     for t in step.layers:
         for (b, n, k) in t.values():
             b.free()

@@ -223,15 +223,17 @@ constexpr float kMfScale = 256.0f;   // 2^8 x' in the A operand
 constexpr float kMfBig = 255.0f;     // |x'| from which a workgroup keeps the fp32 VALU path (fp16 hi would overflow)
 
 // x' of the slice as MFMA A operands: [group][word w][hi, lo][M rows][8 halves], the 8 halves of word w in the code
-// word's nibble order (k 8w + 0, 4, 1, 5, 2, 6, 3, 7), odd k scaled 1/16; group sums [group][16] (rows >= M zero).
-// Sets *big when some |x'| >= kMfBig (or is not finite).
-template <int M, bool COH>
-__device__ __forceinline__ void stage_x_mf(const GemvP& p, int g0, int g1, int gps, _Float16* xh, float* xsum, int* big) {
+// word's nibble order (k 8w + 0, 4, 1, 5, 2, 6, 3, 7), odd k scaled 1/16; group sums [group][XSS] (rows >= M zero).
+// tid / nt: the calling thread among the nt staging threads (whole waves). True in a thread that saw some
+// |x'| >= kMfBig (or not finite): the caller then stages fp32 x' for the VALU arithmetic instead.
+template <int M, bool COH, int XSS>
+__device__ __forceinline__ bool stage_x_mf(const GemvP& p, int g0, int g1, int gps, _Float16* xh, float* xsum, int tid,
+                                           int nt) {
   constexpr int U = 8;
-  const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wv = tid >> 6;
+  const int lane = tid & 63, wv = tid >> 6;
   const int KL = gps * 32, kb = g0 * 32, ke = g1 * 32, nx = M * KL;
-  if (M < 16)
-    for (int i = tid; i < gps * (16 - M); i += nt) xsum[(i / (16 - M)) * 16 + M + i % (16 - M)] = 0.0f;
+  if (M < XSS)
+    for (int i = tid; i < gps * (XSS - M); i += nt) xsum[(i / (XSS - M)) * XSS + M + i % (XSS - M)] = 0.0f;
   bool bad = false;
   for (int i0 = 0; i0 < nx; i0 += U * nt) {
     int mm[U], kl[U];
@@ -257,11 +259,11 @@ __device__ __forceinline__ void stage_x_mf(const GemvP& p, int g0, int g1, int g
         xh[at] = hi;
         xh[at + M * 8] = lo;
         bad = bad || !(__builtin_fabsf(x) < kMfBig);
-        if ((lane & 31) == 0) xsum[g * 16 + mm[u]] = gs;
+        if ((lane & 31) == 0) xsum[g * XSS + mm[u]] = gs;
       }
     }
   }
-  if (bad) *big = 1;
+  return bad;
 }
 
 // one group's records of one 64-row tile in the MFMA B layout: lane l holds word l / 16 of rows 16 b + l % 16, and the
@@ -447,7 +449,7 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
 #pragma unroll
         for (int t = 0; t < T; ++t) m0[i][t] = load_rec_mf(p, tl(t), min(wg0 + i, glast), lane);
     }
-    stage_x_mf<M, false>(p, g0, g1, p.gps, (_Float16*)xs, xsum, s_last);
+    if (stage_x_mf<M, false, (M < 16 ? 16 : M)>(p, g0, g1, p.gps, (_Float16*)xs, xsum, tid, blockDim.x)) *s_last = 1;
     __syncthreads();
     if (*s_last == 0) {
       float am[T][4][4];   // [tile][16-row block][i]: rows 16 b + lane % 16, x row 4 (lane / 16) + i
