@@ -331,3 +331,103 @@ const st = new P.PackStore(g, { dir: 'pack' });
         O.q4_gemv(capi.gemv_args(w=w.ctypes.data, w_enc=enc, w_rows=128, w_cols=256, x=x.ctypes.data, N=128, K=256,
                                  y=want.ctypes.data))
         assert rel_l2(got, want) <= 2e-5, key
+
+
+def test_js_pick_surface_and_v5_errors(tmp_path):
+    """engine/llm/lopsx.js:225-328: kxPick follows PICK, setPicks overrides it (a non-object value = the engine's own
+    kernel), setKX(false) turns picks off, okV5 needs a 4-bit weight at a 16-byte offset with K % 32 == 0; the v5
+    entry points refuse what the reference's v5 path refuses, with its texts, before any device call."""
+    out = run_node(tmp_path, r"""
+const g = {}, B = { ptr: 0 };
+const w = (rows, cols, off = 0, enc = 'q4g32a.t64') => ({ buf: B, off, enc, rows, cols });
+const a = (N, K, pro, epi, extra = {}) => Object.assign({ w: w(N, K), x: { buf: B }, N, K, pro, epi, y: { buf: B } }, extra);
+const r = {};
+r.nPick = Object.keys(P.PICK).length;
+r.head = P.kxPick(a(262144, 1536, 'rms', 'softcap'));
+r.e2b = P.kxPick(a(8192, 2048, 'rms', 'geglu'));
+r.off8 = P.kxPick(Object.assign(a(262144, 1536, 'rms', 'softcap'), { w: w(262144, 1536, 8) }));
+r.q8 = P.kxPick(Object.assign(a(262144, 1536, 'rms', 'softcap'), { w: w(262144, 1536, 0, 'q8g64s.t64') }));
+P.setPicks({ 'rms.geglu.8192x2048': { ND: 2, L: 16 }, 'rms.softcap.262144x1536': 'engine' });
+r.over = P.kxPick(a(8192, 2048, 'rms', 'geglu'));
+r.engine = P.kxPick(a(262144, 1536, 'rms', 'softcap'));
+r.kept = P.kxPick(a(1536, 6144, 'raw', 'store'));
+r.now = P.picksNow();
+P.setKX(false); r.off = P.kxPick(a(1536, 6144, 'raw', 'store')); P.setKX(true);
+P.setPicks(null); r.reset = P.kxPick(a(262144, 1536, 'rms', 'softcap')); r.nowNull = P.picksNow();
+r.direct = [P.directOkV5({ x: { rowB: 8 }, K: 64 }), P.directOkV5({ x: { rowB: 6 }, K: 64 }),
+            P.directOkV5({ x: { ldx: 66 }, K: 64 }), P.directOkV5({ x: {}, K: 64, norm: { off: 2 } })];
+r.u8 = P.u8ok(); r.needs = P.DIRECT_NEEDS; r.ver = P.KERNEL_VERSION;
+const errs = [];
+const t = (f) => { try { f(); errs.push('no error'); } catch (e) { errs.push(e.message); } };
+t(() => P.gemvV5(g, Object.assign(a(64, 256, 'raw', 'store'), { w: w(64, 256, 4) })));
+t(() => P.gemvV5(g, a(64, 256, 'raw', 'store'), { ND: 1, L: 16 }));
+t(() => P.gemvV5(g, a(64, 4096, 'raw', 'store')));
+t(() => P.gemvV5(g, a(64, 4096, 'rms', 'geglu', { kPer: 2048 })));
+t(() => P.gemvV5(g, a(96, 256, 'raw', 'store')));
+t(() => P.gemvV5(g, a(64, 256, 'raw', 'store', { kPer: 48 })));
+t(() => P.gemvMV5(g, a(64, 8192, 'rms', 'softcap', { M: 2, kPer: 4096 })));
+t(() => P.gemvMV5(g, a(96, 256, 'raw', 'store', { M: 2 })));
+t(() => P.v5code({ M: 1 }));
+r.errs = errs;
+console.log(JSON.stringify(r));
+""")
+    r = json.loads(out.strip().splitlines()[-1])
+    assert r["nPick"] == 17
+    assert r["head"] == {"ND": 4, "L": 16, "deq": "mask"}
+    assert r["e2b"] is None and r["off8"] is None and r["q8"] is None   # not a key / not okV5
+    assert r["over"] == {"ND": 2, "L": 16} and r["engine"] is None
+    assert r["kept"] == {"ND": 4, "L": 16, "mode": "direct"}
+    assert r["now"] == {"rms.geglu.8192x2048": {"ND": 2, "L": 16}, "rms.softcap.262144x1536": "engine"}
+    assert r["off"] is None and r["reset"] == {"ND": 4, "L": 16, "deq": "mask"} and r["nowNull"] is None
+    assert r["direct"] == [True, False, False, False]
+    assert r["u8"] is False and r["needs"] == {"gemv": 9, "gemvM": 10} and r["ver"] == "mi355x-hip-1"
+    assert r["errs"] == [
+        "kernx v5: not a 4-bit, 16-byte aligned, K % 32 weight",
+        "kernx v5: 1024 threads",
+        "kernx v5: K 4096 needs a kPer",
+        "kernx v5: geglu needs one split",
+        "kernx v5: N % 64",
+        "kernx v5: kPer must be a multiple of 32",
+        "kernx v5: softcap needs one split",
+        "kernx v5: N % 64",
+        'kernx v5: no WGSL on the HIP backend (config {"M":1})',
+    ]
+
+
+@pytest.mark.gpu
+def test_js_v5_entry_points_match_gemv(tmp_path):
+    """gemvV5 / gemvMV5 with the reference's pick options run the same kernels as gemv / gemvM: the same split count
+    and the same bits, and those agree with the oracle (2e-5 relative L2, inside BASELINE's 1e-3)."""
+    N, K, M = 1536, 6144, 3
+    w, _ = O.pack_q4(O.randn(N * K, 21, 0.05), N, K)
+    x = O.randn(M * K, 22)
+    _save(tmp_path, w=w, x=x)
+    out = run_node(tmp_path, r"""
+const g = await_gpu();
+const up = (name) => { const b = fs.readFileSync(name + '.bin'); return g.upload(new Uint8Array(b.buffer, b.byteOffset, b.length)); };
+const [w, x] = ['w', 'x'].map(up);
+const N = 1536, K = 6144, M = 3, kPer = 2048;
+const W = { buf: w, off: 0, enc: 'q4g32a.t64', rows: N, cols: K };
+const ys = [0, 1, 2, 3].map(() => g.buffer(M * N * 3 * 4));
+const a1 = (y) => ({ w: W, x: { buf: x, rowB: 0 }, N, K, kPer, pro: 'raw', epi: 'store', y: { buf: y } });
+const aM = (y) => ({ w: W, x: { buf: x, ldx: K }, M, N, K, kPer, pro: 'raw', epi: 'store', y: { buf: y, ldm: N } });
+const pick = P.kxPick(a1(ys[0]));
+const ns = [P.gemv(g, a1(ys[0])), P.gemvV5(g, a1(ys[1]), pick), P.gemvM(g, aM(ys[2])), P.gemvMV5(g, aM(ys[3]), pick)];
+(async () => {
+  await g.done();
+  for (let i = 0; i < 4; ++i) fs.writeFileSync('y' + i + '.bin', Buffer.from(await g.read(ys[i])));
+  console.log(JSON.stringify({ ns, pick }));
+  g.freeAll(); g.device.destroy();
+})();
+""")
+    r = json.loads(out.strip().splitlines()[-1])
+    assert r["pick"] == {"ND": 4, "L": 16, "mode": "direct"} and r["ns"] == [3, 3, 3, 3]
+    y = [np.fromfile(str(tmp_path / ("y%d.bin" % i)), np.float32) for i in range(4)]
+    n1, nM = 3 * N, 3 * M * N
+    assert np.array_equal(y[0][:n1], y[1][:n1]) and np.array_equal(y[2][:nM], y[3][:nM])
+    want = np.zeros(3 * M * N, np.float32)
+    O.q4_gemvM(capi.gemvm_args(w=w.ctypes.data, w_rows=N, w_cols=K, x=x.ctypes.data, x_ldx=K, M=M, N=N, K=K,
+                               kPer=2048, y=want.ctypes.data, y_ldm=N))
+    r2 = rel_l2(y[3][:nM], want)
+    print("gemvMV5", r2)
+    assert np.all(np.isfinite(y[3][:nM])) and r2 <= 2e-5
