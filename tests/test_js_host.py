@@ -63,7 +63,8 @@ P.createGpu({ device: 0 }).then(() => res.push('no error'), (e) => res.push((e i
     assert res[5] == "gemvM: prologue sum"
     assert res[6] == "gemm: K must be a multiple of 32"
     assert res[7].startswith("gemm: unsupported weight encoding")
-    assert res[8].startswith("GpuError: ") and ("no HIP device" in res[8] or "gfx950" in res[8])
+    if not os.path.exists("/dev/kfd"):   # no GPU driver here: opening a device must fail with GpuError
+        assert res[8].startswith("GpuError: ") and ("no HIP device" in res[8] or "gfx950" in res[8])
 
 
 def _save(tmp_path, **arrays):
