@@ -71,8 +71,9 @@ class Step:
         st[1::2] = 1.0 / np.sqrt(1.0 + 1e-6)
         self.st = c.to_device(st)
         self.qkvp = c.Buffer(M * QKV * 4)
-        self.tpart = c.Buffer(4 * M * D * 4)
+        self.obuf = c.Buffer(M * D * 4)
         self.mbuf = c.Buffer(M * MLP * 4)
+        self.dpart = c.Buffer(4 * M * D * 4)
         self.logits = c.Buffer(M * VOCAB * 4)
         mx = np.zeros(M * (VOCAB // 64) * 2 + 2 * M + 4, np.float32)
         mx[M * (VOCAB // 64) * 2 + 1::2] = 1.0
@@ -80,40 +81,43 @@ class Step:
         self.mx_stat_off = M * (VOCAB // 64) * 2 + 1
 
     def free_acts(self):
-        for b in (self.x, self.st, self.qkvp, self.tpart, self.mbuf, self.logits, self.mx):
+        for b in (self.x, self.st, self.qkvp, self.obuf, self.mbuf, self.dpart, self.logits, self.mx):
             b.free()
 
     # one projection, M = 1 through gemv, M > 1 through gemvM (the reference's decode / verify call pairs)
-    def proj(self, w, n, k, x, y, pro="raw", epi="store", kPer=0, stat=None, stat_off=0, mx=None):
+    def proj(self, w, n, k, x, y, pro="raw", epi="store", kPer=0, stat=None, stat_off=0, mx=None, ldx=0):
         c, M = self.c, self.M
+        N = n // 2 if epi == "geglu" else n   # a geglu's weight holds the gate rows, then the up rows
         if M == 1:
-            a = c.gemv_args(w=w, w_rows=n if epi != "geglu" else n, w_cols=k, x=x, N=n if epi != "geglu" else n // 2,
-                            K=k, kPer=kPer, pro=c.PRO[pro], epi=c.EPI[epi], y=y, stat=stat, stat_off=stat_off,
-                            norm=self.nw, mx=mx)
+            a = c.gemv_args(w=w, w_rows=n, w_cols=k, x=x, N=N, K=k, kPer=kPer, pro=c.PRO[pro], epi=c.EPI[epi], y=y,
+                            stat=stat, stat_off=stat_off, norm=self.nw, mx=mx)
             return c.q4_gemv(a)
-        a = c.gemvm_args(w=w, w_rows=n, w_cols=k, x=x, x_ldx=k, M=M, N=n if epi != "geglu" else n // 2, K=k,
-                         kPer=kPer, pro=c.PRO[pro], epi=c.EPI[epi], y=y, stat=stat, stat_off=stat_off, stat_ld=2,
-                         norm=self.nw, mx=mx)
+        a = c.gemvm_args(w=w, w_rows=n, w_cols=k, x=x, x_ldx=ldx or k, M=M, N=N, K=k, kPer=kPer, pro=c.PRO[pro],
+                         epi=c.EPI[epi], y=y, stat=stat, stat_off=stat_off, stat_ld=2, norm=self.nw, mx=mx)
         return c.q4_gemvM(a)
 
     def ops(self, only=None):
-        """enqueue the step (or only one projection kind over all layers)"""
-        for t in self.layers:
+        """enqueue the step (or only one projection kind over all layers). Every op reads its predecessor's output:
+        o the q rows of qkv, gate_up o's output, down gate_up's, the next layer's qkv (and the head) the first K-split
+        partial of down. In the model a norm sits between some of them (normadd / rowstats, not GEMVs, not part of
+        the step); their rstd slots are fixed inputs here."""
+        for li, t in enumerate(self.layers):
+            xin = self.x if li == 0 else self.dpart
             if only in (None, "qkv"):
                 b, n, k = t["qkv"]
-                self.proj(b, n, k, self.x, self.qkvp, "rms", stat=self.st, stat_off=1)
+                self.proj(b, n, k, xin, self.qkvp, "rms", stat=self.st, stat_off=1)
             if only in (None, "o"):
                 b, n, k = t["o"]
-                self.proj(b, n, k, self.qkvp, self.tpart, "raw", kPer=2048)
+                self.proj(b, n, k, self.qkvp, self.obuf, "raw", kPer=2048, ldx=QKV)
             if only in (None, "gu"):
                 b, n, k = t["gu"]
-                self.proj(b, n, k, self.x, self.mbuf, "rms", "geglu", stat=self.st, stat_off=1)
+                self.proj(b, n, k, self.obuf, self.mbuf, "rms", "geglu", stat=self.st, stat_off=1)
             if only in (None, "down"):
                 b, n, k = t["down"]
-                self.proj(b, n, k, self.mbuf, self.tpart, "raw", kPer=2048)
+                self.proj(b, n, k, self.mbuf, self.dpart, "raw", kPer=2048)
         if only in (None, "head"):
             # the head's rms slot lives in the mx buffer past the tile maxima (engine/llm/gemma4.js:505-508)
-            self.proj(self.head, VOCAB, D, self.x, self.logits, "rms", "softcap", stat=self.mx,
+            self.proj(self.head, VOCAB, D, self.dpart, self.logits, "rms", "softcap", stat=self.mx,
                       stat_off=self.mx_stat_off, mx=self.mx)
 
     def step_bytes(self, only=None):

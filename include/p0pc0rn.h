@@ -57,13 +57,15 @@ enum { P0_ENC_Q4G32A_T64 = 1, P0_ENC_Q8G64S_T64 = 2, P0_ENC_F16 = 3 };          
 enum { P0_PRO_RAW = 0, P0_PRO_RMS = 1, P0_PRO_SUM = 2, P0_PRO_PLEG = 3 };           /* gemv / gemvM a.pro */
 enum { P0_EPI_STORE = 0, P0_EPI_GEGLU = 1, P0_EPI_SOFTCAP = 2 };                    /* gemv / gemvM a.epi */
 enum { P0_XMODE_F16 = 0, P0_XMODE_LNMOD = 1, P0_XMODE_RMS = 2, P0_XMODE_BF16 = 3 }; /* gemm a.x.mode */
-enum { P0_GEPI_F16 = 0, P0_GEPI_F32 = 1, P0_GEPI_RESADD = 2, P0_GEPI_SWIGLU = 3, P0_GEPI_BIAS = 4 }; /* gemm a.epi */
+enum { P0_GEPI_F16 = 0, P0_GEPI_F32 = 1, P0_GEPI_RESADD = 2, P0_GEPI_SWIGLU = 3, P0_GEPI_BIAS = 4,
+       P0_GEPI_HEADS = 5 };                                                         /* gemm a.epi */
+enum { P0_ROPE_INTER = 0, P0_ROPE_HALF = 1 };                                       /* gemm a.heads.ropeMode */
 enum { P0_ACT_SILU = 0, P0_ACT_GELU = 1 };                                          /* gemm a.act (swiglu) */
 
 /* ---- device / buffers ------------------------------------------------------------------------------------------ */
 const char* p0_last_error(void);
 int p0_version(void);                          /* library ABI version (P0_ABI_VERSION) */
-#define P0_ABI_VERSION 1
+#define P0_ABI_VERSION 2
 
 typedef struct {
   char name[64];          /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
@@ -100,10 +102,16 @@ int p0_timer_stop(float* ms);
 /* ---- recorded op sequences: the decode-step recorder (engine/llm/drunner.js:1-8, 83-101 DecodeRunner) ------------ */
 /* Between p0_record_begin and p0_record_end the ops called on this thread are recorded (HIP stream capture of the
  * current stream) instead of run; p0_replay enqueues the whole recorded sequence with one launch. The library's ops
- * clear nothing with memset and leave their split-K counters at zero, so a recording replays any number of times. */
+ * clear nothing with memset and leave their split-K counters at zero, so a recording replays any number of times.
+ * Buffers: the caller's buffers must outlive the recording. The library memory its kernels read (the GEMM's activation
+ * staging workspace, the op table and state of a chain run inside it) is held by the recording: a later growth of the
+ * workspace or a p0_chain_free leaves it in place until p0_record_free. A GEMM call that needs a larger staging
+ * workspace than the current one is refused while recording (run it once before, or use p0_q4_gemm_noalloc).
+ * p0_record_info gives the number of launches a replay makes (the DecodeRunner's dispatch count). */
 int p0_record_begin(void);
 int p0_record_end(void** rec_out);
 int p0_replay(void* rec);
+int p0_record_info(void* rec, int32_t* launches);
 int p0_record_free(void* rec);
 
 /* ---- q4g32a.t64 GEMV: y = x W^T for ONE row (engine/llm/lops.js:108-141) ---------------------------------------- */
@@ -173,6 +181,17 @@ typedef struct {
   int32_t act;         /* swiglu activation */
   int32_t store;       /* resadd: 1 = Y = gate * (acc + bias) instead of += */
   int32_t res;         /* bias: 1 = add the previous Y in place */
+  /* heads (engine/ops/gemm.js:212-250, a.heads): every 128 output columns are one head; head h is a query head for
+   * h < hq, a key head for h < hq + hkv, else a value head. Query and key heads are RMS-normalised over their 128 values
+   * (eps), times the norm weights (ev[ev_off + c] for queries, ev[ev_off + 128 + c] for keys), then rotated by the
+   * RoPE table rope[row][64][cos, sin] (row = heads_row_off + m): heads_rope P0_ROPE_INTER pairs columns (2p, 2p + 1)
+   * with entry p, P0_ROPE_HALF pairs (d, d + 64) with entry d. Every head is written as fp16, head-major:
+   * Y[((h * heads_ltot) + heads_row_off + m) * 128 + c] from byte y_off (y_ld and y_n0 are not used). */
+  int64_t heads_ltot, heads_row_off;
+  int32_t heads_hq, heads_hkv;
+  float heads_eps;     /* 0 = 1e-6 */
+  int32_t heads_rope;
+  const float* rope;   /* the RoPE table (a.heads.rope.buf) */
 } p0_gemm_args_t;
 int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out);
 

@@ -342,6 +342,48 @@ int p0o_q4_gemvM(const p0_gemvm_args_t* a) {   /* engine/llm/lops_spec.js:163-19
 static inline float bf16_to_f32(uint16_t b) { uint32_t u = (uint32_t)b << 16; float f; memcpy(&f, &u, 4); return f; }
 
 /* engine/ops/gemm.js:55-63 (x prologues), :94-97 (wrow), :139-149 (tile dequant), :187-211 (epilogues) */
+/* the heads epilogue of one output row m (engine/ops/gemm.js:212-250): for each 128-wide head h, sec = 0 (query,
+ * h < Hq), 1 (key, h < Hq + Hkv) or 2 (value). Query and key heads: v = acc * inv * nw[c] with inv = 1 / sqrt(mean of
+ * acc^2 over the head + eps) and nw at ev_off (+ 128 for keys), then RoPE from the table row rowOff + m: 'inter' rotates
+ * the pair (2p, 2p + 1) by entry p (:241-244), 'half' the pair (d, d + 64) by entry d (:237-239). Every head is stored
+ * as fp16 at ((h * Ltot) + rowOff + m) * 128 + c (:240, :245). */
+static void heads_row(const p0_gemm_args_t* a, const float* acc, int64_t m, uint8_t* yb) {
+  const int64_t H = a->N / 128, row = a->heads_row_off + m;
+  const double eps = a->heads_eps != 0.0f ? (double)a->heads_eps : 1e-6;
+  const float* rp = a->rope + row * 128;
+  for (int64_t h = 0; h < H; h++) {
+    const float* v = acc + h * 128;
+    const int sec = h < a->heads_hq ? 0 : h < a->heads_hq + a->heads_hkv ? 1 : 2;
+    double out[128];
+    if (sec == 2) {
+      for (int c = 0; c < 128; c++) out[c] = v[c];
+    } else {
+      double ss = 0, t[128];
+      for (int c = 0; c < 128; c++) ss += (double)v[c] * v[c];
+      const float inv = (float)(1.0 / sqrt(ss / 128.0 + eps));
+      const float* nw = a->ev + a->ev_off + (sec ? 128 : 0);
+      for (int c = 0; c < 128; c++) t[c] = (double)v[c] * inv * nw[c];
+      if (a->heads_rope == P0_ROPE_HALF) {
+        for (int d = 0; d < 64; d++) {
+          const double cs = rp[2 * d], sn = rp[2 * d + 1];
+          out[d] = t[d] * cs - t[d + 64] * sn;
+          out[d + 64] = t[d + 64] * cs + t[d] * sn;
+        }
+      } else {
+        for (int q = 0; q < 64; q++) {
+          const double cs = rp[2 * q], sn = rp[2 * q + 1];
+          out[2 * q] = t[2 * q] * cs - t[2 * q + 1] * sn;
+          out[2 * q + 1] = t[2 * q] * sn + t[2 * q + 1] * cs;
+        }
+      }
+    }
+    for (int c = 0; c < 128; c++) {
+      const uint16_t hv = p0o_f2h((float)out[c]);
+      memcpy(yb + 2 * ((h * a->heads_ltot + row) * 128 + c), &hv, 2);
+    }
+  }
+}
+
 int p0o_q4_gemm(const p0_gemm_args_t* a) {
   int64_t M = a->M, N = a->N, K = a->K, ldx = a->x_ld ? a->x_ld : K, ldy = a->y_ld ? a->y_ld : N;
   int64_t wG = a->w_cols / 32, Nw = a->w_rows;
@@ -385,6 +427,10 @@ int p0o_q4_gemm(const p0_gemm_args_t* a) {
       double s = 0;
       for (int64_t k = 0; k < K; k++) s += (double)xr[k] * (double)wr[k];
       acc[n] = (float)s;
+    }
+    if (a->epi == P0_GEPI_HEADS) {   /* engine/ops/gemm.js:212-250 */
+      heads_row(a, acc, m, yb);
+      continue;
     }
     for (int64_t n = 0; n < N; n++) {
       int64_t o = m * ldy + a->y_n0;

@@ -17,7 +17,8 @@ ENC = {"q4g32a.t64": 1, "q8g64s.t64": 2, "f16": 3}
 PRO = {"raw": 0, "rms": 1, "sum": 2, "pleg": 3}
 EPI = {"store": 0, "geglu": 1, "softcap": 2}
 XMODE = {"f16": 0, "lnmod": 1, "rms": 2, "bf16": 3}
-GEPI = {"f16": 0, "f32": 1, "resadd": 2, "swiglu": 3, "bias": 4}
+GEPI = {"f16": 0, "f32": 1, "resadd": 2, "swiglu": 3, "bias": 4, "heads": 5}
+ROPE = {"inter": 0, "half": 1}
 ACT = {"silu": 0, "gelu": 1}
 
 # every symbol the header declares (tests check the library exports each one)
@@ -25,7 +26,7 @@ HEADER_SYMBOLS = [
     "p0_last_error", "p0_version", "p0_open", "p0_close", "p0_device_info", "p0_set_stream", "p0_get_stream",
     "p0_buffer", "p0_free", "p0_upload", "p0_read", "p0_fill", "p0_copy", "p0_done", "p0_timer_start", "p0_timer_stop",
     "p0_q4_gemv", "p0_q4_gemvM", "p0_q4_gemm", "p0_q4_dequant", "p0_fill_q4_sym", "p0_fill_randn", "p0_gemv_tune",
-    "p0_record_begin", "p0_record_end", "p0_replay", "p0_record_free",
+    "p0_record_begin", "p0_record_end", "p0_replay", "p0_record_info", "p0_record_free",
     "p0_chain_begin", "p0_chain_end", "p0_chain_run", "p0_chain_status", "p0_chain_info", "p0_chain_free",
     "p0_chain_tune", "p0_rowstats", "p0_normadd", "p0_argmax", "p0_argmaxM", "p0_upload_file",
 ]
@@ -64,7 +65,9 @@ class GemmArgs(C.Structure):
                 ("M", i64), ("N", i64), ("K", i64), ("wr0", i64), ("wr1", i64), ("wk0", i64), ("epi", i32),
                 ("y", vp), ("y_off", i64), ("y_ld", i64), ("y_n0", i64), ("ev", vp), ("ev_off", i64),
                 ("stats", vp), ("stats_off", i64), ("pv", vp), ("pv_off", i64), ("pv_stride", i64),
-                ("bv", vp), ("bv_off", i64), ("bv_up", i64), ("act", i32), ("store", i32), ("res", i32)]
+                ("bv", vp), ("bv_off", i64), ("bv_up", i64), ("act", i32), ("store", i32), ("res", i32),
+                ("heads_ltot", i64), ("heads_row_off", i64), ("heads_hq", i32), ("heads_hkv", i32),
+                ("heads_eps", f32), ("heads_rope", i32), ("rope", vp)]
 
 
 class RowstatsArgs(C.Structure):
@@ -107,6 +110,7 @@ def lib():
             "p0_q4_dequant": [vp, i64, i64, i64, vp, vp], "p0_fill_q4_sym": [vp, i64, i64, i64, C.c_uint32, f32],
             "p0_fill_randn": [vp, i64, i64, C.c_uint32, f32, i32], "p0_gemv_tune": [C.c_int, C.c_int],
             "p0_record_begin": [], "p0_record_end": [C.POINTER(vp)], "p0_replay": [vp], "p0_record_free": [vp],
+            "p0_record_info": [vp, C.POINTER(i32)],
             "p0_chain_begin": [], "p0_chain_end": [C.POINTER(vp)], "p0_chain_run": [vp],
             "p0_chain_status": [vp, C.POINTER(i32)], "p0_chain_info": [vp, C.POINTER(ChainInfo)], "p0_chain_free": [vp],
             "p0_chain_tune": [C.c_int, C.c_int],
@@ -216,6 +220,11 @@ class Recording:
     def replay(self):
         check(lib().p0_replay(self.handle))
 
+    def launches(self):
+        n = i32()
+        check(lib().p0_record_info(self.handle, C.byref(n)))
+        return n.value
+
     def free(self):
         if self.handle:
             lib().p0_record_free(self.handle)
@@ -308,7 +317,7 @@ def gemm_args(**kw):
     a = GemmArgs()
     a.w_enc = 1
     for k, v in kw.items():
-        setattr(a, k, _ptr(v) if k in ("w", "x", "y", "ev", "stats", "pv", "bv") else v)
+        setattr(a, k, _ptr(v) if k in ("w", "x", "y", "ev", "stats", "pv", "bv", "rope") else v)
     return a
 
 

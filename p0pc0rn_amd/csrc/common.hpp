@@ -5,11 +5,19 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <memory>
 #include <string>
+#include <vector>
 
 #include "../../include/p0pc0rn.h"
 
 namespace p0 {
+
+// Device memory of the library's own that kernels read (the activation staging workspace, a chain's op table and
+// state), held by shared ownership: a recording (p0_record_*) whose captured kernels read such memory holds a
+// reference, so the memory outlives a later growth of the workspace or a p0_chain_free until the recording is freed.
+using Keep = std::shared_ptr<void>;
+void keep_for_recording(const Keep& k);   // the recording being made on the current stream, if any, holds k
 
 // The per-process library context: one device, one current stream, one split-K workspace.
 struct Ctx {
@@ -28,11 +36,18 @@ struct Ctx {
   // misaligned fp16): grown on demand, never inside a stream capture (ensure_xstage)
   void* xstage = nullptr;
   size_t xstage_bytes = 0;
+  Keep xstage_keep;                 // owns xstage (freed once no recording holds it)
+  bool recording = false;           // between p0_record_begin and p0_record_end
+  std::vector<Keep> rec_keeps;      // what the recording being made holds
   int cu_count = 0;
   hipDeviceProp_t prop{};
 };
 Ctx& ctx();
 int ensure_xstage(size_t bytes, const char* op);   // P0_OK, or an error (no room while the stream is being captured)
+// per-file set-up at p0_open (kernel attributes; the no-allocation GEMM's scratch address)
+int gemm_init();
+int gemv_init();
+int misc_init();
 
 // Thread-local message of the last failure (p0_last_error).
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
@@ -45,6 +60,16 @@ inline int require_open(const char* op) {
   if (ctx().device < 0) {
     set_error("%s: no device (p0_open was not called)", op);
     return P0_ENODEV;
+  }
+  return P0_OK;
+}
+// true between p0_chain_begin and p0_chain_end (gemv.hip): only gemv / gemvM calls join a chain, every other op
+// refuses to run meanwhile instead of running out of order
+bool building_chain();
+inline int refuse_in_chain(const char* op) {
+  if (building_chain()) {
+    set_error("%s: only gemv / gemvM calls join a chain (a chain is being built)", op);
+    return P0_EINVAL;
   }
   return P0_OK;
 }

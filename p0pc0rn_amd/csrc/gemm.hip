@@ -2,7 +2,7 @@
 //
 // Replaces the WebGPU dispatch of gemm (engine/ops/gemm.js:255-322) for the q4 encoding, with its prologues
 // f16 | lnmod | rms (engine/ops/gemm.js:55-63; plus bf16 activations converted to fp16) and epilogues
-// f16 | f32 | resadd | swiglu | bias (engine/ops/gemm.js:187-211).
+// f16 | f32 | resadd | swiglu | bias | heads (engine/ops/gemm.js:187-250).
 //
 // Two kernels:
 //  * x_stage_kernel<XM> writes X' (the prologue-applied activations, fp16, dense rows of K) into the context's staging
@@ -37,6 +37,11 @@ struct GemmP {
   const float* ev; int64_t evOff;
   const float* bv; int64_t bvOff, bvUp;
   int act, store, res;
+  // heads epilogue: head-major rows of Ltot, query / key head counts, eps, RoPE mode and table
+  int64_t hLtot, hRow0;
+  int hq, hkv, hrope;
+  float heps;
+  const float* rope;
 };
 
 struct XStageP {   // the prologue of engine/ops/gemm.js:55-63 over the caller's X
@@ -171,7 +176,108 @@ __device__ __forceinline__ u32x4n deq_word(uint32_t v, uint32_t sm, bool fast) {
 // 8 waves in 2 (M) x 4 (N), two per SIMD so that one wave's waits are covered by the other's MFMAs; each wave owns a
 // 128 x 64 sub-tile as 4 x 2 blocks of 32 x 32 (128 fp32 accumulators per lane)
 constexpr int kWaves = 8, kThreads = 64 * kWaves, WTM = 128, WTN = 64, IB = WTM / 32, JB = WTN / 32;
+// ---- the heads epilogue (engine/ops/gemm.js:212-250): QK-RMSNorm over each 128-wide head, RoPE, head-major fp16 rows.
+// A 256-wide output tile holds two whole heads (n0 is a multiple of 256): head hp of the tile is the wave pair
+// wn = 2 hp (head columns 0..63) and 2 hp + 1 (64..127), in each of the two wave rows wm. acc[i][j][e] is row
+// 32 i + 8 (e / 4) + e % 4 + 4 (lane / 32) of the wave's 128 and column 32 j + lane % 32 of its 64.
+//  * sum of squares per row: a lane adds its two columns; per 32-row block i, a transposing butterfly over the 32 lanes
+//    of each half-wave (offsets 16, 8, 4, 2: a lane keeps one half of its 16 sums and takes the partner's matching half,
+//    then offset 1 adds the last pair) leaves a lane the sum of one row over the wave's 64 columns; the two waves' sums
+//    of a head are added through LDS, even wave first, so both waves see the same sum;
+//  * query / key heads: v = acc * inv * nw[c], inv = 1 / sqrt(sum / 128 + eps), then the rotation: 'inter' pairs the
+//    columns (2p, 2p + 1), which sit in neighbouring lanes; 'half' pairs (d, d + 64), which sit in the two waves of the
+//    pair, so the values cross through LDS, one block i (32 rows) per round;
+//  * every head is stored fp16 at ((head Ltot) + row0 + m) 128 + c.
+__device__ __forceinline__ void heads_epilogue(const GemmP& p, float16v (&acc)[WTM / 32][WTN / 32], uint8_t* lds,
+                                               int m0, int n0, int wm, int wn, int lane) {
+  constexpr int IBh = WTM / 32, JBh = WTN / 32;
+  float* red = (float*)lds;                       // [wn][wm * 128 + row]: 4 x 256 floats
+  float* xch = (float*)(lds + 4096);              // [wave][j][e][lane]: the 'half' exchange, 8 x 2 x 16 x 64 floats
+  const int wv = wm * 4 + wn, hh = lane >> 5;
+  __syncthreads();   // every wave has read its last fragments: the stage memory is free
+#pragma unroll
+  for (int i = 0; i < IBh; ++i) {
+    float ss[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) ss[e] = __builtin_fmaf(acc[i][0][e], acc[i][0][e], acc[i][1][e] * acc[i][1][e]);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int o = 16 >> st, half = 8 >> st;
+      const bool up = (lane & o) != 0;
+#pragma unroll
+      for (int k = 0; k < half; ++k) {
+        const float send = up ? ss[k] : ss[k + half], keep = up ? ss[k + half] : ss[k];
+        ss[k] = keep + __shfl_xor(send, o, 64);
+      }
+    }
+    const float tot = ss[0] + __shfl_xor(ss[0], 1, 64);
+    const int e = ((lane & 16) ? 8 : 0) + ((lane & 8) ? 4 : 0) + ((lane & 4) ? 2 : 0) + ((lane & 2) ? 1 : 0);
+    if (!(lane & 1)) red[wn * 256 + wm * 128 + 32 * i + 8 * (e >> 2) + (e & 3) + 4 * hh] = tot;
+  }
+  __syncthreads();
+  const int hd = (n0 >> 7) + (wn >> 1);
+  const int sec = hd < p.hq ? 0 : hd < p.hq + p.hkv ? 1 : 2;
+  const int c0 = (wn & 1) * 64 + (lane & 31);   // head column of j = 0 (j = 1: + 32)
+  float nw[JBh];
+#pragma unroll
+  for (int j = 0; j < JBh; ++j) nw[j] = sec < 2 ? p.ev[p.evOff + (sec ? 128 : 0) + c0 + 32 * j] : 1.0f;
+  const float* rede = red + (wn & ~1) * 256 + wm * 128;
+  const float* redo = red + (wn | 1) * 256 + wm * 128;
+  _Float16* y = (_Float16*)p.y;
+#pragma unroll
+  for (int i = 0; i < IBh; ++i) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {   // normalised values, in place
+      const int r = 32 * i + 8 * (e >> 2) + (e & 3) + 4 * hh;
+      const float inv = sec < 2 ? 1.0f / sqrtf((rede[r] + redo[r]) / 128.0f + p.heps) : 1.0f;
+#pragma unroll
+      for (int j = 0; j < JBh; ++j) acc[i][j][e] = sec < 2 ? acc[i][j][e] * inv * nw[j] : acc[i][j][e];
+    }
+    float pv[JBh][16];   // the rotation partner of each value
+    if (p.hrope == P0_ROPE_HALF) {
+#pragma unroll
+      for (int j = 0; j < JBh; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) xch[((wv * JBh + j) * 16 + e) * 64 + lane] = acc[i][j][e];
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < JBh; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) pv[j][e] = xch[(((wv ^ 1) * JBh + j) * 16 + e) * 64 + lane];
+      __syncthreads();   // the next round rewrites the exchange area
+    } else {
+#pragma unroll
+      for (int j = 0; j < JBh; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) pv[j][e] = __shfl_xor(acc[i][j][e], 1, 64);
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = m0 + wm * WTM + 32 * i + 8 * (e >> 2) + (e & 3) + 4 * hh;
+      const int64_t row = p.hRow0 + (m < p.M ? m : p.M - 1);
+#pragma unroll
+      for (int j = 0; j < JBh; ++j) {
+        const int c = c0 + 32 * j;
+        const float v = acc[i][j][e];
+        float out = v;
+        if (sec < 2) {
+          if (p.hrope == P0_ROPE_HALF) {   // pair (d, d + 64), entry d: the low half subtracts, the high half adds
+            const float* rp = p.rope + row * 128 + 2 * (c & 63);
+            out = (wn & 1) ? v * rp[0] + pv[j][e] * rp[1] : v * rp[0] - pv[j][e] * rp[1];
+          } else {                         // pair (2q, 2q + 1), entry q
+            const float* rp = p.rope + row * 128 + (c & ~1);
+            out = (c & 1) ? pv[j][e] * rp[1] + v * rp[0] : v * rp[0] - pv[j][e] * rp[1];
+          }
+        }
+        if (m < p.M) y[(hd * p.hLtot + p.hRow0 + m) * 128 + c] = to_h(out);
+      }
+    }
+  }
+}
 
+
+// HEADS: the instantiation with the heads epilogue (the others' register allocation stays as it is without it)
+template <bool HEADS>
 __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmP p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -340,7 +446,9 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmP p) {
     const int64_t o = (int64_t)m * p.ldy + p.ny0;                           \
     __VA_ARGS__                                                             \
   }
-  if (p.epi == P0_GEPI_F16) {
+  if (HEADS) {
+    heads_epilogue(p, acc, lds, m0, n0, wm, wn, lane);
+  } else if (p.epi == P0_GEPI_F16) {
     P0_EPI_LOOP(if (m < p.M && n < p.N) ((_Float16*)p.y)[o + n] = to_h(a);)
   } else if (p.epi == P0_GEPI_F32) {
     P0_EPI_LOOP(if (m < p.M && n < p.N) ((float*)p.y)[o + n] = a;)
@@ -377,10 +485,23 @@ static const char* gepi_name(int e) {
     case P0_GEPI_RESADD: return "resadd";
     case P0_GEPI_SWIGLU: return "swiglu";
     case P0_GEPI_BIAS: return "bias";
+    case P0_GEPI_HEADS: return "heads";
   }
   return "?";
 }
 
+}  // namespace p0
+
+namespace p0 {
+// more than 64 KB of dynamic LDS must be allowed once per kernel; done at p0_open, so no call sets it lazily (for
+// instance while its stream is being captured)
+int gemm_init() {
+  P0_HIP(hipFuncSetAttribute((const void*)q4_gemm_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds),
+         "p0_open: gemm");
+  P0_HIP(hipFuncSetAttribute((const void*)q4_gemm_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds),
+         "p0_open: gemm");
+  return P0_OK;
+}
 }  // namespace p0
 
 using namespace p0;
@@ -400,8 +521,32 @@ extern "C" int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out) {
   if (a->wk0 % 32) { set_error("gemm: wk0 must be a multiple of 32"); return P0_EINVAL; }
   if (a->w_cols % 32 || a->w_rows % 64 || a->w_cols < a->wk0 + K) { set_error("gemm: weight shape"); return P0_EINVAL; }
   if (a->w_off % 4) { set_error("gemm: weight offset"); return P0_EINVAL; }
+  // the weight rows the call reads (engine/ops/gemm.js:94-97): wr0 .. wr0 + N - 1, or for a swiglu the gate rows
+  // wr0 .. wr0 + N/2 - 1 and the up rows wr1 .. wr1 + N/2 - 1
+  if (a->wr0 < 0 || a->wr1 < 0) { set_error("gemm: negative weight row"); return P0_EINVAL; }
+  {
+    const bool sw = a->epi == P0_GEPI_SWIGLU;
+    const int64_t span = sw ? N / 2 : N, top = sw && a->wr1 > a->wr0 ? a->wr1 : a->wr0;
+    if (top + span > a->w_rows) {
+      set_error("gemm: weight rows %lld + %lld past the %lld rows of the weight", (long long)top, (long long)span,
+                (long long)a->w_rows);
+      return P0_EINVAL;
+    }
+  }
   if (a->x_mode < P0_XMODE_F16 || a->x_mode > P0_XMODE_BF16) { set_error("gemm: x mode %d", a->x_mode); return P0_EINVAL; }
-  if (a->epi < P0_GEPI_F16 || a->epi > P0_GEPI_BIAS) { set_error("gemm: epilogue %d", a->epi); return P0_EINVAL; }
+  if (a->epi < P0_GEPI_F16 || a->epi > P0_GEPI_HEADS) { set_error("gemm: epilogue %d", a->epi); return P0_EINVAL; }
+  if (a->epi == P0_GEPI_HEADS) {   // one head per 128 output columns (engine/ops/gemm.js:213)
+    if (N % 128) { set_error("gemm: heads needs N a multiple of 128"); return P0_EINVAL; }
+    if (!a->ev || !a->rope) { set_error("gemm: heads needs ev (the norm weights) and heads.rope"); return P0_EINVAL; }
+    if (a->heads_rope != P0_ROPE_INTER && a->heads_rope != P0_ROPE_HALF) {
+      set_error("gemm: heads rope mode %d", a->heads_rope); return P0_EINVAL;
+    }
+    if (a->heads_hq < 0 || a->heads_hkv < 0 || a->heads_row_off < 0 || a->heads_row_off + M > a->heads_ltot) {
+      set_error("gemm: heads rows %lld + %lld past Ltot %lld", (long long)a->heads_row_off, (long long)M,
+                (long long)a->heads_ltot);
+      return P0_EINVAL;
+    }
+  }
   if (a->epi == P0_GEPI_SWIGLU && (N & 1)) { set_error("gemm: swiglu needs an even N"); return P0_EINVAL; }
   if (!a->w || !a->x || !a->y) { set_error("gemm: missing w, x or y buffer"); return P0_EINVAL; }
   if ((a->x_mode == P0_XMODE_LNMOD || a->x_mode == P0_XMODE_RMS) && (!a->stats || !a->pv)) {
@@ -409,6 +554,7 @@ extern "C" int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out) {
   }
   if (a->epi == P0_GEPI_BIAS && !a->ev) { set_error("gemm: bias needs ev"); return P0_EINVAL; }
   if (int r = require_open("gemm")) return r;
+  if (int r = refuse_in_chain("gemm")) return r;
 
   GemmP p{};
   p.w = (const uint8_t*)a->w + a->w_off;
@@ -423,6 +569,8 @@ extern "C" int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out) {
   p.ev = a->ev; p.evOff = a->ev_off;
   p.bv = a->bv; p.bvOff = a->bv_off; p.bvUp = a->bv_up;
   p.act = a->act; p.store = a->store; p.res = a->res;
+  p.hLtot = a->heads_ltot; p.hRow0 = a->heads_row_off; p.hq = a->heads_hq; p.hkv = a->heads_hkv;
+  p.hrope = a->heads_rope; p.heps = a->heads_eps != 0.0f ? a->heads_eps : 1e-6f; p.rope = a->rope;
   (void)gepi_name;
 
   // X': the caller's fp16 rows when they can be streamed as they are (16-byte aligned rows), else one staging pass
@@ -434,6 +582,7 @@ extern "C" int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out) {
     p.ldx = ldx;
   } else {
     if (int r = ensure_xstage((size_t)M * K * 2, "gemm")) return r;
+    keep_for_recording(ctx().xstage_keep);
     XStageP q{};
     q.x = xbase; q.ldx = ldx; q.kx0 = a->x_k0; q.xmode = a->x_mode;
     q.M = (int)M; q.K = (int)K;
@@ -449,13 +598,11 @@ extern "C" int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out) {
     p.x = (const _Float16*)ctx().xstage;
     p.ldx = K;
   }
-  static bool lds_set = false;
-  if (!lds_set) {   // more than 64 KB of dynamic LDS must be allowed once
-    P0_HIP(hipFuncSetAttribute((const void*)q4_gemm_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds), "gemm");
-    lds_set = true;
-  }
   const int64_t tiles = ((N + BN - 1) / BN) * ((M + BM - 1) / BM);
-  hipLaunchKernelGGL(q4_gemm_kernel, dim3((unsigned)tiles), dim3(kThreads), kGemmLds, ctx().cur, p);
+  if (a->epi == P0_GEPI_HEADS)
+    hipLaunchKernelGGL(q4_gemm_kernel<true>, dim3((unsigned)tiles), dim3(kThreads), kGemmLds, ctx().cur, p);
+  else
+    hipLaunchKernelGGL(q4_gemm_kernel<false>, dim3((unsigned)tiles), dim3(kThreads), kGemmLds, ctx().cur, p);
   P0_LAUNCHED("gemm");
   if (flops_out) *flops_out = 2.0 * (double)M * (double)N * (double)K;
   return P0_OK;

@@ -138,8 +138,10 @@ struct ChainExec {
   size_t lds;
   chain_kernel_t kernel;
   int mailboxes;     // ops that take their input from a mailbox
+  Keep dev;          // owns ops and st (a recording that captured a run of the chain holds it too)
 };
 static ChainBuild* g_chain = nullptr;
+bool building_chain() { return g_chain != nullptr; }
 static std::map<unsigned*, size_t> g_state_bytes;   // sizes of the uncached state blocks
 
 // Chain state (completion flags and the run tag) lives in uncached device memory: a flag store and the polls of
@@ -334,15 +336,18 @@ static bool plan_pipe(std::vector<GemvP>& ops, int G, int M) {
   return true;
 }
 
+// the q8 kernels' LDS allowance, set once at p0_open (never lazily, e.g. while the stream is being captured)
+int gemv_init() {
+  for (int M : {1, 2})
+    P0_HIP(hipFuncSetAttribute((const void*)q8_kernel(M), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)q8_lds_bytes(16)), "p0_open: gemv");
+  return P0_OK;
+}
+
 // q8g64s.t64: one workgroup per (64-row tile, split), gemv_q8.hip
 static int launch_q8(GemvP& p, int M, const char* op) {
   q8_kernel_t k = q8_kernel(M);
   const size_t lds = q8_lds_bytes(M);
-  static bool attr[2] = {false, false};
-  if (!attr[M == 1]) {
-    P0_HIP(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)q8_lds_bytes(16)), op);
-    attr[M == 1] = true;
-  }
   hipLaunchKernelGGL(k, dim3((unsigned)p.NT, (unsigned)p.nsplit), dim3(256), lds, ctx().cur, p);
   P0_LAUNCHED(op);
   return P0_OK;
@@ -433,6 +438,11 @@ extern "C" int p0_q4_gemv(const p0_gemv_args_t* a, int32_t* nsplit_out) {
   if (K <= 0 || K % G) { set_error("gemv: K must be a multiple of %lld", (long long)G); return P0_EINVAL; }
   if (N <= 0) { set_error("gemv: N must be positive"); return P0_EINVAL; }
   if (a->w_cols < K) { set_error("gemv: weight has %lld columns < K %lld", (long long)a->w_cols, (long long)K); return P0_EINVAL; }
+  if (a->w_rows < (a->epi == P0_EPI_GEGLU ? 2 * N : N)) {   // a geglu reads the up rows at N .. 2N - 1
+    set_error("gemv: weight has %lld rows < %s %lld", (long long)a->w_rows, a->epi == P0_EPI_GEGLU ? "2N" : "N",
+              (long long)(a->epi == P0_EPI_GEGLU ? 2 * N : N));
+    return P0_EINVAL;
+  }
   if (a->pro < P0_PRO_RAW || a->pro > P0_PRO_PLEG) { set_error("gemv: prologue %d", a->pro); return P0_EINVAL; }
   if (a->epi < P0_EPI_STORE || a->epi > P0_EPI_SOFTCAP) { set_error("gemv: epilogue %d", a->epi); return P0_EINVAL; }
   if (!a->w || !a->x || !a->y) { set_error("gemv: missing w, x or y buffer"); return P0_EINVAL; }
@@ -482,6 +492,11 @@ extern "C" int p0_q4_gemvM(const p0_gemvm_args_t* a, int32_t* nsplit_out) {
   if (K <= 0 || K % G) { set_error("gemvM: K must be a multiple of %lld", (long long)G); return P0_EINVAL; }
   if (N <= 0) { set_error("gemvM: N must be positive"); return P0_EINVAL; }
   if (a->w_cols < K) { set_error("gemvM: weight has %lld columns < K %lld", (long long)a->w_cols, (long long)K); return P0_EINVAL; }
+  if (a->w_rows < (a->epi == P0_EPI_GEGLU ? 2 * N : N)) {
+    set_error("gemvM: weight has %lld rows < %s %lld", (long long)a->w_rows, a->epi == P0_EPI_GEGLU ? "2N" : "N",
+              (long long)(a->epi == P0_EPI_GEGLU ? 2 * N : N));
+    return P0_EINVAL;
+  }
   if (a->epi < P0_EPI_STORE || a->epi > P0_EPI_SOFTCAP) { set_error("gemvM: epilogue %d", a->epi); return P0_EINVAL; }
   if (!a->w || !a->x || !a->y) { set_error("gemvM: missing w, x or y buffer"); return P0_EINVAL; }
   if (a->pro == P0_PRO_RMS && (!a->norm || !a->stat)) { set_error("gemvM: rms needs norm and stat buffers"); return P0_EINVAL; }
@@ -633,6 +648,14 @@ extern "C" int p0_chain_end(void** out) {
     delete ex;
     return fail_hip(e, "p0_chain_end");
   }
+  {
+    GemvP* ops_mem = ex->ops;
+    unsigned* st_mem = ex->st;
+    ex->dev = Keep(ops_mem, [st_mem](void* q) {
+      hipFree(q);
+      state_free(st_mem);
+    });
+  }
   *out = ex;
   return P0_OK;
 }
@@ -645,6 +668,7 @@ extern "C" int p0_chain_run(void* chain) {
   hipLaunchKernelGGL(ex->kernel, dim3((unsigned)ex->grid), dim3(64 * ex->W), ex->lds, ctx().cur, ex->ops, ex->n_ops,
                      ex->st, g_chain_force_give_up ? -1 : g_chain_spin);
   P0_LAUNCHED("p0_chain_run");
+  keep_for_recording(ex->dev);
   return P0_OK;
 }
 
@@ -685,9 +709,7 @@ extern "C" int p0_chain_free(void* chain) {
   if (!chain) return P0_OK;
   auto* ex = (ChainExec*)chain;
   if (ctx().device >= 0) hipStreamSynchronize(ctx().cur);
-  hipFree(ex->ops);
-  state_free(ex->st);
-  delete ex;
+  delete ex;   // the op table and state go once no recording that ran the chain holds them
   return P0_OK;
 }
 

@@ -247,6 +247,10 @@ napi_value Gemm(napi_env env, napi_callback_info info) {
   g.pv = ptr<const float>(env, o, "pv"); g.pv_off = i64(env, o, "pv_off"); g.pv_stride = i64(env, o, "pv_stride");
   g.bv = ptr<const float>(env, o, "bv"); g.bv_off = i64(env, o, "bv_off"); g.bv_up = i64(env, o, "bv_up");
   g.act = i32(env, o, "act"); g.store = i32(env, o, "store"); g.res = i32(env, o, "res");
+  g.heads_ltot = i64(env, o, "heads_ltot"); g.heads_row_off = i64(env, o, "heads_row_off");
+  g.heads_hq = i32(env, o, "heads_hq"); g.heads_hkv = i32(env, o, "heads_hkv");
+  g.heads_eps = (float)field(env, o, "heads_eps"); g.heads_rope = i32(env, o, "heads_rope");
+  g.rope = ptr<const float>(env, o, "rope");
   double flops = 0;
   if (fail(env, p0_q4_gemm(&g, &flops))) return nullptr;
   return make_num(env, flops);
@@ -338,6 +342,18 @@ napi_value Replay(napi_env env, napi_callback_info info) {
   if (fail(env, p0_replay(handle(env, a[0])))) return nullptr;
   return undef(env);
 }
+napi_value RecordInfo(napi_env env, napi_callback_info info) {
+  auto a = args(env, info, 1);
+  int32_t n = 0;
+  if (fail(env, p0_record_info(handle(env, a[0]), &n))) return nullptr;
+  return make_num(env, n);
+}
+napi_value ChainInfo(napi_env env, napi_callback_info info) {
+  auto a = args(env, info, 1);
+  p0_chain_info_t ci{};
+  if (fail(env, p0_chain_info(handle(env, a[0]), &ci))) return nullptr;
+  return make_num(env, ci.n_ops);
+}
 napi_value RecordFree(napi_env env, napi_callback_info info) {
   auto a = args(env, info, 1);
   if (fail(env, p0_record_free(handle(env, a[0])))) return nullptr;
@@ -379,7 +395,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"read", Read}, {"fill", Fill}, {"copy", Copy}, {"done", Done}, {"timerStart", TimerStart}, {"timerStop", TimerStop},
       {"gemv", Gemv}, {"gemvM", GemvM}, {"gemm", Gemm}, {"dequant", Dequant}, {"fillQ4Sym", FillQ4Sym},
       {"fillRandn", FillRandn}, {"version", Version}, {"recordBegin", RecordBegin}, {"recordEnd", RecordEnd},
-      {"replay", Replay}, {"recordFree", RecordFree}, {"chainBegin", ChainBegin}, {"chainEnd", ChainEnd},
+      {"replay", Replay}, {"recordInfo", RecordInfo}, {"recordFree", RecordFree}, {"chainInfo", ChainInfo}, {"chainBegin", ChainBegin}, {"chainEnd", ChainEnd},
       {"chainRun", ChainRun}, {"chainStatus", ChainStatus}, {"chainFree", ChainFree},
       {"rowstats", Rowstats}, {"normadd", Normadd}, {"argmaxM", ArgmaxM}, {"uploadFile", UploadFile},
   };

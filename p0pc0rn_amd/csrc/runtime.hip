@@ -7,9 +7,21 @@
 namespace p0 {
 
 Ctx& ctx() {
-  static Ctx c;
-  return c;
+  static Ctx* c = new Ctx();   // never destroyed: nothing of it is released after the HIP runtime at process exit
+  return *c;
 }
+
+void keep_for_recording(const Keep& k) {
+  Ctx& c = ctx();
+  if (c.recording && k) c.rec_keeps.push_back(k);
+}
+
+// a recording: the instantiated graph and the library memory its kernels read
+struct Rec {
+  hipGraphExec_t exec = nullptr;
+  std::vector<Keep> keeps;
+  int32_t nodes = 0;
+};
 
 static thread_local std::string g_err;
 
@@ -23,14 +35,19 @@ int ensure_xstage(size_t bytes, const char* op) {
   }
   size_t want = bytes < (256ull << 20) ? (256ull << 20) : (bytes + (1ull << 20) - 1) / (1ull << 20) * (1ull << 20);
   P0_HIP(hipStreamSynchronize(c.cur), op);   // the old buffer may still be read by enqueued work
-  if (c.xstage) hipFree(c.xstage);
+  // the old buffer is released here unless a recording captured a kernel that reads it: then it lives on until the
+  // last such recording is freed (p0_record_free)
+  c.xstage_keep.reset();
   c.xstage = nullptr;
   c.xstage_bytes = 0;
-  hipError_t e = hipMalloc(&c.xstage, want);
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, want);
   if (e != hipSuccess) {
     set_error("%s: activation staging workspace of %zu B: %s", op, want, hipGetErrorString(e));
     return P0_ENOMEM;
   }
+  c.xstage_keep = Keep(p, [](void* q) { hipFree(q); });
+  c.xstage = p;
   c.xstage_bytes = want;
   return P0_OK;
 }
@@ -100,6 +117,9 @@ int p0_open(int device) {
   P0_HIP(hipMalloc((void**)&c.counters, kCounters * sizeof(unsigned)), "p0_open: workspace");
   P0_HIP(hipMemset(c.counters, 0, kCounters * sizeof(unsigned)), "p0_open: workspace");
   P0_HIP(hipDeviceSynchronize(), "p0_open");
+  if (int r = gemm_init()) return r;
+  if (int r = gemv_init()) return r;
+  if (int r = misc_init()) return r;
   c.part_floats = kPartBytes / sizeof(float);
   c.n_counters = kCounters;
   c.cur = c.own;
@@ -114,7 +134,7 @@ int p0_close(void) {
   hipStreamSynchronize(c.own);
   hipFree(c.part);
   hipFree(c.counters);
-  if (c.xstage) hipFree(c.xstage);
+  c.xstage_keep.reset();   // freed unless a recording still holds it
   hipEventDestroy(c.ev0);
   hipEventDestroy(c.ev1);
   hipStreamDestroy(c.own);
@@ -197,6 +217,7 @@ int p0_fill(void* dst, size_t dst_off, uint32_t value, size_t words) {
 
 int p0_copy(const void* src, size_t src_off, void* dst, size_t dst_off, size_t bytes) {
   if (int r = require_open("p0_copy")) return r;
+  if (int r = refuse_in_chain("p0_copy")) return r;
   const char* a = (const char*)src + src_off;
   char* b = (char*)dst + dst_off;
   if (((uintptr_t)a | (uintptr_t)b | bytes) & 3) {   // copyBufferToBuffer's rule: offsets and size multiples of 4
@@ -227,32 +248,56 @@ int p0_done(void) {   // Gpu.done: wait for everything enqueued; faults of earli
 // ---- recorded op sequences (engine/llm/drunner.js:1-8, 83-101: one decode token recorded once, submitted per token)
 int p0_record_begin(void) {
   if (int r = require_open("p0_record_begin")) return r;
-  P0_HIP(hipStreamBeginCapture(ctx().cur, hipStreamCaptureModeThreadLocal), "p0_record_begin");
+  Ctx& c = ctx();
+  if (c.recording) { set_error("p0_record_begin: a recording is already being made"); return P0_EINVAL; }
+  P0_HIP(hipStreamBeginCapture(c.cur, hipStreamCaptureModeThreadLocal), "p0_record_begin");
+  c.recording = true;
+  c.rec_keeps.clear();
   return P0_OK;
 }
 
 int p0_record_end(void** out) {
   if (int r = require_open("p0_record_end")) return r;
+  Ctx& c = ctx();
+  std::vector<Keep> keeps;
+  keeps.swap(c.rec_keeps);
+  c.recording = false;
   hipGraph_t graph = nullptr;
-  P0_HIP(hipStreamEndCapture(ctx().cur, &graph), "p0_record_end");
+  P0_HIP(hipStreamEndCapture(c.cur, &graph), "p0_record_end");
+  size_t nodes = 0;
+  hipGraphGetNodes(graph, nullptr, &nodes);
   hipGraphExec_t exec = nullptr;
   hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
   hipGraphDestroy(graph);
   if (e != hipSuccess) return fail_hip(e, "p0_record_end: instantiate");
-  *out = (void*)exec;
+  Rec* rec = new Rec();
+  rec->exec = exec;
+  rec->keeps = std::move(keeps);
+  rec->nodes = (int32_t)nodes;
+  *out = (void*)rec;
   return P0_OK;
 }
 
 int p0_replay(void* rec) {
   if (int r = require_open("p0_replay")) return r;
   if (!rec) { set_error("p0_replay: no recording"); return P0_EINVAL; }
-  P0_HIP(hipGraphLaunch((hipGraphExec_t)rec, ctx().cur), "p0_replay");
+  P0_HIP(hipGraphLaunch(((Rec*)rec)->exec, ctx().cur), "p0_replay");
+  return P0_OK;
+}
+
+int p0_record_info(void* rec, int32_t* nodes) {
+  if (!rec || !nodes) { set_error("p0_record_info: no recording or output"); return P0_EINVAL; }
+  *nodes = ((Rec*)rec)->nodes;
   return P0_OK;
 }
 
 int p0_record_free(void* rec) {
   if (!rec) return P0_OK;
-  P0_HIP(hipGraphExecDestroy((hipGraphExec_t)rec), "p0_record_free");
+  Rec* r = (Rec*)rec;
+  if (ctx().device >= 0) hipStreamSynchronize(ctx().cur);   // replays still enqueued read what the recording holds
+  hipError_t e = hipGraphExecDestroy(r->exec);
+  delete r;   // releases the memory only this recording still held
+  if (e != hipSuccess) return fail_hip(e, "p0_record_free");
   return P0_OK;
 }
 

@@ -12,6 +12,39 @@ export const EPI = { store: 0, geglu: 1, softcap: 2 };
 /** the device address of a buffer handle (0 = absent) */
 export const addr = (b) => (b ? b.ptr : 0);
 
+/** a view's extent against its buffer: a handle that knows its size (`_pf`, every Gpu.buffer) must hold `end` bytes.
+ *  WebGPU bound-checks every binding; a HIP kernel reading or writing past an allocation can fault the device, so the
+ *  ops check on the host before the call. */
+export function within(op, name, buf, end) {
+  if (buf && buf._pf != null && end > buf._pf) throw new Error(`${op}: ${name} needs ${end} B of a ${buf._pf} B buffer`);
+}
+/** bytes of a weight tensor of `rows` x `cols` in its record encoding */
+export function weightBytes(enc, rows, cols) {
+  return enc === 'q8g64s.t64' ? (rows / 64) * (cols / 64) * 4224 : (rows / 64) * (cols / 32) * 1280;
+}
+/** the number of K splits gemv writes (engine/llm/lops.js:116-121) */
+function splitsOf(K, kPer) {
+  const kch = !kPer && K > 2048 ? Math.ceil(K / 256) * 256 : KCH;
+  const kp = kPer ? Math.min(kPer, kch) : Math.min(K, kch);
+  return kp > 0 ? Math.ceil(K / kp) : 1;
+}
+/** host-side bounds of gemv / gemvM's views (M rows of x) */
+export function checkViews(op, a, M, nsplit) {
+  const K = a.K, N = a.N, geglu = a.epi === 'geglu', pro = a.pro || 'raw';
+  within(op, 'w', a.w.buf, (a.w.off || 0) + weightBytes(a.w.enc, a.w.rows, a.w.cols));
+  const ldx = a.x.ldx || K;
+  if (pro === 'sum' || pro === 'pleg') {
+    const n = (a.src && a.src.n) || 1, ld = (a.src && a.src.ld) || 0;
+    within(op, 'x', a.x.buf, ((n - 1) * ld + (M - 1) * ldx + K) * 4);
+  } else within(op, 'x', a.x.buf, ((a.x.rowB || 0) + (M - 1) * ldx + K) * 4);
+  const ldm = (a.y.ldm || N), ldy = a.ldy || a.y.ldy || (M > 1 ? M * ldm : N);
+  within(op, 'y', a.y.buf, ((geglu || a.epi === 'softcap' ? 0 : (nsplit - 1) * ldy) + (M - 1) * ldm + N) * 4);
+  if (pro === 'rms') within(op, 'norm', a.norm && a.norm.buf, ((a.norm && a.norm.off || 0) + K) * 4);
+  if (pro === 'pleg' && a.ev) within(op, 'ev', a.ev.buf, ((a.ev.off || 0) + (M - 1) * (a.ev.ld || 0) + K) * 4);
+  if (a.epi === 'softcap' && a.mx) within(op, 'mx', a.mx.buf, M * (N / 64) * 8);
+  if (geglu) within(op, 'w', a.w.buf, (a.w.off || 0) + weightBytes(a.w.enc, 2 * N, a.w.cols));
+}
+
 function encOf(op, enc) {
   const e = ENC[enc];
   if (!e || e === ENC.f16) throw new Error(op + ': encoding ' + enc);
@@ -30,6 +63,7 @@ function optOf(op, what, table, v) {
  *  a.kx (the reference's pick switch) is accepted and has no effect: this build has one kernel family per regime. */
 export function gemv(g, a) {
   const w = encOf('gemv', a.w.enc);
+  checkViews('gemv', a, 1, splitsOf(a.K, a.kPer));
   return native().gemv({
     w: addr(a.w.buf), w_off: a.w.off || 0, w_enc: w, w_rows: a.w.rows, w_cols: a.w.cols,
     x: addr(a.x.buf), x_rowB: a.x.rowB || 0,

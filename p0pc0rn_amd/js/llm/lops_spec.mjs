@@ -2,7 +2,7 @@
 // on the MI355X library. Same argument object, return value and errors as the reference.
 'use strict';
 import { native } from '../native.mjs';
-import { ENC, PRO, EPI, addr } from './lops.mjs';
+import { ENC, PRO, EPI, addr, checkViews } from './lops.mjs';
 
 /** a = { w: {buf, off, enc, rows, cols}, x: {buf, ldx, rowB}, M, N, K, kPer, pro: raw|rms|pleg, epi: store|geglu|softcap,
  *        y: {buf, ldy (floats between splits), ldm (floats between rows)}, stat: {buf, off, ld} (rms: rstd of row m at
@@ -15,6 +15,8 @@ export function gemvM(g, a) {
   const pro = a.pro || 'raw', epi = a.epi || 'store';
   if (!(pro in PRO) || pro === 'sum') throw new Error('gemvM: prologue ' + pro);
   if (!(epi in EPI)) throw new Error('gemvM: epilogue ' + epi);
+  const kp = a.kPer ? Math.min(a.kPer, 2048) : a.K;   // engine/llm/lops_spec.js:170
+  checkViews('gemvM', a, a.M, kp > 0 ? Math.ceil(a.K / kp) : 1);
   return native().gemvM({
     w: addr(a.w.buf), w_off: a.w.off || 0, w_enc: enc, w_rows: a.w.rows, w_cols: a.w.cols,
     x: addr(a.x.buf), x_ldx: a.x.ldx || 0, x_rowB: a.x.rowB || 0,

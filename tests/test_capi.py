@@ -63,6 +63,8 @@ def gemv_err(**kw):
     (dict(w_enc=2, K=96, w_cols=96), "gemv: kPer must be a multiple of 64"),
     (dict(w_enc=7), "gemv: encoding 7"),
     (dict(K=48, w_cols=48), "gemv: kPer must be a multiple of 32"),
+    (dict(N=128), "gemv: weight has 64 rows < N 128"),
+    (dict(epi=1), "gemv: weight has 64 rows < 2N 128"),
 ])
 def test_gemv_argument_errors(kw, msg):
     rc, err = gemv_err(**kw)
@@ -92,6 +94,8 @@ def gemvm_err(**kw):
     (dict(K=4096, w_cols=4096, kPer=1024, epi=1), "gemvM: geglu needs one split"),
     (dict(w_off=6), "gemvM: weight offset"),
     (dict(M=17), "gemvM: M 17 (this build: 1..16)"),
+    (dict(N=128), "gemvM: weight has 64 rows < N 128"),
+    (dict(epi=1), "gemvM: weight has 64 rows < 2N 128"),
 ])
 def test_gemvM_argument_errors(kw, msg):
     rc, err = gemvm_err(**kw)
@@ -120,6 +124,18 @@ def gemm_err(**kw):
     (dict(epi=3, N=63), "gemm: swiglu needs an even N"),
     (dict(x_mode=1), "gemm: lnmod needs stats and pv"),
     (dict(epi=4), "gemm: bias needs ev"),
+    (dict(N=128), "gemm: weight rows 0 + 128 past the 64 rows of the weight"),
+    (dict(wr0=32), "gemm: weight rows 32 + 64 past the 64 rows of the weight"),
+    (dict(wr0=-64), "gemm: negative weight row"),
+    (dict(w_rows=128, epi=3, N=128, wr0=0, wr1=96), "gemm: weight rows 96 + 64 past the 128 rows of the weight"),
+    (dict(w_rows=128, epi=3, N=128, wr0=96, wr1=0), "gemm: weight rows 96 + 64 past the 128 rows of the weight"),
+    (dict(w_rows=128, N=128, epi=5), "gemm: heads needs ev (the norm weights) and heads.rope"),
+    (dict(w_rows=192, epi=5, N=192, ev=16, rope=16), "gemm: heads needs N a multiple of 128"),
+    (dict(w_rows=128, epi=5, N=128, ev=16, rope=16, heads_ltot=3), "gemm: heads rows 0 + 4 past Ltot 3"),
+    (dict(w_rows=128, epi=5, N=128, ev=16, rope=16, heads_ltot=8, heads_row_off=5),
+     "gemm: heads rows 5 + 4 past Ltot 8"),
+    (dict(w_rows=128, epi=5, N=128, ev=16, rope=16, heads_ltot=8, heads_rope=2), "gemm: heads rope mode 2"),
+    (dict(epi=6), "gemm: epilogue 6"),
 ])
 def test_gemm_argument_errors(kw, msg):
     rc, err = gemm_err(**kw)

@@ -1,0 +1,226 @@
+"""GPU parity at the BASELINE decode configurations B and C (Gemma-4-E2B-shaped, hidden 2048), through the C ABI.
+
+The op sequence is bench.py's decode step at its exact shapes, cut to two layers plus the whole head:
+  qkv 3072x2048 (rms) -> o 2048x2048 (raw, kPer 2048) -> gate_up 2x8192x2048 (rms, geglu) -> down 2048x8192
+  (raw, kPer 2048: 4 K-split partials) -> next layer's qkv (rms over down's first partial) ... -> lm_head
+  262144x2048 (rms, softcap 30, per-tile max / argmax).
+Every op reads its predecessor's output, as in bench.py (the norms between them in the model are not GEMVs; the rstd
+slots are fixed inputs). Config B runs it at M = 1 as one pipelined chain (the headline path) and as a recording of
+standalone launches; config C at M = 5 (the verify pass) both ways, and the M sweep {2, 4, 8, 16} as standalone gemvM
+calls at the qkv and gate_up shapes. Each op is checked against the oracle run on the input that op read on the GPU
+(its predecessor's output, read back), after every output was NaN-filled; the head's 4096 tile maxima are checked
+against the oracle and its argmax indices by their defining property over the GPU's own logits.
+Tolerance: relative L2 <= 1e-3 (BASELINE) and this build's fp32 bar of 2e-5.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from p0pc0rn_amd import capi
+from tests.conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+D, QKV, MLP, V = 2048, 3072, 8192, 262144
+NAN = 0x7FC00000
+
+
+def _check(got, want, what):
+    r = rel_l2(got, want)
+    print(f"{what}: rel_l2 {r:.3e}", flush=True)
+    assert np.all(np.isfinite(got)), what + ": non-finite output"
+    assert r <= 1e-3 and r <= 2e-5, (what, r)
+
+
+class E2B:
+    """two decode layers + the head at bench.py's shapes, M rows; symmetric BASELINE weights filled on the device and,
+    bit-identically, on the host by the oracle's copy of the same counter hash"""
+
+    def __init__(self, M, layers=2, seed=5):
+        self.M, self.L = M, layers
+        shapes = {"qkv": (QKV, D), "o": (D, D), "gu": (2 * MLP, D), "dn": (D, MLP)}
+        self.w_host, self.w_dev = {}, {}
+        for l in range(layers):
+            for i, (k, (n, kk)) in enumerate(shapes.items()):
+                s = seed * 101 + l * 16 + i
+                self.w_host[(l, k)] = O.fill_q4_sym(n, kk, s, 0.02)
+                b = capi.Buffer(n // 64 * kk // 32 * 1280)
+                capi.fill_q4_sym(b, n, kk, s, 0.02)
+                self.w_dev[(l, k)] = b
+        self.w_host["head"] = O.fill_q4_sym(V, D, seed * 101 + 99, 0.02)
+        self.w_dev["head"] = capi.Buffer(V // 64 * D // 32 * 1280)
+        capi.fill_q4_sym(self.w_dev["head"], V, D, seed * 101 + 99, 0.02)
+        self.x = O.fill_randn(M * D, seed)[0]
+        self.nw = np.linspace(0.8, 1.2, D).astype(np.float32)
+        st = np.zeros(2 * M + 4, np.float32)
+        st[1::2][:M] = 1.0 / np.sqrt(1.0 + 1e-6)
+        self.st = st
+        NT = V // 64
+        self.mx_len = M * NT * 2 + 2 * M + 4
+        mx = np.zeros(self.mx_len, np.float32)
+        mx[M * NT * 2 + 1::2][:M] = 0.9
+        self.mx = mx
+        self.mx_stat_off = M * NT * 2 + 1
+        self.dev = {"x": capi.to_device(self.x), "nw": capi.to_device(self.nw), "st": capi.to_device(st),
+                    "mx": capi.to_device(mx)}
+        self.out_len = {}
+        for l in range(layers):
+            self.out_len.update({("qkv", l): M * QKV, ("o", l): M * D, ("gu", l): M * MLP, ("dn", l): 4 * M * D})
+        self.out_len["head"] = M * V
+        self.out = {k: capi.Buffer(4 * n) for k, n in self.out_len.items()}
+
+    def fields(self, bufs, w):
+        """(name, weight key, input key, field dict) per op; bufs / w map keys to Buffers or host pointers"""
+        M, ops = self.M, []
+        P, E = capi.PRO, capi.EPI
+        for l in range(self.L):
+            xin = "x" if l == 0 else ("dn", l - 1)   # the previous down's first K-split partial
+            ops.append((("qkv", l), (l, "qkv"), xin, dict(w_rows=QKV, w_cols=D, N=QKV, K=D, pro=P["rms"],
+                                                             stat=bufs["st"], stat_off=1, norm=bufs["nw"])))
+            ops.append((("o", l), (l, "o"), ("qkv", l), dict(w_rows=D, w_cols=D, N=D, K=D, kPer=2048, pro=P["raw"],
+                                                              x_ldx=QKV)))
+            ops.append((("gu", l), (l, "gu"), ("o", l), dict(w_rows=2 * MLP, w_cols=D, N=MLP, K=D, pro=P["rms"],
+                                                              epi=E["geglu"], stat=bufs["st"], stat_off=1,
+                                                              norm=bufs["nw"])))
+            ops.append((("dn", l), (l, "dn"), ("gu", l), dict(w_rows=D, w_cols=MLP, N=D, K=MLP, kPer=2048,
+                                                               pro=P["raw"])))
+        ops.append(("head", "head", ("dn", self.L - 1), dict(w_rows=V, w_cols=D, N=V, K=D, pro=P["rms"],
+                                                              epi=E["softcap"], stat=bufs["mx"],
+                                                              stat_off=self.mx_stat_off, norm=bufs["nw"],
+                                                              mx=bufs["mx"], cap=30.0)))
+        out = []
+        for name, wk, xk, f in ops:
+            f = dict(f, w=w[wk], x=bufs[xk], y=bufs[name])
+            if M > 1:
+                f.setdefault("x_ldx", f["K"])
+                f.update(M=M, stat_ld=2, y_ldm=f["N"])
+                if f.get("epi", 0) == E["store"]:
+                    f["y_ldy"] = M * f["N"]
+            else:
+                f.pop("x_ldx", None)
+                if f.get("epi", 0) == E["store"]:
+                    f["ldy"] = f["N"]
+            out.append((name, wk, xk, f))
+        return out
+
+    def enqueue(self):
+        for name, wk, xk, f in self.fields(dict(self.dev, **self.out), self.w_dev):
+            if self.M == 1:
+                capi.q4_gemv(capi.gemv_args(**f))
+            else:
+                capi.q4_gemvM(capi.gemvm_args(**f))
+
+    def reset(self):
+        for b in self.out.values():
+            b.fill_u32(NAN)
+        self.dev["mx"].upload(self.mx)
+
+    def check(self, what):
+        got = {k: self.out[k].read(np.float32, n) for k, n in self.out_len.items()}
+        gmx = self.dev["mx"].read(np.float32, self.mx_len)
+        M = self.M
+        hostbuf = {"x": self.x, "st": self.st, "nw": self.nw}
+        for name, wk, xk, f in self.fields({k: 0 for k in list(self.out_len) + ["x", "st", "nw", "mx"]}, self.w_host):
+            xin = np.ascontiguousarray(hostbuf["x"] if xk == "x" else got[xk], np.float32)
+            y = np.full(self.out_len[name], np.nan, np.float32)
+            mx = self.mx.copy()
+            f = dict(f, w=self.w_host[wk].ctypes.data, x=xin.ctypes.data, y=y.ctypes.data, norm=self.nw.ctypes.data)
+            if name == "head":
+                f.update(stat=mx.ctypes.data, mx=mx.ctypes.data)
+            else:
+                f["stat"] = self.st.ctypes.data if "stat" in f else None
+            (O.q4_gemv if M == 1 else O.q4_gemvM)((capi.gemv_args if M == 1 else capi.gemvm_args)(**f))
+            _check(got[name], y, f"{what} {name}")
+        # the head's per-tile (max, argmax): maxima against the oracle, indices by their defining property over the
+        # GPU's own logits (the first row of the tile holding the tile's largest value)
+        NT = V // 64
+        lg = got["head"].reshape(M, NT, 64)
+        gm = gmx[:2 * NT * M:2].reshape(M, NT)
+        gi = gmx[1:2 * NT * M:2].view(np.uint32).reshape(M, NT)
+        assert np.allclose(gm, mx[:2 * NT * M:2].reshape(M, NT), rtol=1e-5, atol=1e-5), what + ": tile maxima"
+        want_i = (np.argmax(lg, axis=2) + np.arange(NT)[None, :] * 64).astype(np.uint32)
+        assert np.array_equal(gi, want_i), what + ": tile argmax"
+        assert np.array_equal(gm, np.take_along_axis(lg, (gi % 64).astype(np.int64)[:, :, None], 2)[:, :, 0])
+
+    def free(self):
+        for b in list(self.w_dev.values()) + list(self.dev.values()) + list(self.out.values()):
+            b.free()
+
+
+@pytest.fixture(scope="module")
+def e2b1(dev):
+    s = E2B(1)
+    yield s
+    s.free()
+
+
+def test_config_b_decode_step_as_one_chain(e2b1):
+    """config B: the E2B-shaped layers + head planned into ONE pipelined chain launch (bench.py's headline path)"""
+    s = e2b1
+    ch = capi.chain(s.enqueue)
+    info = ch.info()
+    print("chain", info, flush=True)
+    assert info["n_ops"] == 4 * s.L + 1 and info["m"] == 1
+    for run in range(2):   # a second run of the same chain (the run tag advances; no reset)
+        s.reset()
+        ch.run()
+        assert not ch.status()
+        s.check(f"config B chain run {run}")
+    ch.free()
+
+
+def test_config_b_decode_step_as_a_recording(e2b1):
+    """config B as a recording of one launch per op (the DecodeRunner's graph mode)"""
+    s = e2b1
+    rec = capi.record(s.enqueue)
+    assert rec.launches() == 4 * s.L + 1
+    s.reset()
+    rec.replay()
+    s.check("config B graph")
+    rec.free()
+
+
+@pytest.mark.parametrize("way", ["chain", "graph"])
+def test_config_c_verify_pass_m5(dev, way):
+    """config C: the verify pass (M = 1 + 4 draft tokens) at the E2B shapes, as one pipelined chain and as a
+    recording of standalone gemvM launches (which run on the matrix cores for M >= 2)"""
+    s = E2B(5, seed=6)
+    try:
+        if way == "chain":
+            ch = capi.chain(s.enqueue)
+            print("chain", ch.info(), flush=True)
+            s.reset()
+            ch.run()
+            assert not ch.status()
+            ch.free()
+        else:
+            rec = capi.record(s.enqueue)
+            s.reset()
+            rec.replay()
+            rec.free()
+        s.check(f"config C M=5 {way}")
+    finally:
+        s.free()
+
+
+@pytest.mark.parametrize("M", [2, 4, 8, 16])
+@pytest.mark.parametrize("op", ["qkv", "gate_up"])
+def test_config_c_sweep_standalone(dev, M, op):
+    """config C's M sweep at the qkv (rms) and gate_up (rms + geglu) shapes: standalone gemvM, each record read once
+    for all M rows"""
+    N, rows, epi = (QKV, QKV, capi.EPI["store"]) if op == "qkv" else (MLP, 2 * MLP, capi.EPI["geglu"])
+    w = O.fill_q4_sym(rows, D, 300 + M, 0.02)
+    x = O.fill_randn(M * D, 301 + M)[0]
+    nw = np.linspace(0.9, 1.1, D).astype(np.float32)
+    st = np.zeros(2 * M, np.float32)
+    st[1::2] = 0.8
+    f = dict(w_rows=rows, w_cols=D, x_ldx=D, M=M, N=N, K=D, pro=capi.PRO["rms"], epi=epi, stat_off=0, stat_ld=2,
+             y_ldm=N)
+    want = np.full(M * N, np.nan, np.float32)
+    O.q4_gemvM(capi.gemvm_args(**f, w=w.ctypes.data, x=x.ctypes.data, y=want.ctypes.data, stat=st.ctypes.data,
+                               norm=nw.ctypes.data))
+    d = {k: capi.to_device(v) for k, v in dict(w=w, x=x, stat=st, norm=nw).items()}
+    yb = capi.Buffer(M * N * 4).fill_u32(NAN)
+    capi.q4_gemvM(capi.gemvm_args(**f, **d, y=yb))
+    _check(yb.read(np.float32), want, f"gemvM M={M} {op}")
+    for b in list(d.values()) + [yb]:
+        b.free()

@@ -138,26 +138,33 @@ const g = await_gpu();
 const up = (name) => { const b = fs.readFileSync(name + '.bin'); return g.upload(new Uint8Array(b.buffer, b.byteOffset, b.length)); };
 const [w1, w2, x] = ['w1', 'w2', 'x'].map(up);
 const y1 = g.buffer(512 * 4), y2 = g.buffer(256 * 4);
-const r = new P.DecodeRunner(g, { mode: '%s' });
-r.begin();
+const r = new P.DecodeRunner(g, { mode: '%s', reuse: true });
+r.begin(0);
 P.gemv(g, { w: { buf: w1, off: 0, enc: 'q4g32a.t64', rows: 512, cols: 1024 }, x: { buf: x }, N: 512, K: 1024, y: { buf: y1 } });
 P.gemv(g, { w: { buf: w2, off: 0, enc: '%s', rows: 256, cols: 512 }, x: { buf: y1 }, N: 256, K: 512, y: { buf: y2 } });
-const tk = r.end();
+const tk = r.end(y2, 16);
 (async () => {
   const outs = [];
   for (let i = 0; i < 3; i++) {
     g.fill(y1, 0, 0x7fc00000, 512); g.fill(y2, 0, 0x7fc00000, 256);
-    await r.submit(tk);
-    outs.push(Buffer.from(await g.read(y2)).toString('base64'));
+    const o32 = await r.submit(tk);   // the token's first four result words, through the parity's staging buffer
+    const y = Buffer.from(await g.read(y2));
+    if (Buffer.compare(Buffer.from(o32.buffer, o32.byteOffset, 16), y.subarray(0, 16)) !== 0) throw new Error('stage');
+    outs.push(y.toString('base64'));
   }
   fs.writeFileSync('y1.bin', Buffer.from(await g.read(y1)));
   fs.writeFileSync('y2.bin', Buffer.from(await g.read(y2)));
-  console.log(JSON.stringify({ same: outs.every((o) => o === outs[0]), submits: r.submits }));
-  r.forget(); g.freeAll(); g.device.destroy();
+  console.log(JSON.stringify({ same: outs.every((o) => o === outs[0]), submits: r.submits, dispatches: r.dispatches }));
+  r.forget();
+  let released = '';
+  try { await r.submit(tk); } catch (e) { released = e.message; }
+  if (!released.includes('released')) throw new Error('a forgotten token must not run: ' + released);
+  await r.destroy(); g.freeAll(); g.device.destroy();
 })();
 """ % (mode, "q4g32a.t64" if enc2 == "q4" else "q8g64s.t64"))
     res = json.loads(out.strip().splitlines()[-1])
     assert res["same"] and res["submits"] == 3
+    assert res["dispatches"] == (2 if mode == "chain" else 3)   # chain: 2 ops; graph: 2 launches + the result copy
     y1 = np.fromfile(str(tmp_path / "y1.bin"), np.float32)
     y2 = np.fromfile(str(tmp_path / "y2.bin"), np.float32)
     want1 = np.zeros(N1, np.float32)
@@ -256,7 +263,7 @@ def make_pack(root):
     (root / "blk.bin").write_bytes(bytes(blk))
     (root / "emb.bin").write_bytes(emb)
     manifest = {
-        "pack_version": "test-1",
+        "format": "pocketflux.pack", "format_version": 1, "pack_version": "test-1",
         "shards": [{"name": "blk", "file": "blk.bin", "bytes": len(blk)}, {"name": "emb", "file": "emb.bin", "bytes": len(emb)}],
         "tensors": {
             "w.q4": {"shard": "blk", "offset": 0, "bytes": wq4.nbytes, "enc": "q4g32a.t64", "shape": [128, 256]},
@@ -432,3 +439,208 @@ const ns = [P.gemv(g, a1(ys[0])), P.gemvV5(g, a1(ys[1]), pick), P.gemvM(g, aM(ys
     r2 = rel_l2(y[3][:nM], want)
     print("gemvMV5", r2)
     assert np.all(np.isfinite(y[3][:nM])) and r2 <= 2e-5
+
+
+# ------------------------------------------------------------------------------------------------ DecodeRunner contract
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["graph", "chain"])
+def test_js_decode_loop_gemma4_shaped(tmp_path, mode):
+    """engine/llm/gemma4.js:547-590's overlapped loop, unchanged in shape: token i is recorded with begin(parity) ...
+    end(argBuf), submitted once its input is written, and `o32 = await pend; o32[0]` is the next id. A token is
+    x = table[id] (written by the host before the submit, as the loop writes s.pler), h = W1 x' (rms), logits =
+    softcap(W2 h') (rms) with per-tile maxima, then (graph mode) argmax over the tiles into the result words; in chain
+    mode (GEMV ops only) the result is tile 0's (max, index) pair. Three tokens; each id must be the oracle's."""
+    D, H, V = 256, 512, 1024
+    w1, _ = O.pack_q4(O.randn(H * D, 41, 0.05), H, D)
+    w2, _ = O.pack_q4(O.randn(V * H, 42, 0.05), V, H)
+    table = O.randn(V * D, 43).reshape(V, D)
+    nw1 = np.linspace(0.8, 1.2, D).astype(np.float32)
+    nw2 = np.linspace(1.1, 0.9, H).astype(np.float32)
+    _save(tmp_path, w1=w1, w2=w2, table=table, nw1=nw1, nw2=nw2)
+    out = run_node(tmp_path, r"""
+const g = await_gpu();
+const up = (name) => { const b = fs.readFileSync(name + '.bin'); return g.upload(new Uint8Array(b.buffer, b.byteOffset, b.length)); };
+const [w1, w2, nw1, nw2] = ['w1', 'w2', 'nw1', 'nw2'].map(up);
+const tb = fs.readFileSync('table.bin'), table = new Float32Array(tb.buffer, tb.byteOffset, tb.length / 4);
+const D = 256, H = 512, V = 1024, mode = '%s';
+const s = { x: g.buffer(D * 4), h: g.buffer(H * 4), logits: g.buffer(V * 4), st: g.buffer(16),
+            mx: g.buffer((V / 64 + 1) * 8), arg: g.buffer(16) };
+g.upload(new Float32Array([0, 1, 0, 1]), '', s.st);          // rstd slots: the rms prologues read 1
+g.upload(new Float32Array([1]), '', s.mx, (V / 64) * 8 + 4);  // the head's rstd lives past the tile maxima
+const encodeStep = () => {
+  P.gemv(g, { w: { buf: w1, off: 0, enc: 'q4g32a.t64', rows: H, cols: D }, x: { buf: s.x, rowB: 0 }, N: H, K: D,
+              pro: 'rms', stat: { buf: s.st, off: 1 }, norm: { buf: nw1, off: 0 }, y: { buf: s.h } });
+  P.gemv(g, { w: { buf: w2, off: 0, enc: 'q4g32a.t64', rows: V, cols: H }, x: { buf: s.h, rowB: 0 }, N: V, K: H,
+              pro: 'rms', stat: { buf: s.mx, off: (V / 64) * 2 + 1 }, norm: { buf: nw2, off: 0 }, epi: 'softcap',
+              cap: 30, mx: { buf: s.mx }, y: { buf: s.logits } });
+  if (mode === 'chain') return s.mx;
+  P.argmax(g, { mx: { buf: s.mx }, n: V / 64, out: { buf: s.arg } });
+  return s.arg;
+};
+const core = g.runner, dr = new P.DecodeRunner(g, { mode });
+const rec = (pos, parity) => { g.runner = dr; try { dr.begin(parity); const ob = encodeStep(pos); return dr.end(ob); } finally { g.runner = core; if (dr.cur) dr.cur = null; } };
+const ids = [], words = [];
+let pend = null, tk = null;
+const feed = async (id, i) => {
+  if (!tk) tk = rec(i, i & 1);
+  g.upload(table.subarray(id * D, (id + 1) * D), '', s.x);
+  pend = dr.submit(tk); tk = null;
+};
+(async () => {
+  await feed(7, 0);
+  tk = rec(1, 1);
+  for (let i = 0; i < 3; i++) {
+    const o32 = await pend; pend = null;
+    words.push([o32[0], o32[1]]);
+    const nxt = mode === 'chain' ? (o32[0] * 3 + 1) %% V : o32[0];   // chain mode: tile 0's index, mapped to an id
+    ids.push(nxt);
+    if (i + 1 < 3) await feed(nxt, i + 1);
+    if (i + 2 < 3) tk = rec(i + 2, i & 1);
+  }
+  await dr.destroy();
+  console.log(JSON.stringify({ ids, words, submits: dr.submits, dispatches: dr.dispatches }));
+  g.freeAll(); g.device.destroy();
+})();
+""" % mode)
+    res = json.loads(out.strip().splitlines()[-1])
+    assert res["submits"] == 3
+    st_mx = np.zeros((V // 64 + 1) * 2, np.float32)
+    st_mx[(V // 64) * 2 + 1] = 1.0
+    st = np.array([0, 1, 0, 1], np.float32)
+    cur = 7
+    for i in range(3):
+        x = np.ascontiguousarray(table[cur])
+        h = np.zeros(H, np.float32)
+        O.q4_gemv(capi.gemv_args(w=w1.ctypes.data, w_rows=H, w_cols=D, x=x.ctypes.data, N=H, K=D, pro=capi.PRO["rms"],
+                                 y=h.ctypes.data, stat=st.ctypes.data, stat_off=1, norm=nw1.ctypes.data))
+        lg = np.zeros(V, np.float32)
+        mx = st_mx.copy()
+        O.q4_gemv(capi.gemv_args(w=w2.ctypes.data, w_rows=V, w_cols=H, x=h.ctypes.data, N=V, K=H,
+                                 pro=capi.PRO["rms"], epi=capi.EPI["softcap"], y=lg.ctypes.data, mx=mx.ctypes.data,
+                                 stat_off=(V // 64) * 2 + 1, norm=nw2.ctypes.data, cap=30.0))
+        if mode == "chain":
+            idx, val = int(mx[1:2].view(np.uint32)[0]), mx[0]
+            nxt = (idx * 3 + 1) % V
+        else:
+            idx = int(np.argmax(lg))
+            val = lg[idx]
+            nxt = idx
+        got_idx, got_bits = res["words"][i]
+        assert got_idx == idx, (i, got_idx, idx)
+        assert abs(np.uint32(got_bits).view(np.float32) - val) <= 1e-4 * max(1.0, abs(val))
+        assert res["ids"][i] == nxt
+        cur = nxt
+    assert res["dispatches"] == 3 * (2 if mode == "chain" else 4)   # graph: 2 GEMVs + argmax + the result copy
+
+
+def test_js_fp16_helpers_exhaustive(tmp_path):
+    """the host's f2h / h2f (p0pc0rn_amd/js/core/gpu.mjs, the reference's CPU helpers engine/core/gpu.js:273-297):
+    h2f over all 65536 patterns and f2h over random f32 bit patterns, every half value, every midpoint between
+    neighbouring halves (ties to even) and the f32 neighbours of those midpoints, against numpy's IEEE binary16 RNE"""
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    rng = np.random.default_rng(11)
+    halves = np.arange(0, 0x7c00, dtype=np.uint16).view(np.float16).astype(np.float64)
+    mids = ((halves[:-1] + halves[1:]) / 2).astype(np.float32)
+    vals = [rng.integers(0, 2 ** 32, 200_000, dtype=np.uint64).astype(np.uint32).view(np.float32),
+            halves.astype(np.float32), mids, np.nextafter(mids, np.float32(np.inf)),
+            np.nextafter(mids, np.float32(-np.inf)),
+            np.float32([65504, 65519, 65519.996, 65520, 65536, 1e9, np.inf, -np.inf, 0.0, -0.0, 2 ** -24, 2 ** -25,
+                        1.5 * 2 ** -25, 2 ** -26, 6.1e-5, -6.1e-5])]
+    f = np.concatenate([v.astype(np.float32) for v in vals])
+    f = np.concatenate([f, -f])
+    _save(tmp_path, h=h, f=f)
+    run_node(tmp_path, r"""
+const hb = fs.readFileSync('h.bin'), fb = fs.readFileSync('f.bin');
+const H = new Uint16Array(hb.buffer, hb.byteOffset, hb.length / 2), F = new Float32Array(fb.buffer, fb.byteOffset, fb.length / 4);
+const ho = new Float64Array(H.length), fo = new Uint16Array(F.length);
+for (let i = 0; i < H.length; i++) ho[i] = P.h2f(H[i]);
+for (let i = 0; i < F.length; i++) fo[i] = P.f2h(F[i]);
+fs.writeFileSync('ho.bin', Buffer.from(ho.buffer)); fs.writeFileSync('fo.bin', Buffer.from(fo.buffer));
+console.log('ok');
+""")
+    ho = np.fromfile(str(tmp_path / "ho.bin"), np.float64)
+    want_h = h.view(np.float16).astype(np.float64)
+    nan = np.isnan(want_h)
+    assert np.array_equal(np.isnan(ho), nan) and np.array_equal(ho[~nan], want_h[~nan])
+    assert np.array_equal(np.signbit(ho[~nan]), np.signbit(want_h[~nan]))   # -0 stays -0
+    fo = np.fromfile(str(tmp_path / "fo.bin"), np.uint16)
+    fn = np.isnan(f)
+    assert np.array_equal(fo[~fn], f[~fn].astype(np.float16).view(np.uint16))
+    assert np.all(fo[fn] == 0x7e00)
+
+
+def test_js_weightstore_open_status_and_errors(tmp_path):
+    """WeightStore (engine/core/store.js:50-115): open() reads and checks the manifest with the reference's texts,
+    status() / download() report a missing shard, readRows takes unsorted and repeated ids, PackStore.init = open"""
+    pk = tmp_path / "pack"
+    pk.mkdir()
+    exp = make_pack(pk)
+    bad = tmp_path / "bad"
+    bad.mkdir()
+    (bad / "manifest.json").write_text(json.dumps({"format": "other", "format_version": 2, "shards": [], "tensors": {}}))
+    out = run_node(tmp_path, r"""
+(async () => {
+  const res = [];
+  const t = async (fn) => { try { await fn(); res.push('no error'); } catch (e) { res.push(e.message); } };
+  await t(() => new P.WeightStore({}, { base: 'nowhere' }).open());
+  await t(() => new P.WeightStore({}, { base: 'bad' }).open());
+  const st = new P.WeightStore({}, { base: 'pack' });
+  const m = await st.open();
+  res.push(m.pack_version, JSON.stringify(st.status()));
+  const r4 = await st.readRows('emb.q4', [9, 3, 3, 4, 0]);
+  fs.writeFileSync('r4.bin', Buffer.from(r4.buffer));
+  fs.truncateSync('pack/emb.bin', 10);
+  const s2 = st.status();
+  res.push(s2.complete, s2.missing.join(','));
+  await t(() => st.download());
+  const ps = await new P.PackStore({}, { dir: 'pack' }).init();
+  res.push(ps.m.pack_version);
+  console.log(JSON.stringify(res));
+})();
+""")
+    res = json.loads(out.strip().splitlines()[-1])
+    assert res[0] == "pack manifest unavailable (offline and not downloaded)"
+    assert res[1] == "unsupported pack format other/2"
+    assert res[2] == "test-1"
+    st = json.loads(res[3])
+    assert st["complete"] and st["missing"] == [] and st["have"] == st["total"]
+    r4 = np.fromfile(str(tmp_path / "r4.bin"), np.float32).reshape(5, 64)
+    assert np.array_equal(r4, exp["want4"][[9, 3, 3, 4, 0]])
+    assert res[4] is False and res[5] == "emb"
+    assert res[6] == "download: no network source; the pack directory lacks emb"
+    assert res[7] == "test-1"
+
+
+def test_js_view_bounds_and_unsupported_options(tmp_path):
+    """views are checked against their buffers on the host (a handle with _pf), and the options this build does not
+    have are refused with an Error instead of running something else"""
+    out = run_node(tmp_path, r"""
+const buf = (n) => ({ ptr: 0, _pf: n });
+const res = [];
+const t = (f) => { try { f(); res.push('no error'); } catch (e) { res.push(e.message); } };
+const W = (rows, cols, b) => ({ buf: b || buf(rows / 64 * cols / 32 * 1280), off: 0, enc: 'q4g32a.t64', rows, cols });
+t(() => P.gemv({}, { w: W(128, 256), x: { buf: buf(255 * 4) }, N: 128, K: 256, y: { buf: buf(512) } }));
+t(() => P.gemv({}, { w: W(128, 256), x: { buf: buf(1024) }, N: 128, K: 256, y: { buf: buf(511) } }));
+t(() => P.gemv({}, { w: W(128, 256, buf(1000)), x: { buf: buf(1024) }, N: 128, K: 256, y: { buf: buf(512) } }));
+t(() => P.gemvM({}, { w: W(128, 256), x: { buf: buf(1024 * 3 - 4), ldx: 256 }, M: 3, N: 128, K: 256, y: { buf: buf(1536) } }));
+t(() => P.gemm({}, { w: W(128, 256), x: { buf: buf(4 * 256 * 2 - 2) }, M: 4, N: 128, K: 256, y: { buf: buf(1024) } }));
+t(() => P.gemm({}, { w: W(128, 256), x: { buf: buf(2048) }, M: 4, N: 128, K: 256, epi: 'f32', y: { buf: buf(2047) } }));
+t(() => P.gemm({}, { w: W(128, 256), x: { buf: buf(2048) }, M: 4, N: 128, K: 256, acc: 'f16', y: { buf: buf(1024) } }));
+t(() => P.gemm({}, { w: W(128, 256), x: { buf: buf(2048) }, M: 4, N: 128, K: 256, epi: 'onormgate', y: { buf: buf(1024) } }));
+t(() => P.gemm({}, { w: W(256, 256), x: { buf: buf(2048) }, M: 4, N: 256, K: 256, epi: 'heads', y: { buf: buf(4096) },
+                     ev: { buf: buf(1024) }, heads: { Ltot: 4, Hq: 1, Hkv: 0, ropeMode: 'inter', rope: { buf: buf(2047) } } }));
+t(() => P.gemm({}, { w: W(256, 256), x: { buf: buf(2048) }, M: 4, N: 256, K: 256, epi: 'heads', y: { buf: buf(4096) },
+                     heads: { Ltot: 4, ropeMode: 'sideways' } }));
+console.log(JSON.stringify(res));
+""")
+    res = json.loads(out.strip().splitlines()[-1])
+    assert res[0] == "gemv: x needs 1024 B of a 1020 B buffer"
+    assert res[1] == "gemv: y needs 512 B of a 511 B buffer"
+    assert res[2] == "gemv: w needs 20480 B of a 1000 B buffer"
+    assert res[3] == "gemvM: x needs 3072 B of a 3068 B buffer"
+    assert res[4] == "gemm: x needs 2048 B of a 2046 B buffer"
+    assert res[5] == "gemm: y needs 2048 B of a 2047 B buffer"
+    assert res[6] == "gemm: acc f16 is not part of this build (it accumulates in fp32)"
+    assert res[7] == "gemm: epilogue onormgate is not part of this build"
+    assert res[8] == "gemm: heads.rope needs 2048 B of a 2047 B buffer"
+    assert res[9] == "gemm: heads ropeMode sideways"
