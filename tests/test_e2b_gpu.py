@@ -103,7 +103,7 @@ class E2B:
         return out
 
     def enqueue(self):
-        for name, wk, xk, f in self.fields(dict(self.dev, **self.out), self.w_dev):
+        for name, wk, xk, f in self.fields({**self.dev, **self.out}, self.w_dev):
             if self.M == 1:
                 capi.q4_gemv(capi.gemv_args(**f))
             else:

@@ -204,8 +204,9 @@ def test_flux_block_out_and_mlp_calls(dev):
     rows = ROWS
     rr = np.ascontiguousarray(resid.reshape(L, D)[rows])
     want1 = rr.copy()
-    O.q4_gemm(capi.gemm_args(w=w_proj.ctypes.data, w_rows=D, w_cols=D, x=np.ascontiguousarray(o16.reshape(L, D)[rows]).ctypes.data,
-                             M=len(rows), N=D, K=D, epi=capi.GEPI["resadd"], y=want1.ctypes.data, ev=gate.ctypes.data))
+    orow = np.ascontiguousarray(o16.reshape(L, D)[rows])   # bound to a name: ctypes takes its address
+    O.q4_gemm(capi.gemm_args(w=w_proj.ctypes.data, w_rows=D, w_cols=D, x=orow.ctypes.data, M=len(rows), N=D, K=D,
+                             epi=capi.GEPI["resadd"], y=want1.ctypes.data, ev=gate.ctypes.data))
     check(g_r1[rows], want1, "FLUX proj resadd", 1e-5)
     want_m = np.zeros((len(rows), MLP), np.float16)
     st_s = np.ascontiguousarray(st.reshape(L, 2)[rows])

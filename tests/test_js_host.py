@@ -491,8 +491,10 @@ const feed = async (id, i) => {
   tk = rec(1, 1);
   for (let i = 0; i < 3; i++) {
     const o32 = await pend; pend = null;
-    words.push([o32[0], o32[1]]);
-    const nxt = mode === 'chain' ? (o32[0] * 3 + 1) %% V : o32[0];   // chain mode: tile 0's index, mapped to an id
+    // graph: the argmax words [index, max bits]; chain: tile 0's [max bits, index] pair, its index mapped to an id
+    const idx = mode === 'chain' ? o32[1] : o32[0], bits = mode === 'chain' ? o32[0] : o32[1];
+    words.push([idx, bits]);
+    const nxt = mode === 'chain' ? (idx * 3 + 1) %% V : idx;
     ids.push(nxt);
     if (i + 1 < 3) await feed(nxt, i + 1);
     if (i + 2 < 3) tk = rec(i + 2, i & 1);
