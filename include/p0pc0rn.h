@@ -194,6 +194,14 @@ typedef struct {
   const float* rope;   /* the RoPE table (a.heads.rope.buf) */
 } p0_gemm_args_t;
 int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out);
+/* p0_q4_gemm without any allocation. No counterpart in the reference: this is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The same kernels and
+ * results as p0_q4_gemm; the activation staging that bf16 / lnmod / rms / unaligned fp16 activations need goes to a
+ * static device scratch of 32 MiB (M * K * 2 bytes at most, else P0_EINVAL), allocated with the library's code on each
+ * GPU and held until the process ends. Every call on one GPU shares that scratch: calls that may overlap on one GPU
+ * (two streams, two threads) race and must be ordered by the caller. Nothing in it needs to start at zero (each call
+ * writes all it reads). */
+int p0_q4_gemm_noalloc(const p0_gemm_args_t* a, double* flops_out);
 
 /* ---- bit-exact dequant of whole q4g32a.t64 weights --------------------------------------------------------------- */
 /* out32 (may be NULL): fl32(q * scale + min), row-major [N][K]; out16 (may be NULL): fl16 of that, the GEMM tile value. */

@@ -493,9 +493,25 @@ static const char* gepi_name(int e) {
 }  // namespace p0
 
 namespace p0 {
+// The no-allocation GEMM's activation staging: a file-scope device array, 32 MiB (M K fp16 values of X', e.g. the
+// FLUX.2-klein block's 4608 x 3072 rows with room to spare), held by every GPU the library runs on until the process
+// ends. Host code never uses the array's name as an address: its device address on each GPU is looked up once, at
+// p0_open with that device current, and kept per device.
+constexpr size_t kScratchBytes = 32ull << 20;
+constexpr int kScratchDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+static void* g_scratch[kScratchDevices] = {};
+
 // more than 64 KB of dynamic LDS must be allowed once per kernel; done at p0_open, so no call sets it lazily (for
-// instance while its stream is being captured)
+// instance while its stream is being captured). Also looks up the scratch address on the current device.
 int gemm_init() {
+  int dv = -1;
+  P0_HIP(hipGetDevice(&dv), "p0_open: gemm");
+  if (dv >= 0 && dv < kScratchDevices && !g_scratch[dv]) {
+    void* ptr = nullptr;
+    P0_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "p0_open: gemm scratch address");
+    g_scratch[dv] = ptr;
+  }
   P0_HIP(hipFuncSetAttribute((const void*)q4_gemm_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds),
          "p0_open: gemm");
   P0_HIP(hipFuncSetAttribute((const void*)q4_gemm_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds),
@@ -506,7 +522,9 @@ int gemm_init() {
 
 using namespace p0;
 
-extern "C" int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out) {
+// The GEMM call. stage_fixed != nullptr: the activation staging goes to that buffer of stage_cap bytes (the
+// no-allocation entry point's static scratch) instead of the context's workspace, which may grow (hipMalloc).
+static int gemm_call(const p0_gemm_args_t* a, double* flops_out, void* stage_fixed, size_t stage_cap) {
   if (!a) { set_error("gemm: no arguments"); return P0_EINVAL; }
   if (a->w_enc != P0_ENC_Q4G32A_T64) {   // engine/ops/gemm.js:266-267
     set_error(a->w_enc == P0_ENC_Q8G64S_T64 ? "gemm: unsupported weight encoding q8g64s.t64 (this build: q4g32a.t64)"
@@ -553,8 +571,18 @@ extern "C" int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out) {
     set_error("gemm: %s needs stats and pv", a->x_mode == P0_XMODE_LNMOD ? "lnmod" : "rms"); return P0_EINVAL;
   }
   if (a->epi == P0_GEPI_BIAS && !a->ev) { set_error("gemm: bias needs ev"); return P0_EINVAL; }
+  // X': the caller's fp16 rows when they can be streamed as they are (16-byte aligned rows), else one staging pass
+  const int64_t ldx = a->x_ld ? a->x_ld : K;
+  const uint8_t* xbase = (const uint8_t*)a->x + a->x_off;
+  const bool direct = a->x_mode == P0_XMODE_F16 && ((uintptr_t)(xbase + 2 * a->x_k0) % 16 == 0) && (2 * ldx) % 16 == 0;
+  if (!direct && stage_cap && (size_t)M * K * 2 > stage_cap) {
+    set_error("gemm_noalloc: the activations need %lld B of fp16 staging; the static scratch holds %zu B",
+              (long long)(M * K * 2), stage_cap);
+    return P0_EINVAL;
+  }
   if (int r = require_open("gemm")) return r;
   if (int r = refuse_in_chain("gemm")) return r;
+  if (stage_cap && !stage_fixed) { set_error("gemm_noalloc: no scratch on device %d", ctx().device); return P0_ENODEV; }
 
   GemmP p{};
   p.w = (const uint8_t*)a->w + a->w_off;
@@ -573,29 +601,29 @@ extern "C" int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out) {
   p.hrope = a->heads_rope; p.heps = a->heads_eps != 0.0f ? a->heads_eps : 1e-6f; p.rope = a->rope;
   (void)gepi_name;
 
-  // X': the caller's fp16 rows when they can be streamed as they are (16-byte aligned rows), else one staging pass
-  const int64_t ldx = a->x_ld ? a->x_ld : K;
-  const uint8_t* xbase = (const uint8_t*)a->x + a->x_off;
-  const bool direct = a->x_mode == P0_XMODE_F16 && ((uintptr_t)(xbase + 2 * a->x_k0) % 16 == 0) && (2 * ldx) % 16 == 0;
   if (direct) {
     p.x = (const _Float16*)xbase + a->x_k0;
     p.ldx = ldx;
   } else {
-    if (int r = ensure_xstage((size_t)M * K * 2, "gemm")) return r;
-    keep_for_recording(ctx().xstage_keep);
+    void* stage = stage_fixed;
+    if (!stage) {
+      if (int r = ensure_xstage((size_t)M * K * 2, "gemm")) return r;
+      keep_for_recording(ctx().xstage_keep);
+      stage = ctx().xstage;
+    }
     XStageP q{};
     q.x = xbase; q.ldx = ldx; q.kx0 = a->x_k0; q.xmode = a->x_mode;
     q.M = (int)M; q.K = (int)K;
     q.st = a->stats; q.stOff = a->stats_off;
     q.pv = a->pv; q.pvOff = a->pv_off; q.pvShift = (uint32_t)(a->pv_off + a->pv_stride);
-    q.out = (_Float16*)ctx().xstage;
+    q.out = (_Float16*)stage;
     const int esz = (a->x_mode == P0_XMODE_F16 || a->x_mode == P0_XMODE_BF16) ? 2 : 4;
     q.vec = ((uintptr_t)(xbase + esz * a->x_k0) % 16 == 0) && (esz * ldx) % 16 == 0;
     const int64_t chunks = M * (K / 8);
     const int64_t blocks = (chunks + 255) / 256 < 8192 ? (chunks + 255) / 256 : 8192;
     hipLaunchKernelGGL(x_stage_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx().cur, q);
     P0_LAUNCHED("gemm");
-    p.x = (const _Float16*)ctx().xstage;
+    p.x = (const _Float16*)stage;
     p.ldx = K;
   }
   const int64_t tiles = ((N + BN - 1) / BN) * ((M + BM - 1) / BM);
@@ -606,4 +634,13 @@ extern "C" int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out) {
   P0_LAUNCHED("gemm");
   if (flops_out) *flops_out = 2.0 * (double)M * (double)N * (double)K;
   return P0_OK;
+}
+
+extern "C" int p0_q4_gemm(const p0_gemm_args_t* a, double* flops_out) { return gemm_call(a, flops_out, nullptr, 0); }
+
+// The no-allocation variant: the same kernels, the activation staging in the static scratch of this file (its
+// address on the open device was looked up at p0_open); nothing is allocated or freed.
+extern "C" int p0_q4_gemm_noalloc(const p0_gemm_args_t* a, double* flops_out) {
+  const int dv = ctx().device;
+  return gemm_call(a, flops_out, dv >= 0 && dv < kScratchDevices ? g_scratch[dv] : nullptr, kScratchBytes);
 }
