@@ -276,6 +276,54 @@ __device__ __forceinline__ void heads_epilogue(const GemmP& p, float16v (&acc)[W
 }
 
 
+// ---- the epilogues: acc[i][j][e] is row 8 (e / 4) + 4 (lane / 32) + e % 4, column lane % 32 of
+// block (i, j) of the wave's 128 x 64 sub-tile. One loop per epilogue (a uniform branch), each small enough to unroll
+// completely: the accumulators stay in registers.
+template <bool HEADS>
+__device__ __forceinline__ void gemm_epilogue(const GemmP& p, float16v (&acc)[WTM / 32][WTN / 32], uint8_t* lds, int m0,
+                                              int n0, int wm, int wn, int lane) {
+  const int mb = m0 + wm * WTM + 4 * (lane >> 5), nb = n0 + wn * WTN + (lane & 31);
+#define P0_EPI_LOOP(...)                                                    \
+  _Pragma("unroll") for (int i = 0; i < IB; ++i)                            \
+  _Pragma("unroll") for (int j = 0; j < JB; ++j)                            \
+  _Pragma("unroll") for (int e = 0; e < 16; ++e) {                          \
+    const int m = mb + i * 32 + 8 * (e >> 2) + (e & 3), n = nb + j * 32;    \
+    const float a = acc[i][j][e];                                           \
+    const int64_t o = (int64_t)m * p.ldy + p.ny0;                           \
+    __VA_ARGS__                                                             \
+  }
+  if (HEADS) {
+    heads_epilogue(p, acc, lds, m0, n0, wm, wn, lane);
+  } else if (p.epi == P0_GEPI_F16) {
+    P0_EPI_LOOP(if (m < p.M && n < p.N) ((_Float16*)p.y)[o + n] = to_h(a);)
+  } else if (p.epi == P0_GEPI_F32) {
+    P0_EPI_LOOP(if (m < p.M && n < p.N) ((float*)p.y)[o + n] = a;)
+  } else if (p.epi == P0_GEPI_RESADD) {   // engine/ops/gemm.js:192-197
+    P0_EPI_LOOP(if (m < p.M && n < p.N) {
+      const float g = p.ev ? p.ev[p.evOff + n] : 1.0f, b = p.bv ? p.bv[p.bvOff + n] : 0.0f;
+      float* yp = (float*)p.y + o + n;
+      *yp = p.store ? g * (a + b) : *yp + g * (a + b);
+    })
+  } else if (p.epi == P0_GEPI_BIAS) {
+    P0_EPI_LOOP(if (m < p.M && n < p.N) {
+      _Float16* yp = (_Float16*)p.y + o + n;
+      float r = a + p.ev[p.evOff + n];
+      if (p.res) r += (float)*yp;
+      *yp = to_h(r);
+    })
+  } else {   // swiglu: gate = even column, up = the next one, in the neighbouring lane (engine/ops/gemm.js:200-206)
+    P0_EPI_LOOP({
+      const float up = __shfl_xor(a, 1, 64);
+      if (m < p.M && n < p.N && !(n & 1)) {
+        const int jn = n >> 1;
+        const float gB = p.bv ? p.bv[p.bvOff + jn] : 0.0f, uB = p.bv ? p.bv[p.bvOff + p.bvUp + jn] : 0.0f;
+        ((_Float16*)p.y)[o + jn] = to_h(act_f(p, a + gB) * (up + uB));
+      }
+    })
+  }
+#undef P0_EPI_LOOP
+}
+
 // HEADS: the instantiation with the heads epilogue (the others' register allocation stays as it is without it)
 template <bool HEADS>
 __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmP p) {
@@ -433,49 +481,7 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmP p) {
     }
   }
 
-  // ---- epilogue: acc[i][j][e] is row 8 (e / 4) + 4 (lane / 32) + e % 4, column lane % 32 of block (i, j).
-  // One loop per epilogue (a uniform branch), each small enough to unroll completely: the accumulators stay in
-  // registers.
-  const int mb = m0 + wm * WTM + 4 * (lane >> 5), nb = n0 + wn * WTN + (lane & 31);
-#define P0_EPI_LOOP(...)                                                    \
-  _Pragma("unroll") for (int i = 0; i < IB; ++i)                            \
-  _Pragma("unroll") for (int j = 0; j < JB; ++j)                            \
-  _Pragma("unroll") for (int e = 0; e < 16; ++e) {                          \
-    const int m = mb + i * 32 + 8 * (e >> 2) + (e & 3), n = nb + j * 32;    \
-    const float a = acc[i][j][e];                                           \
-    const int64_t o = (int64_t)m * p.ldy + p.ny0;                           \
-    __VA_ARGS__                                                             \
-  }
-  if (HEADS) {
-    heads_epilogue(p, acc, lds, m0, n0, wm, wn, lane);
-  } else if (p.epi == P0_GEPI_F16) {
-    P0_EPI_LOOP(if (m < p.M && n < p.N) ((_Float16*)p.y)[o + n] = to_h(a);)
-  } else if (p.epi == P0_GEPI_F32) {
-    P0_EPI_LOOP(if (m < p.M && n < p.N) ((float*)p.y)[o + n] = a;)
-  } else if (p.epi == P0_GEPI_RESADD) {   // engine/ops/gemm.js:192-197
-    P0_EPI_LOOP(if (m < p.M && n < p.N) {
-      const float g = p.ev ? p.ev[p.evOff + n] : 1.0f, b = p.bv ? p.bv[p.bvOff + n] : 0.0f;
-      float* yp = (float*)p.y + o + n;
-      *yp = p.store ? g * (a + b) : *yp + g * (a + b);
-    })
-  } else if (p.epi == P0_GEPI_BIAS) {
-    P0_EPI_LOOP(if (m < p.M && n < p.N) {
-      _Float16* yp = (_Float16*)p.y + o + n;
-      float r = a + p.ev[p.evOff + n];
-      if (p.res) r += (float)*yp;
-      *yp = to_h(r);
-    })
-  } else {   // swiglu: gate = even column, up = the next one, in the neighbouring lane (engine/ops/gemm.js:200-206)
-    P0_EPI_LOOP({
-      const float up = __shfl_xor(a, 1, 64);
-      if (m < p.M && n < p.N && !(n & 1)) {
-        const int jn = n >> 1;
-        const float gB = p.bv ? p.bv[p.bvOff + jn] : 0.0f, uB = p.bv ? p.bv[p.bvOff + p.bvUp + jn] : 0.0f;
-        ((_Float16*)p.y)[o + jn] = to_h(act_f(p, a + gB) * (up + uB));
-      }
-    })
-  }
-#undef P0_EPI_LOOP
+  gemm_epilogue<HEADS>(p, acc, lds, m0, n0, wm, wn, lane);
 }
 
 static const char* gepi_name(int e) {
@@ -627,10 +633,9 @@ static int gemm_call(const p0_gemm_args_t* a, double* flops_out, void* stage_fix
     p.ldx = K;
   }
   const int64_t tiles = ((N + BN - 1) / BN) * ((M + BM - 1) / BM);
-  if (a->epi == P0_GEPI_HEADS)
-    hipLaunchKernelGGL(q4_gemm_kernel<true>, dim3((unsigned)tiles), dim3(kThreads), kGemmLds, ctx().cur, p);
-  else
-    hipLaunchKernelGGL(q4_gemm_kernel<false>, dim3((unsigned)tiles), dim3(kThreads), kGemmLds, ctx().cur, p);
+  const bool heads = a->epi == P0_GEPI_HEADS;
+  hipLaunchKernelGGL(heads ? q4_gemm_kernel<true> : q4_gemm_kernel<false>, dim3((unsigned)tiles), dim3(kThreads),
+                     kGemmLds, ctx().cur, p);
   P0_LAUNCHED("gemm");
   if (flops_out) *flops_out = 2.0 * (double)M * (double)N * (double)K;
   return P0_OK;

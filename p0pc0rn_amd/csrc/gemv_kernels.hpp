@@ -212,9 +212,12 @@ struct Rec {
 
 // ---- GEMV-M on MFMA (standalone launches, M >= 2). Per q4 group and 16 weight rows, two v_mfma_f32_16x16x32_f16
 // compute D[m][n] = 2^8 sum_k x'[m][k] q[n][k]: the A operand holds 2^8 x' split into fp16 hi + lo (2^8 x' = hi + lo to
-// 2^-22), the B operand the codes as exact fp16 values q (even k) and 16 q (odd k, whose x' carry the 1/16). The matrix
-// cores flush fp16 subnormals, so every operand is kept normal: the codes come out of a code word as 1024 + q
-// (OR-ing the exponent of 1024 into masked nibbles) minus 1024, and the 2^8 keeps lo normal down to |x'| ~ 2^-11.
+// 2^-22), the B operand the codes as exact fp16 values q (even k) and 16 q (odd k, whose x' carry the 1/16). Every
+// operand is kept a normal fp16 number (a one-instruction probe on MI355X found fp16 subnormal inputs NOT flushed, but
+// this path does not depend on that): the codes come out of a code word as 1024 + q (OR-ing the exponent of 1024 into
+// masked nibbles) minus 1024, and the 2^8 keeps lo normal down to |x'| ~ 2^-11.
+// Rounding: these rows are not bit-identical to the fp32 VALU path's (which p0_q4_gemv and the chain kernels use);
+// they agree to ~3e-7 relative L2. The VALU path for every M is p0_gemv_tune knob 4 = 17.
 // Lane l holds D[4 (l / 16) + i][l % 16]: one weight row per lane, so each lane applies its row's scale and min
 // (2^-8 s D + m sum x') in fp32.
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
