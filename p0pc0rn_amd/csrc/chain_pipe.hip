@@ -317,13 +317,20 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
     return ctl_ld(lctl + L::CtlGo) != 0;
   };
   // x' of groups [g0, g1) from the previous op's mailbox: each compute thread polls its own elements until all of them
-  // carry this run's tag (bounded like wait_flags), then writes x' and the group sums as stage_x does (raw prologue).
-  // The poll is the load: the hand-off costs one memory round trip instead of a flag round trip and then an x load.
+  // carry this run's tag (bounded like wait_flags), then writes x' and the group sums as stage_x does (raw or rms
+  // prologue: for rms the rstd slot and the thread's norm weights are loaded before the poll, as they are inputs of
+  // the chain). The poll is the load: the hand-off costs one memory round trip instead of a flag round trip and then
+  // an x load.
   auto stage_mbx = [&](const GemvP& p, int g0, int g1, int gps, float odd) -> bool {
     constexpr int U = 4, NT = 64 * kPC;
     const int KL = gps * 32, kb = g0 * 32, ke = g1 * 32;
+    const bool rms = p.pro == P0_PRO_RMS;
+    const float rstd = rms ? p.ST[p.statOff] : 1.0f;
     int go = spin_limit >= 0;
     for (int i0 = 0; go && i0 < KL; i0 += U * NT) {
+      float nw[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) nw[u] = rms ? p.NW[p.nOff + min(kb + i0 + u * NT + tc, ke - 1)] : 1.0f;
       unsigned long long w[U];
       for (int spins = 0;; ++spins) {
         bool ok = true;
@@ -346,7 +353,8 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int kl = i0 + u * NT + tc;
-        const float v = kb + kl < ke ? __uint_as_float((unsigned)w[u]) : 0.0f;
+        const float xv = __uint_as_float((unsigned)w[u]);
+        const float v = kb + kl < ke ? (rms ? xv * rstd * nw[u] : xv) : 0.0f;   // the rms prologue's own order
         const float gsum = sum32(v);
         if (kl < KL) {
           xs[kl] = (kl & 1) ? v * odd : v;   // kb is even: k and kl share parity
@@ -362,9 +370,10 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
     cbar();
     return ctl_ld(lctl + L::CtlGo) != 0;
   };
-  // this op's rows, with their values as stored, into its mailbox (after the epilogue's own stores)
-  auto post_mbx = [&](const GemvP& p, int n, float v) {
-    __hip_atomic_store(P0_GLOBAL(unsigned long long, p.mbxOut + n),
+  // this op's rows, with their values as stored, into its mailbox (after the epilogue's own stores): the element of
+  // split `split`, row n sits at its offset from Y, split * ldy + n
+  auto post_mbx = [&](const GemvP& p, int split, int n, float v) {
+    __hip_atomic_store(P0_GLOBAL(unsigned long long, p.mbxOut + (int64_t)split * p.ldy + n),
                        ((unsigned long long)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
   const unsigned* const mine = flags + (size_t)(b % kFlagCopies) * n_ops * Gp;   // this XCD's copy
@@ -380,8 +389,8 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
       const int xgps = q8 ? 16 * s.nh : 32 * s.nh;
       const float odd = q8 ? 1.0f : 0.0625f;
       if (p.mbxIn) {
-        // op i - 1's completion is not waited for here: its mailbox says its outputs are all written. Op i + 1 waits
-        // for op i - 1's flags with op i's (GemvP::flags2), so every later op still sees every earlier op complete.
+        // op i - 1's completion is not waited for here: its mailbox says its outputs are all written, and with them
+        // that every earlier op is complete (the planner's argument, gemv.hip plan_mailboxes)
         if (!stage_mbx(p, xg0, xg1, xgps, odd)) {
           abandon = true;
           break;
@@ -472,7 +481,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
             if (tc < rows) {
               const float yv = (p.coh & 2) ? epilogue<true>(p, s.split, m, n >> 6, n & 63, v0, v1)
                                            : epilogue<false>(p, s.split, m, n >> 6, n & 63, v0, v1);
-              if (M == 1 && p.mbxOut) post_mbx(p, n, yv);
+              if (M == 1 && p.mbxOut) post_mbx(p, s.split, n, yv);
             }
           }
         }
@@ -557,7 +566,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
             if (lane < rows || p.epi == P0_EPI_SOFTCAP) {
               const float yv = (p.coh & 2) ? epilogue<true>(p, s.split, m, n >> 6, n & 63, v0, v1)
                                            : epilogue<false>(p, s.split, m, n >> 6, n & 63, v0, v1);
-              if (M == 1 && p.mbxOut && lane < rows) post_mbx(p, n, yv);
+              if (M == 1 && p.mbxOut && lane < rows) post_mbx(p, s.split, n, yv);
             }
           }
           __builtin_amdgcn_s_waitcnt(0xC07F);

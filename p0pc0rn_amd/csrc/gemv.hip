@@ -212,39 +212,52 @@ static void mark_coherence(std::vector<GemvP>& ops, int M) {
   }
 }
 
-// Mailbox hand-offs of a pipelined M = 1 chain (chain_pipe.hip). Op i takes its x from op i - 1's mailbox when
-//  * op i - 1 has one split and a store or geglu epilogue (it writes final values, all N of them), and did not take its
-//    own input from a mailbox,
-//  * op i has the raw prologue and its x[0, K) lies inside op i - 1's outputs (its only input is op i - 1's output),
-//  * op i writes nothing op i - 1 writes (no write-after-write between the two: op i does not wait for op i - 1's
-//    stores to be acknowledged, only for its mailbox).
-// Op i + 1 then waits for op i - 1's flags together with op i's. The mailboxes live in the chain state after the
-// flags, 2 words per producer row; returns the words they take and sets mb_out / mb_in (word offsets, -1: none).
+// Mailbox hand-offs of a pipelined M = 1 chain. Op i takes its x from op i - 1's mailbox (one 64-bit word per output
+// element of op i - 1, at the element's float offset from op i - 1's Y: run tag << 32 | the value's bits) when
+//  * op i's prologue is raw or rms and its x, [rowB, rowB + K) of X, lies inside one split of op i - 1's store or geglu
+//    output (op i - 1's element f = split * ldy + n, n < N);
+//  * op i reads nothing else that an op of the chain writes (rms: the rstd slot and the norm weights), and op i and op
+//    i - 1 write nothing in common.
+// Completion needs no flags around it: each workgroup runs the ops in order and waits for its own stores of an op
+// before it moves on, so once every element of op i - 1 is in its mailbox, every workgroup that had a unit in op i - 1
+// is done with every op up to i - 1, and (by the same argument one op earlier) so is every other workgroup with every
+// op before i - 1. So a run of mailbox hand-offs needs no flag wait at all; an op that waits for flags instead still
+// sees every earlier op complete in the flags of op i - 1.
 static size_t plan_mailboxes(std::vector<GemvP>& ops, std::vector<int64_t>& mb_out, std::vector<int64_t>& mb_in) {
   const size_t n = ops.size();
   mb_out.assign(n, -1);
   mb_in.assign(n, -1);
+  std::vector<std::vector<Span>> rd(n), wr(n);
+  for (size_t i = 0; i < n; ++i) op_spans(ops[i], 1, rd[i], wr[i]);
+  auto meet = [](const std::vector<Span>& x, const std::vector<Span>& y) {
+    for (const Span& a : x)
+      for (const Span& b : y)
+        if (a.a < b.b && b.a < a.b) return true;
+    return false;
+  };
   size_t words = 0;
   for (size_t i = 1; i < n; ++i) {
     const GemvP& pr = ops[i - 1];
     GemvP& c = ops[i];
-    if (mb_in[i - 1] >= 0 || pr.nsplit != 1 || (pr.epi != P0_EPI_STORE && pr.epi != P0_EPI_GEGLU)) continue;
-    if (c.pro != P0_PRO_RAW) continue;
+    if (pr.epi != P0_EPI_STORE && pr.epi != P0_EPI_GEGLU) continue;
+    if (c.pro != P0_PRO_RAW && c.pro != P0_PRO_RMS) continue;
     const intptr_t d = (intptr_t)(const void*)(c.X + c.rowB) - (intptr_t)(const void*)pr.Y;
-    if (d < 0 || d % 4 || d / 4 + c.K > pr.N) continue;
-    std::vector<Span> rp, wp, rc, wc;
-    op_spans(pr, 1, rp, wp);
-    op_spans(c, 1, rc, wc);
-    bool waw = false;
-    for (const Span& a : wc)
-      for (const Span& b2 : wp) waw = waw || (a.a < b2.b && b2.a < a.b);
-    if (waw) continue;
+    if (d < 0 || d % 4) continue;
+    const int64_t f = d / 4, ld = pr.nsplit > 1 ? pr.ldy : (int64_t)pr.N;
+    const int64_t sp = f / ld, r = f % ld;
+    if (sp >= pr.nsplit || r + c.K > pr.N) continue;
+    if (c.pro == P0_PRO_RMS) {   // the rstd slot and the norm weights: inputs of the chain, not written by its ops
+      std::vector<Span> extra{rd[i].begin() + 1, rd[i].end()};
+      bool written = false;
+      for (size_t j = 0; j < n && !written; ++j) written = meet(extra, wr[j]);
+      if (written) continue;
+    }
+    if (meet(wr[i], wr[i - 1])) continue;
     if (mb_out[i - 1] < 0) {
       mb_out[i - 1] = (int64_t)words;
-      words += 2 * (size_t)pr.N;
+      words += 2 * (size_t)((pr.nsplit - 1) * ld + pr.N);
     }
-    mb_in[i] = mb_out[i - 1] + 2 * (d / 4);
-    if (i + 1 < n) ops[i + 1].flags2 = 1;
+    mb_in[i] = mb_out[i - 1] + 2 * f;
   }
   return words;
 }

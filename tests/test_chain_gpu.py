@@ -152,7 +152,10 @@ def test_chain_matches_oracle(dev, M, gemvM, pipe_m):
     elif M > 1:
         assert info["waves_per_workgroup"] == 8
     if M == 1 and info["waves_per_workgroup"] == 12:
-        assert info["mailboxes"] == 2   # o takes qkv's output, down the geglu output (the others: flags)
+        # o takes qkv's output, gate_up (rms) o's, down the geglu output, the head (rms) the 'sum' op's; qkv and the
+        # 'sum' op (two partials per element) wait for flags. As gemvM calls, op 4 reads down's first split raw (gemvM
+        # has no 'sum' prologue), which is a mailbox hand-off too.
+        assert info["mailboxes"] == (5 if gemvM else 4)
     s.reset_outputs()
     ch.run()
     assert not ch.status()
@@ -388,9 +391,8 @@ def test_chain_errors(dev):
 def test_chain_mailboxes_match_flags(dev):
     """Mailbox hand-offs (an op polls the previous op's tagged outputs instead of its completion flags) compute the
     same bits as the flag hand-offs, run after run: the x values an op stages are the same floats either way. Checked
-    over the mini step (two store -> raw and geglu -> raw hand-offs, one of them into a 2-split op) and over a chain of
-    layers that read and rewrite the same two buffers (every other op a mailbox consumer, the rest wait for two ops'
-    flags)."""
+    over the mini step (store -> raw, store -> rms, geglu -> raw into a 2-split op, and rms into the softcap head) and
+    over a chain of layers that read and rewrite the same two buffers (every op after the first a mailbox consumer)."""
     s = MiniStep(seed=61)
     old = capi.chain_tune(7, 1)
     try:
@@ -403,7 +405,7 @@ def test_chain_mailboxes_match_flags(dev):
     print("mailbox chain", im, "flag chain", iff, flush=True)
     if im["waves_per_workgroup"] != 12:
         pytest.skip("this device plans the general chain kernel (mailboxes are a pipelined-chain feature)")
-    assert im["mailboxes"] == 2 and iff["mailboxes"] == 0
+    assert im["mailboxes"] == 4 and iff["mailboxes"] == 0
     res = []
     for ch in (ch_f, ch_m, ch_m, ch_f, ch_m):
         s.reset_outputs()
@@ -436,7 +438,7 @@ def test_chain_mailboxes_match_flags(dev):
         ch_f = capi.chain(enqueue)
     finally:
         capi.chain_tune(7, old)
-    assert ch_m.info()["mailboxes"] == L and ch_f.info()["mailboxes"] == 0
+    assert ch_m.info()["mailboxes"] == 2 * L - 1 and ch_f.info()["mailboxes"] == 0
     outs = []
     for ch in (ch_f, ch_m, ch_m):
         a.upload(a0)
@@ -478,7 +480,8 @@ def _gemv(w, N, K, x, y, **kw):
 
 def test_chain_mailbox_cases(dev):
     """Which hand-offs take a mailbox, and that each computes what the flag hand-off computes:
-      a. op 1 reads x at an offset inside op 0's output (rows 128..383 of 384): mailbox;
+      a. op 1 reads x at an offset inside op 0's output (rows 128..383 of 384): mailbox, and so does op 2 (op 1's
+         whole output; a consumer may itself be a producer);
       b. op 3 writes into op 2's output (write after write): flags;
       c. op 5, 16 K-splits, reads op 4's output, which op 4 writes with large per-workgroup shares (one wave per
          64-row unit): mailbox;
@@ -508,7 +511,7 @@ def test_chain_mailbox_cases(dev):
     print("mailbox chain", im, flush=True)
     if im["waves_per_workgroup"] != 12:
         pytest.skip("this device plans the general chain kernel (mailboxes are a pipelined-chain feature)")
-    assert im["mailboxes"] == 2 and ch_f.info()["mailboxes"] == 0
+    assert im["mailboxes"] == 3 and ch_f.info()["mailboxes"] == 0
     outs = []
     for ch in (ch_f, ch_m, ch_m):
         for k in b:
