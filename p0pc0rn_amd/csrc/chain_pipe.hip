@@ -148,6 +148,29 @@ __device__ __forceinline__ float dot16_q8(const u32x4 q, const float* __restrict
   return da + db;
 }
 __device__ __forceinline__ float h2f_u16(const uint8_t* p) { return (float)*(const _Float16*)p; }
+// dot32 (gemv_kernels.hpp) against a group's 32 x' values held in registers: the same products in the same order
+__device__ __forceinline__ float dot32r(const u32x4 q, const float4 (&x4)[8]) {
+  const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+  float da = 0.0f, db = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float4 xa = x4[2 * w], xb = x4[2 * w + 1];
+    const uint32_t v = u[w], v8 = v >> 8;
+    const h2_t a = __builtin_bit_cast(h2_t, v & 0x000F000Fu);
+    const h2_t b = __builtin_bit_cast(h2_t, v & 0x00F000F0u);
+    const h2_t c = __builtin_bit_cast(h2_t, v8 & 0x000F000Fu);
+    const h2_t e = __builtin_bit_cast(h2_t, v8 & 0x00F000F0u);
+    da = __builtin_fmaf((float)a.x, xa.x, da);
+    db = __builtin_fmaf((float)a.y, xb.x, db);
+    da = __builtin_fmaf((float)b.x, xa.y, da);
+    db = __builtin_fmaf((float)b.y, xb.y, db);
+    da = __builtin_fmaf((float)c.x, xa.z, da);
+    db = __builtin_fmaf((float)c.y, xb.z, db);
+    da = __builtin_fmaf((float)e.x, xa.w, da);
+    db = __builtin_fmaf((float)e.y, xb.w, db);
+  }
+  return da + db;
+}
 
 // first weight row of part (unit j, block r, part pt) of a share
 __device__ __forceinline__ int share_row(const GemvP& p, const Share& s, int G, int j, int r, int pt) {
@@ -186,7 +209,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
     int q0 = 0, pend = -1;
     auto publish = [&](int q) { asm_lds_st(a_full + (q % kRing) * 4, (unsigned)q + 1); };
     for (int i = 0; i < n_ops; ++i) {
-      const GemvP& p = ops[i];
+      const GemvP& p = op_at(ops, i);
       // Touch every 64-byte line of the op's parameters: the op table would otherwise be fetched from memory (the
       // weight stream evicts it from L2 every run) by the compute waves' scalar loads, one miss after another, on the
       // chain's critical path; the loaders run ops ahead, so the lines are in the CU's scalar cache by then.
@@ -380,7 +403,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
   int q0 = 0;
   bool abandon = false;
   for (int i = 0; i < n_ops; ++i) {
-    const GemvP& p = ops[i];
+    const GemvP& p = op_at(ops, i);
     const Share s = share_of<Q8>(p, b, G);
     if (s.nu > 0) {
       // x' of the split in 32-k groups; the q4 dot products take odd k pre-scaled 1/16, the q8 ones plain x'
@@ -426,6 +449,46 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
             if (g < s.ngs) acc = __builtin_fmaf(sc, d - 128.0f * (xsum[2 * g] + xsum[2 * g + 1]), acc);
           }
           if (qq == 0) red[(rp * M * kPC + c) * 16 + rr] = acc;   // q8 chains have M = 1
+        }
+       } else if (M == 1 && s.nh == 2) {
+        // splits of 33 .. 64 groups (two slots per 16-row part): compute waves 0-3 take the first half's slot of every
+        // part, waves 4-7 the second's; lane = (group gl = 8 (c % 4) + lane / 8 of the half, rows lane % 8 and
+        // lane % 8 + 8). The lane's 32 x' values are read into registers once for the whole share, so a part costs
+        // it two code reads and two scale reads, where one pair per lane and slot would read the 32 x' values for
+        // every slot (the LDS reads of all compute waves, issued together after each barrier, set the pace of the
+        // slot phase). Odd groups take their two rows in the other order, so that the lanes of a read instruction
+        // fall into both halves of the LDS banks.
+        const int hh = c >> 2, gl = 8 * (c & 3) + (lane >> 3), r8 = lane & 7;
+        const int g = 32 * hh + gl;
+        const bool live = g < s.ngs;   // groups past the split add exact zeros (their x' and sums are staged as 0)
+        const float4* x4 = (const float4*)(xs + g * 32);
+        float4 xr[8];
+#pragma unroll
+        for (int w = 0; w < 8; ++w) xr[w] = x4[w];
+        const float xg = xsum[g];
+        const int ra = (gl & 1) ? r8 + 8 : r8, rb = ra ^ 8;
+        for (int rp = 0; rp < nrp; ++rp) {
+          const int q = q0 + rp * 2 + hh;
+          wait_slot(q);
+          const uint8_t* slot = lds + (q % kRing) * kSlotB;
+          const u32x4 qa = *(const u32x4l*)(slot + (gl * 16 + ra) * 16), qb = *(const u32x4l*)(slot + (gl * 16 + rb) * 16);
+          const uint32_t sa = *(const uint32_t*)(slot + 8192 + (gl * 16 + ra) * 4);
+          const uint32_t sb = *(const uint32_t*)(slot + 8192 + (gl * 16 + rb) * 4);
+          const float ya = __builtin_fmaf(live ? h2f_lo(sa) * 16777216.0f : 0.0f, dot32r(qa, xr),
+                                          (live ? h2f_hi(sa) : 0.0f) * xg);
+          const float yb = __builtin_fmaf(live ? h2f_lo(sb) * 16777216.0f : 0.0f, dot32r(qb, xr),
+                                          (live ? h2f_hi(sb) : 0.0f) * xg);
+          // rows r8 and r8 + 8 summed over the wave's 8 groups (lane bits 3-5)
+          float lo = (gl & 1) ? yb : ya, hi = (gl & 1) ? ya : yb;
+#pragma unroll
+          for (int off = 8; off < 64; off <<= 1) {
+            lo += __shfl_xor(lo, off, 64);
+            hi += __shfl_xor(hi, off, 64);
+          }
+          if (lane < 8) {
+            red[(rp * kPC + c) * 16 + r8] = lo;
+            red[(rp * kPC + c) * 16 + r8 + 8] = hi;
+          }
         }
        } else {
         // every compute lane takes pair tc = 16 group + row of each slot; a part's slots are its halves; x' row m

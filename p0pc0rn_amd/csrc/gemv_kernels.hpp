@@ -76,6 +76,16 @@ struct GemvP {
   int mf;             // standalone GEMV-M (M >= 2): the MFMA path (gemv_item), else the fp32 VALU path
 };
 
+// Op i of a chain's op table, read through the constant address space. The table is read-only for the whole launch,
+// so every field read at a uniform op index becomes a scalar load. Through a global pointer the compiler has to
+// assume that the chain loop's waits and atomics may write the table, and reads each field with a vector load; every
+// such load then waits behind the wave's other memory traffic (the outputs' stores, the loaders' LDS-DMA), one field
+// at a time. The index goes through readfirstlane: the op loops leave early on a timed-out wait, and the compiler may
+// then hold the loop counter in a vector register, which would make the address (and the loads) per lane again.
+__device__ __forceinline__ const GemvP& op_at(const GemvP* ops, int i) {
+  return *(const GemvP*)((const __attribute__((address_space(4))) GemvP*)ops + __builtin_amdgcn_readfirstlane(i));
+}
+
 __device__ __forceinline__ float gelu_tanh(float v) {   // engine/llm/lops.js:26
   float t = 0.7978845608028654f * (v + 0.044715f * v * v * v);
   t = fminf(15.0f, fmaxf(-15.0f, t));
@@ -916,7 +926,7 @@ __global__ __launch_bounds__(64 * W) void q4_gemv_chain_kernel(const GemvP* __re
     return s_go != 0;
   };
   for (int i = 0; i < n_ops && !abandon; ++i) {
-    const GemvP& p = ops[i];
+    const GemvP& p = op_at(ops, i);
     bool waited = i == 0;
     auto ready = [&]() -> bool {
       if (waited) return true;   // only the workgroup's first item of op i waits for op i - 1
