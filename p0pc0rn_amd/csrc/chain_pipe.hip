@@ -148,6 +148,16 @@ __device__ __forceinline__ float dot16_q8(const u32x4 q, const float* __restrict
   return da + db;
 }
 __device__ __forceinline__ float h2f_u16(const uint8_t* p) { return (float)*(const _Float16*)p; }
+// v summed over lanes l, l ^ 8, l ^ 16, l ^ 24, ... (lane bits 3-5), with VALU lane moves only: a DPP rotation by 8
+// inside each 16-lane row, then the gfx950 row and half swaps (permlane16 / permlane32), each of which hands back
+// the value and its partner's in two registers
+__device__ __forceinline__ float sum_lanes_8_16_32(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
 // dot32 (gemv_kernels.hpp) against a group's 32 x' values held in registers: the same products in the same order
 __device__ __forceinline__ float dot32r(const u32x4 q, const float4 (&x4)[8]) {
   const uint32_t u[4] = {q.x, q.y, q.z, q.w};
@@ -170,6 +180,24 @@ __device__ __forceinline__ float dot32r(const u32x4 q, const float4 (&x4)[8]) {
     db = __builtin_fmaf((float)e.y, xb.w, db);
   }
   return da + db;
+}
+
+// The parameters the epilogue and the mailbox post read, loaded at the op's start (while the workgroup waits for the
+// op's input) and pinned in registers. Read where they are used, each would be a scalar load that waits for the
+// scalar cache, and the epilogue's branches put several such waits in a row on the op's critical path.
+struct EpiP {
+  float* Y;
+  float* MX;
+  unsigned long long* mbxOut;
+  int64_t ldy, ldm;
+  float cap;
+  int epi, NT, coh;
+};
+__device__ __forceinline__ EpiP epi_of(const GemvP& p) {
+  EpiP e{p.Y, p.MX, p.mbxOut, p.ldy, p.ldm, p.cap, p.epi, p.NT, p.coh};
+  asm volatile("" : "+s"(e.Y), "+s"(e.MX), "+s"(e.mbxOut), "+s"(e.ldy), "+s"(e.ldm), "+s"(e.cap), "+s"(e.epi),
+               "+s"(e.NT), "+s"(e.coh));
+  return e;
 }
 
 // first weight row of part (unit j, block r, part pt) of a share
@@ -316,8 +344,14 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
     while (ctl_ld(lctl + L::CtlBar) < gen) __builtin_amdgcn_s_sleep(0);
     __builtin_amdgcn_s_waitcnt(0xC07F);
   };
-  auto wait_slot = [&](int q) {
-    while (ctl_ld(lctl + L::CtlFull + q % kRing) != (unsigned)q + 1) __builtin_amdgcn_s_sleep(0);
+  // false if the compute waves gave up meanwhile (a wave that stages its own x' gives up on its own, and the
+  // loaders then stop publishing)
+  auto wait_slot = [&](int q) -> bool {
+    while (ctl_ld(lctl + L::CtlFull + q % kRing) != (unsigned)q + 1) {
+      if (ctl_ld(lctl + L::CtlStop)) return false;
+      __builtin_amdgcn_s_sleep(0);
+    }
+    return true;
   };
   // the G flags at f (and at f2, when not null) hold this run's tag (wave c == 0 polls); false in every compute
   // thread if the wait gave up
@@ -393,9 +427,59 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
     cbar();
     return ctl_ld(lctl + L::CtlGo) != 0;
   };
+  // stage_mbx for the 8 groups [gw, gw + 8) of the split [g0, g1) that this compute wave computes with (the two-slot
+  // spread path): element k0 + 64 u + lane per lane, so each 32-lane half holds one group, and the x' values and group
+  // sums come out bit-identical to stage_mbx's. No other wave reads them, so the wave waits for no other before its
+  // slots. On a timeout the wave sets the stop and go words itself (the slot waits of the other waves end on the
+  // stop word), and the workgroup leaves at its next barrier.
+  auto stage_mbx_wave = [&](const GemvP& p, int g0, int g1, int gw, float odd) -> bool {
+    const bool rms = p.pro == P0_PRO_RMS;
+    const float rstd = rms ? p.ST[p.statOff] : 1.0f;
+    const int ke = g1 * 32, k0 = (g0 + gw) * 32;
+    float nw[4];
+    unsigned long long w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) nw[u] = rms ? p.NW[p.nOff + min(k0 + u * 64 + lane, ke - 1)] : 1.0f;
+    int go = spin_limit >= 0;
+    for (int spins = 0;; ++spins) {
+      bool ok = true;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        w[u] = __hip_atomic_load(P0_GLOBAL(unsigned long long, const_cast<unsigned long long*>(p.mbxIn + min(k0 + u * 64 + lane, ke - 1))),
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) ok = ok && (unsigned)(w[u] >> 32) == tag;
+      if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+      if (!go || spins >= spin_limit || (spins % 64 == 63 && ld_coh(timed_out))) {
+        go = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (!go) {
+      if (lane == 0) {
+        atomicOr(timed_out, 1u);
+        ctl_st(lctl + L::CtlStop, 1u);   // the loaders leave their waits, the other waves their slot waits
+        ctl_st(lctl + L::CtlGo, 0u);
+      }
+      return false;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int kl = (gw + 2 * u) * 32 + lane;   // offset in the split
+      const float xv = __uint_as_float((unsigned)w[u]);
+      const float v = k0 + u * 64 + lane < ke ? (rms ? xv * rstd * nw[u] : xv) : 0.0f;
+      const float gsum = sum32(v);
+      xs[kl] = (kl & 1) ? v * odd : v;
+      if ((lane & 31) == 0) xsum[kl >> 5] = gsum;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the wave's x' is in LDS before it reads it back
+    __builtin_amdgcn_wave_barrier();
+    return true;
+  };
   // this op's rows, with their values as stored, into its mailbox (after the epilogue's own stores): the element of
   // split `split`, row n sits at its offset from Y, split * ldy + n
-  auto post_mbx = [&](const GemvP& p, int split, int n, float v) {
+  auto post_mbx = [&](const EpiP& p, int split, int n, float v) {
     __hip_atomic_store(P0_GLOBAL(unsigned long long, p.mbxOut + (int64_t)split * p.ldy + n),
                        ((unsigned long long)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
@@ -406,12 +490,18 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
     const GemvP& p = op_at(ops, i);
     const Share s = share_of<Q8>(p, b, G);
     if (s.nu > 0) {
+      const EpiP e = epi_of(p);
       // x' of the split in 32-k groups; the q4 dot products take odd k pre-scaled 1/16, the q8 ones plain x'
       const bool q8 = Q8 && p.enc == P0_ENC_Q8G64S_T64;
       const int xg0 = q8 ? 2 * s.gA : s.gA, xg1 = q8 ? 2 * (s.gA + s.ngs) : s.gA + s.ngs;
       const int xgps = q8 ? 16 * s.nh : 32 * s.nh;
       const float odd = q8 ? 1.0f : 0.0625f;
-      if (p.mbxIn) {
+      // the two-slot q4 spread path stages per wave (see stage_mbx_wave)
+      const bool wave_stage = M == 1 && !q8 && s.spread && s.nh == 2 && p.mbxIn;
+      bool wgo = true;
+      if (wave_stage) {
+        wgo = stage_mbx_wave(p, xg0, xg1, 32 * (c >> 2) + 8 * (c & 3), odd);
+      } else if (p.mbxIn) {
         // op i - 1's completion is not waited for here: its mailbox says its outputs are all written, and with them
         // that every earlier op is complete (the planner's argument, gemv.hip plan_mailboxes)
         if (!stage_mbx(p, xg0, xg1, xgps, odd)) {
@@ -467,9 +557,9 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
         for (int w = 0; w < 8; ++w) xr[w] = x4[w];
         const float xg = xsum[g];
         const int ra = (gl & 1) ? r8 + 8 : r8, rb = ra ^ 8;
-        for (int rp = 0; rp < nrp; ++rp) {
+        for (int rp = 0; wgo && rp < nrp; ++rp) {
           const int q = q0 + rp * 2 + hh;
-          wait_slot(q);
+          if (!wait_slot(q)) break;
           const uint8_t* slot = lds + (q % kRing) * kSlotB;
           const u32x4 qa = *(const u32x4l*)(slot + (gl * 16 + ra) * 16), qb = *(const u32x4l*)(slot + (gl * 16 + rb) * 16);
           const uint32_t sa = *(const uint32_t*)(slot + 8192 + (gl * 16 + ra) * 4);
@@ -479,12 +569,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
           const float yb = __builtin_fmaf(live ? h2f_lo(sb) * 16777216.0f : 0.0f, dot32r(qb, xr),
                                           (live ? h2f_hi(sb) : 0.0f) * xg);
           // rows r8 and r8 + 8 summed over the wave's 8 groups (lane bits 3-5)
-          float lo = (gl & 1) ? yb : ya, hi = (gl & 1) ? ya : yb;
-#pragma unroll
-          for (int off = 8; off < 64; off <<= 1) {
-            lo += __shfl_xor(lo, off, 64);
-            hi += __shfl_xor(hi, off, 64);
-          }
+          const float lo = sum_lanes_8_16_32((gl & 1) ? yb : ya), hi = sum_lanes_8_16_32((gl & 1) ? ya : yb);
           if (lane < 8) {
             red[(rp * kPC + c) * 16 + r8] = lo;
             red[(rp * kPC + c) * 16 + r8 + 8] = hi;
@@ -524,6 +609,10 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
         }
        }
         cbar();   // every slot of the share is read, every wave's row sums are in
+        if (wave_stage && !ctl_ld(lctl + L::CtlGo)) {   // a wave's input wait gave up
+          abandon = true;
+          break;
+        }
         if (tc < s.nslot) ctl_add(lctl + L::CtlRel + (q0 + tc) % kRing, 1u);
         // epilogue: compute thread t -> row t of the share (a softcap unit is one whole wave)
         const int rows = s.nu * s.nrb * kStageRows;
@@ -542,9 +631,9 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
               for (int w = 0; w < kPC; ++w) v1 += red[(((rpg + 1) * M + m) * kPC + w) * 16 + r16];
             }
             if (tc < rows) {
-              const float yv = (p.coh & 2) ? epilogue<true>(p, s.split, m, n >> 6, n & 63, v0, v1)
-                                           : epilogue<false>(p, s.split, m, n >> 6, n & 63, v0, v1);
-              if (M == 1 && p.mbxOut) post_mbx(p, s.split, n, yv);
+              const float yv = (e.coh & 2) ? epilogue<true>(e, s.split, m, n >> 6, n & 63, v0, v1)
+                                           : epilogue<false>(e, s.split, m, n >> 6, n & 63, v0, v1);
+              if (M == 1 && e.mbxOut) post_mbx(e, s.split, n, yv);
             }
           }
         }
@@ -626,10 +715,10 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
           for (int m = 0; m < M; ++m) {
             const float v0 = wred[m * 128 + min(lane, rows - 1)];
             const float v1 = s.parts == 2 ? wred[m * 128 + 64 + min(lane, rows - 1)] : 0.0f;
-            if (lane < rows || p.epi == P0_EPI_SOFTCAP) {
-              const float yv = (p.coh & 2) ? epilogue<true>(p, s.split, m, n >> 6, n & 63, v0, v1)
-                                           : epilogue<false>(p, s.split, m, n >> 6, n & 63, v0, v1);
-              if (M == 1 && p.mbxOut && lane < rows) post_mbx(p, s.split, n, yv);
+            if (lane < rows || e.epi == P0_EPI_SOFTCAP) {
+              const float yv = (e.coh & 2) ? epilogue<true>(e, s.split, m, n >> 6, n & 63, v0, v1)
+                                           : epilogue<false>(e, s.split, m, n >> 6, n & 63, v0, v1);
+              if (M == 1 && e.mbxOut && lane < rows) post_mbx(e, s.split, n, yv);
             }
           }
           __builtin_amdgcn_s_waitcnt(0xC07F);

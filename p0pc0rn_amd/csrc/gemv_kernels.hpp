@@ -364,9 +364,9 @@ __device__ __forceinline__ void wave_argmax(float& v, int& r) {
 }
 
 // the epilogue of one wave for x row m: tot0 = row sums of tile0 (gate tile for a geglu), tot1 = the up tile's;
-// returns the value stored at row n of y
-template <bool COH>
-__device__ __forceinline__ float epilogue(const GemvP& p, int split, int m, int tile0, int lane, float tot0, float tot1) {
+// returns the value stored at row n of y. P: GemvP, or any type with its epi, Y, ldy, ldm, cap, MX and NT members
+template <bool COH, class P = GemvP>
+__device__ __forceinline__ float epilogue(const P& p, int split, int m, int tile0, int lane, float tot0, float tot1) {
   const int n = tile0 * 64 + lane;
   if (p.epi == P0_EPI_STORE) {
     stf<COH>(&p.Y[split * p.ldy + m * p.ldm + n], tot0);
