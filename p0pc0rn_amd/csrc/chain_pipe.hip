@@ -491,6 +491,19 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
     const Share s = share_of<Q8>(p, b, G);
     if (s.nu > 0) {
       const EpiP e = epi_of(p);
+      // a spread share's epilogue: compute thread t -> row t of the share (a softcap unit is one whole wave). Its row
+      // indices take integer divisions by per-op values; worked out here, before the input wait, and pinned, they
+      // stay off the op's critical path.
+      const int erows = s.nu * s.nrb * kStageRows;
+      int erpg = 0, er16 = 0, en = 0;
+      if (s.spread) {
+        const int t = min(tc, erows - 1);
+        const int j = t / (s.nrb * kStageRows), rr = t - j * (s.nrb * kStageRows);
+        erpg = (j * s.nrb + rr / kStageRows) * s.parts;
+        er16 = rr & 15;
+        en = share_row(p, s, G, j, 0, 0) + rr;
+        asm volatile("" : "+v"(erpg), "+v"(er16), "+v"(en));
+      }
       // x' of the split in 32-k groups; the q4 dot products take odd k pre-scaled 1/16, the q8 ones plain x'
       const bool q8 = Q8 && p.enc == P0_ENC_Q8G64S_T64;
       const int xg0 = q8 ? 2 * s.gA : s.gA, xg1 = q8 ? 2 * (s.gA + s.ngs) : s.gA + s.ngs;
@@ -614,13 +627,9 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
           break;
         }
         if (tc < s.nslot) ctl_add(lctl + L::CtlRel + (q0 + tc) % kRing, 1u);
-        // epilogue: compute thread t -> row t of the share (a softcap unit is one whole wave)
-        const int rows = s.nu * s.nrb * kStageRows;
+        // epilogue (rows and indices from the op's start)
+        const int rows = erows, rpg = erpg, r16 = er16, n = en;
         if (tc - lane < rows) {
-          const int t = min(tc, rows - 1);
-          const int j = t / (s.nrb * kStageRows), rr = t - j * (s.nrb * kStageRows);
-          const int rpg = (j * s.nrb + rr / kStageRows) * s.parts, r16 = rr & 15;
-          const int n = share_row(p, s, G, j, 0, 0) + rr;
 #pragma unroll
           for (int m = 0; m < M; ++m) {
             float v0 = 0.0f, v1 = 0.0f;
