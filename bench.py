@@ -48,26 +48,36 @@ class Step:
         self.c = capi
         c = capi
         self.layers = []
+        # Bounded activations. The weight scales keep each op's output at its input's magnitude (codes q - 8 have mean
+        # square 21.5; the down projection makes up for the geglu's ~0.65), and the norm weights alternate in sign, so
+        # that the codes' mean of -0.5 s does not pile up a common-mode component op after op. The rstd slots are
+        # fixed inputs (the model's RMSNorm sits outside the step), so the geglu's square makes the magnitude shrink
+        # layer by layer from O(1) towards 0 (a fixed slot cannot hold it at 1: that balance is unstable, and rounding
+        # differences between paths would grow into inf). Values never reach inf or NaN, so an M > 1 verify pass keeps
+        # its matrix-core path (it falls back to the VALU for |x'| >= 255) and every path runs what a model's step runs.
+        sigma = {"qkv": 1 / np.sqrt(21.5 * D), "o": 1 / np.sqrt(21.5 * D), "gu": 1 / np.sqrt(21.5 * D),
+                 "down": 1.55 / np.sqrt(21.5 * MLP)}
         for l in range(LAYERS):
             t = {}
             for name, (n, k) in (("qkv", (QKV, D)), ("o", (D, D)), ("gu", (2 * MLP, D)), ("down", (D, MLP))):
                 b = c.Buffer(n // 64 * k // 32 * 1280)
-                c.fill_q4_sym(b, n, k, seed * 7919 + l * 16 + len(t), 0.02)
+                c.fill_q4_sym(b, n, k, seed * 7919 + l * 16 + len(t), float(sigma[name]))
                 t[name] = (b, n, k)
             self.layers.append(t)
         self.head = c.Buffer(VOCAB // 64 * D // 32 * 1280)
         c.fill_q4_sym(self.head, VOCAB, D, seed * 7919 + 999, 0.02)
         self.weight_bytes = sum(b.nbytes for t in self.layers for (b, n, k) in t.values()) + self.head.nbytes
-        self.nw = c.to_device(np.linspace(0.8, 1.2, D).astype(np.float32))
+        self.nw = c.to_device((np.linspace(0.8, 1.2, D) * (1 - 2 * (np.arange(D) % 2))).astype(np.float32))
         self.M = 0
 
     def alloc(self, M):
-        """activation buffers for M rows (fp16-valued N(0,1) inputs, rstd slots)"""
+        """activation buffers for M rows (fp16-valued N(0,1) inputs), and the rstd slots"""
         c = self.c
         self.M = M
         self.x = c.Buffer(M * D * 4)
         c.fill_randn(self.x, M * D, 12345)
-        st = np.zeros(2 * M + 4, np.float32)
+        # rstd slots: a (pad, rstd) pair per row for each of the 2 per layer rms ops (qkv, gate_up), all 1 / sqrt(1 + eps)
+        st = np.zeros(2 * M * 2 * LAYERS + 4, np.float32)
         st[1::2] = 1.0 / np.sqrt(1.0 + 1e-6)
         self.st = c.to_device(st)
         self.qkvp = c.Buffer(M * QKV * 4)
@@ -79,6 +89,10 @@ class Step:
         mx[M * (VOCAB // 64) * 2 + 1::2] = 1.0
         self.mx = c.to_device(mx)
         self.mx_stat_off = M * (VOCAB // 64) * 2 + 1
+
+    def rms_off(self, j):
+        """stat_off of rms op j (qkv of layer l: j = 2 l, gate_up: 2 l + 1)"""
+        return 2 * self.M * j + 1
 
     def free_acts(self):
         for b in (self.x, self.st, self.qkvp, self.obuf, self.mbuf, self.dpart, self.logits, self.mx):
@@ -101,24 +115,29 @@ class Step:
         o the q rows of qkv, gate_up o's output, down gate_up's, the next layer's qkv (and the head) the first K-split
         partial of down. In the model a norm sits between some of them (normadd / rowstats, not GEMVs, not part of
         the step); their rstd slots are fixed inputs here."""
-        for li, t in enumerate(self.layers):
-            xin = self.x if li == 0 else self.dpart
-            if only in (None, "qkv"):
-                b, n, k = t["qkv"]
-                self.proj(b, n, k, xin, self.qkvp, "rms", stat=self.st, stat_off=1)
-            if only in (None, "o"):
-                b, n, k = t["o"]
-                self.proj(b, n, k, self.qkvp, self.obuf, "raw", kPer=2048, ldx=QKV)
-            if only in (None, "gu"):
-                b, n, k = t["gu"]
-                self.proj(b, n, k, self.obuf, self.mbuf, "rms", "geglu", stat=self.st, stat_off=1)
-            if only in (None, "down"):
-                b, n, k = t["down"]
-                self.proj(b, n, k, self.mbuf, self.dpart, "raw", kPer=2048)
+        for li in range(LAYERS):
+            self.ops_layer(li, ("qkv", "o", "gu", "down") if only is None else (only,))
         if only in (None, "head"):
             # the head's rms slot lives in the mx buffer past the tile maxima (engine/llm/gemma4.js:505-508)
             self.proj(self.head, VOCAB, D, self.dpart, self.logits, "rms", "softcap", stat=self.mx,
                       stat_off=self.mx_stat_off, mx=self.mx)
+
+    def ops_layer(self, li, kinds):
+        """enqueue the projections `kinds` of layer li"""
+        t = self.layers[li]
+        if "qkv" in kinds:
+            b, n, k = t["qkv"]
+            self.proj(b, n, k, self.x if li == 0 else self.dpart, self.qkvp, "rms", stat=self.st,
+                      stat_off=self.rms_off(2 * li))
+        if "o" in kinds:
+            b, n, k = t["o"]
+            self.proj(b, n, k, self.qkvp, self.obuf, "raw", kPer=2048, ldx=QKV)
+        if "gu" in kinds:
+            b, n, k = t["gu"]
+            self.proj(b, n, k, self.obuf, self.mbuf, "rms", "geglu", stat=self.st, stat_off=self.rms_off(2 * li + 1))
+        if "down" in kinds:
+            b, n, k = t["down"]
+            self.proj(b, n, k, self.mbuf, self.dpart, "raw", kPer=2048)
 
     def step_bytes(self, only=None):
         M = self.M

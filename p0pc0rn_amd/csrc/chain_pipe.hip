@@ -41,14 +41,17 @@ template <int M>
 struct PipeL {
   static constexpr int KL = M == 1 ? 3072 : 2048;                   // largest split
   static constexpr int RedRp = M == 1 ? 16 : 4;                     // spread shares: most 16-row parts per workgroup
-  static constexpr int Ring = M <= 2 ? 12 : M == 3 ? 11 : M == 4 ? 10 : 8;   // slots in the ring
-  static constexpr int OffXs = Ring * kSlotB;                       // x' [M][split] (odd k scaled 1/16 for q4)
-  static constexpr int OffXsum = OffXs + M * KL * 4;                // group sums [M][split / 32]
-  static constexpr int OffRed = OffXsum + M * (KL / 32) * 4;        // spread: [part][m][compute wave][16 rows]
+  static constexpr int Ring = M <= 2 ? 12 : M == 3 ? 11 : M == 4 ? 9 : 8;   // slots in the ring
+  // x' [M][split] (odd k scaled 1/16 for q4); for M > 1 on the matrix cores, the same bytes hold the fp16 hi / lo A
+  // operands (stage_x_mf's layout)
+  static constexpr int OffXs = Ring * kSlotB;
+  // group sums [M][split / 32]; M > 1 on the matrix cores: [split / 32][16]
+  static constexpr int OffXsum = OffXs + M * KL * 4;
+  static constexpr int OffRed = OffXsum + (M == 1 ? 1 : 16) * (KL / 32) * 4;   // spread: [part][m][compute wave][16 rows]
   static constexpr int OffWred = OffRed + RedRp * M * kPC * 16 * 4; // per wave: [compute wave][m][2][64 rows]
   static constexpr int OffCtl = OffWred + kPC * M * 2 * 64 * 4;     // control words
   static constexpr int CtlFull = 0, CtlRel = Ring, CtlBar = 2 * Ring, CtlStop = 2 * Ring + 1, CtlGo = 2 * Ring + 2,
-                       CtlTag = 2 * Ring + 3, CtlWords = 2 * Ring + 4;
+                       CtlTag = 2 * Ring + 3, CtlBad = 2 * Ring + 4, CtlWords = 2 * Ring + 5;
   static constexpr int Lds = OffCtl + CtlWords * 4;
   static_assert(Lds <= 160 * 1024 - 256, "pipelined chain LDS");
 };
@@ -203,6 +206,65 @@ __device__ __forceinline__ EpiP epi_of(const GemvP& p) {
 // first weight row of part (unit j, block r, part pt) of a share
 __device__ __forceinline__ int share_row(const GemvP& p, const Share& s, int G, int j, int r, int pt) {
   return ((s.first + j * G) / p.nsplit * s.nrb + r) * kStageRows + (pt ? p.N : 0);
+}
+
+// x' of an M > 1 op's split (raw or rms prologue), every row in one batch of loads. Thread t of the NT compute threads
+// takes k = kb + j NT + t for j < KL / NT and every row m: its norm weights are loaded once for all rows, the rows' rstd
+// slots once per row, and all of its loads are in flight together (stage_x's batches of U elements each wait for a
+// memory round trip, three of them per op at M = 5). The values are prologue_batch's and the group sums sum32's. MF:
+// stage_x_mf's fp16 hi / lo A operands and [group][16] sums (rows >= M zero), and the result is its "too large" flag;
+// else stage_x's fp32 layout (result false).
+template <int M, bool COH, bool MF>
+__device__ __forceinline__ bool stage_rows(const GemvP& p, int g0, int g1, int gps, float* xs, float* xsum, int t) {
+  constexpr int NT = 64 * kPC, J = 2048 / NT;   // splits of M > 1 ops hold at most 2048 k
+  const int lane = t & 63;
+  const int KL = gps * 32, kb = g0 * 32, ke = g1 * 32, nj = KL / NT;
+  const bool rms = p.pro == P0_PRO_RMS;
+  float x[J][M], nw[J], st[M];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    nw[j] = 1.0f;
+    if (j < nj) {
+      const int k = min(kb + j * NT + t, ke - 1);
+#pragma unroll
+      for (int m = 0; m < M; ++m) x[j][m] = ldf<COH>(&p.X[m * p.ldx + p.rowB + k]);
+      if (rms) nw[j] = ldf<COH>(&p.NW[p.nOff + k]);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m) st[m] = rms ? ldf<COH>(&p.ST[p.statOff + m * p.statLd]) : 1.0f;
+  bool bad = false;
+  _Float16* xh = (_Float16*)xs;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    if (j >= nj) break;
+    const int kl = j * NT + t, g = kl >> 5, kk = kl & 31;
+    const bool in = kb + kl < ke;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float v = in ? (rms ? x[j][m] * st[m] * nw[j] : x[j][m]) : 0.0f;
+      const float gs = sum32(v);
+      const float xo = (kl & 1) ? v * 0.0625f : v;
+      if (MF) {
+        const int w = kk >> 3, jj = kk & 7;
+        const float xs8 = xo * kMfScale;
+        const _Float16 hi = (_Float16)xs8;
+        const _Float16 lo = (_Float16)(xs8 - (float)hi);
+        const int at = (((g * 4 + w) * 2) * M + m) * 8 + (((jj & 3) << 1) | (jj >> 2));
+        xh[at] = hi;
+        xh[at + M * 8] = lo;
+        bad = bad || !(__builtin_fabsf(xo) < kMfBig);
+        if ((lane & 31) == 0) xsum[g * 16 + m] = gs;
+      } else {
+        xs[m * KL + kl] = xo;
+        if ((lane & 31) == 0) xsum[m * gps + g] = gs;
+      }
+    }
+    if (MF && (lane & 31) == 0)
+#pragma unroll
+      for (int m = M; m < 16; ++m) xsum[g * 16 + m] = 0.0f;
+  }
+  return bad;
 }
 
 // Q8: the instantiation for chains that hold q8g64s.t64 ops (the q4-only one carries none of their code)
@@ -509,6 +571,8 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
       const int xg0 = q8 ? 2 * s.gA : s.gA, xg1 = q8 ? 2 * (s.gA + s.ngs) : s.gA + s.ngs;
       const int xgps = q8 ? 16 * s.nh : 32 * s.nh;
       const float odd = q8 ? 1.0f : 0.0625f;
+      // M > 1 (q4, no mailboxes at M > 1), spread shares: the slots' arithmetic on the matrix cores
+      bool mf = M >= 2 && !q8 && s.spread;
       // the two-slot q4 spread path stages per wave (see stage_mbx_wave)
       const bool wave_stage = M == 1 && !q8 && s.spread && s.nh == 2 && p.mbxIn;
       bool wgo = true;
@@ -527,9 +591,30 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
           break;
         }
         // op i - 1's outputs are read with coherent loads: no L2 invalidate
-        if (p.coh & 1) stage_x<M, true>(p, xg0, xg1, xgps, xs, xsum, tc, 64 * kPC, odd);
-        else stage_x<M, false>(p, xg0, xg1, xgps, xs, xsum, tc, 64 * kPC, odd);
-        cbar();
+        const bool rows1 = M >= 2 && !q8 && (p.pro == P0_PRO_RAW || p.pro == P0_PRO_RMS);   // stage_rows
+        if (mf) {
+          // M > 1: x' as the matrix cores' fp16 hi / lo operands; a workgroup that holds an x' too large for them
+          // (|x'| >= 255, see stage_x_mf) stages fp32 x' instead and runs this op on the VALU
+          bool bad;
+          if (rows1) bad = (p.coh & 1) ? stage_rows<M, true, true>(p, xg0, xg1, xgps, xs, xsum, tc)
+                                       : stage_rows<M, false, true>(p, xg0, xg1, xgps, xs, xsum, tc);
+          else bad = (p.coh & 1) ? stage_x_mf<M, true, 16>(p, xg0, xg1, xgps, (_Float16*)xs, xsum, tc, 64 * kPC)
+                                 : stage_x_mf<M, false, 16>(p, xg0, xg1, xgps, (_Float16*)xs, xsum, tc, 64 * kPC);
+          if (bad) ctl_st(lctl + L::CtlBad, (unsigned)i + 1);
+          cbar();
+          mf = ctl_ld(lctl + L::CtlBad) != (unsigned)i + 1;
+        }
+        if (!mf) {
+          if (rows1) {
+            if (p.coh & 1) stage_rows<M, true, false>(p, xg0, xg1, xgps, xs, xsum, tc);
+            else stage_rows<M, false, false>(p, xg0, xg1, xgps, xs, xsum, tc);
+          } else if (p.coh & 1) {
+            stage_x<M, true>(p, xg0, xg1, xgps, xs, xsum, tc, 64 * kPC, odd);
+          } else {
+            stage_x<M, false>(p, xg0, xg1, xgps, xs, xsum, tc, 64 * kPC, odd);
+          }
+          cbar();
+        }
       }
       const int nrp = s.nu * s.nrb * s.parts;
       if (s.spread) {
@@ -552,6 +637,42 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
             if (g < s.ngs) acc = __builtin_fmaf(sc, d - 128.0f * (xsum[2 * g] + xsum[2 * g + 1]), acc);
           }
           if (qq == 0) red[(rp * M * kPC + c) * 16 + rr] = acc;   // q8 chains have M = 1
+        }
+       } else if (M >= 2 && mf) {
+        // M > 1 on the matrix cores: compute wave c takes groups 4c .. 4c + 3 of every slot. Per group and the slot's
+        // 16 weight rows, two v_mfma_f32_16x16x32_f16 (x' hi and lo as A, the codes as B: gemv_kernels.hpp's GEMV-M
+        // operands) give D[m][n]: x row m in lanes l / 16 == m / 4 (element m % 4), weight row n = l % 16, to which
+        // each lane applies its row's scale and min.
+        const _Float16* xh = (const _Float16*)xs;
+        const int aw = lane >> 4, arow = min(lane & 15, M - 1), n16 = lane & 15;
+        const bool arow_live = (lane & 15) < M;
+        const half8_t hz = {};
+        for (int rp = 0; rp < nrp; ++rp) {
+          f4_t am = {0.0f, 0.0f, 0.0f, 0.0f};
+          for (int h = 0; h < s.nh; ++h) {
+            const int q = q0 + rp * s.nh + h;
+            wait_slot(q);
+            const uint8_t* slot = lds + (q % kRing) * kSlotB;
+#pragma unroll
+            for (int jg = 0; jg < 4; ++jg) {
+              const int gs = 4 * c + jg, g = 32 * h + gs;   // group of the slot, of the split
+              const uint32_t cw = *(const uint32_t*)(slot + (gs * 16 + n16) * 16 + aw * 4);
+              const uint32_t sm = *(const uint32_t*)(slot + 8192 + (gs * 16 + n16) * 4);
+              const half8_t* ap = (const half8_t*)(xh + (((g * 4 + aw) * 2) * M + arow) * 8);
+              const half8_t ahi = arow_live ? ap[0] : hz, alo = arow_live ? ap[M] : hz;
+              const f4_t sx = *(const f4_t*)(xsum + g * 16 + 4 * aw);
+              const half8_t bq = codes_b(cw);
+              f4_t d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+              d = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bq, d, 0, 0, 0);
+              const bool live = g < s.ngs;
+              const float s8 = live ? h2f_lo(sm) * (1.0f / kMfScale) : 0.0f, mn = live ? h2f_hi(sm) : 0.0f;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) am[e] = __builtin_fmaf(s8, d[e], __builtin_fmaf(mn, sx[e], am[e]));
+            }
+          }
+#pragma unroll
+          for (int m = 0; m < M; ++m)
+            if ((lane >> 4) == (m >> 2)) red[((rp * M + m) * kPC + c) * 16 + n16] = am[m & 3];
         }
        } else if (M == 1 && s.nh == 2) {
         // splits of 33 .. 64 groups (two slots per 16-row part): compute waves 0-3 take the first half's slot of every
