@@ -571,8 +571,8 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
       const int xg0 = q8 ? 2 * s.gA : s.gA, xg1 = q8 ? 2 * (s.gA + s.ngs) : s.gA + s.ngs;
       const int xgps = q8 ? 16 * s.nh : 32 * s.nh;
       const float odd = q8 ? 1.0f : 0.0625f;
-      // M > 1 (q4, no mailboxes at M > 1), spread shares: the slots' arithmetic on the matrix cores
-      bool mf = M >= 2 && !q8 && s.spread;
+      // M > 1 (q4, no mailboxes at M > 1): the slots' arithmetic on the matrix cores
+      bool mf = M >= 2 && !q8;
       // the two-slot q4 spread path stages per wave (see stage_mbx_wave)
       const bool wave_stage = M == 1 && !q8 && s.spread && s.nh == 2 && p.mbxIn;
       bool wgo = true;
@@ -777,10 +777,49 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
               float acc[M];
 #pragma unroll
               for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+              f4_t am = {0.0f, 0.0f, 0.0f, 0.0f};   // M > 1 on the matrix cores (D layout of the spread path)
               for (int h = 0; h < s.nh; ++h) {
                 const int q = q0 + slot_index(s, j, (r * s.parts + pt) * s.nh + h);
                 wait_slot(q);
                 const uint8_t* slot = lds + (q % kRing) * kSlotB;
+                if (M >= 2 && mf) {
+                  // the slot's 32 groups in 4 batches of 8 (each group: two v_mfma_f32_16x16x32_f16, as in the spread
+                  // path); a batch's code and scale words go to registers first, and the slot goes back to the
+                  // loaders once the last batch is read
+                  const _Float16* xh = (const _Float16*)xs;
+                  const int aw = lane >> 4, arow = min(lane & 15, M - 1), n16 = lane & 15;
+                  const bool arow_live = (lane & 15) < M;
+                  const half8_t hz = {};
+#pragma unroll 1
+                  for (int b8 = 0; b8 < 4; ++b8) {
+                    uint32_t cw[8], smw[8];
+#pragma unroll
+                    for (int gg = 0; gg < 8; ++gg) {
+                      const int gs = 8 * b8 + gg;
+                      cw[gg] = *(const uint32_t*)(slot + (gs * 16 + n16) * 16 + aw * 4);
+                      smw[gg] = *(const uint32_t*)(slot + 8192 + (gs * 16 + n16) * 4);
+                    }
+                    if (b8 == 3) {
+                      __builtin_amdgcn_s_waitcnt(0xC07F);   // this wave's reads of the slot are done
+                      if (lane == 0) ctl_add(lctl + L::CtlRel + q % kRing, 1u);
+                    }
+#pragma unroll
+                    for (int gg = 0; gg < 8; ++gg) {
+                      const int g = 32 * h + 8 * b8 + gg;
+                      const half8_t* ap = (const half8_t*)(xh + (((g * 4 + aw) * 2) * M + arow) * 8);
+                      const half8_t ahi = arow_live ? ap[0] : hz, alo = arow_live ? ap[M] : hz;
+                      const f4_t sx = *(const f4_t*)(xsum + g * 16 + 4 * aw);
+                      const half8_t bq = codes_b(cw[gg]);
+                      f4_t d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                      d = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bq, d, 0, 0, 0);
+                      const bool live = g < s.ngs;
+                      const float s8 = live ? h2f_lo(smw[gg]) * (1.0f / kMfScale) : 0.0f, mn = live ? h2f_hi(smw[gg]) : 0.0f;
+#pragma unroll
+                      for (int e = 0; e < 4; ++e) am[e] = __builtin_fmaf(s8, d[e], __builtin_fmaf(mn, sx[e], am[e]));
+                    }
+                  }
+                  continue;
+                }
                 if (q8) {   // lane = (row lane / 4, quarter lane % 4) of each of the slot's 8 groups
                   const int rr = lane >> 2, qq = lane & 3;
                   u32x4 qv[8];
@@ -826,6 +865,12 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
               }
               if (q8) {
                 if ((lane & 3) == 0) wred[pt * 64 + r * 16 + (lane >> 2)] = acc[0];   // q8 chains have M = 1
+                continue;
+              }
+              if (M >= 2 && mf) {   // D[m][n] -> wred: x row m in lanes l / 16 == m / 4, weight row n = l % 16
+#pragma unroll
+                for (int m = 0; m < M; ++m)
+                  if ((lane >> 4) == (m >> 2)) wred[(m * 2 + pt) * 64 + r * 16 + (lane & 15)] = am[m & 3];
                 continue;
               }
 #pragma unroll

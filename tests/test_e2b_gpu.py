@@ -33,24 +33,31 @@ def _check(got, want, what):
 
 class E2B:
     """two decode layers + the head at bench.py's shapes, M rows; symmetric BASELINE weights filled on the device and,
-    bit-identically, on the host by the oracle's copy of the same counter hash"""
+    bit-identically, on the host by the oracle's copy of the same counter hash. bounded: bench.py's weight scales and
+    sign-alternating norm weights, which keep every activation O(1) (|x'| < 255: an M > 1 chain then runs every op on
+    the matrix cores); else sigma 0.02 everywhere, whose activations grow ~4x per op (later M > 1 ops take the VALU
+    fallback)."""
 
-    def __init__(self, M, layers=2, seed=5):
+    def __init__(self, M, layers=2, seed=5, bounded=False):
         self.M, self.L = M, layers
         shapes = {"qkv": (QKV, D), "o": (D, D), "gu": (2 * MLP, D), "dn": (D, MLP)}
+        gain = {"qkv": 1.0, "o": 1.0, "gu": 1.0, "dn": 1.55}
         self.w_host, self.w_dev = {}, {}
         for l in range(layers):
             for i, (k, (n, kk)) in enumerate(shapes.items()):
                 s = seed * 101 + l * 16 + i
-                self.w_host[(l, k)] = O.fill_q4_sym(n, kk, s, 0.02)
+                sig = float(gain[k] / np.sqrt(21.5 * kk)) if bounded else 0.02
+                self.w_host[(l, k)] = O.fill_q4_sym(n, kk, s, sig)
                 b = capi.Buffer(n // 64 * kk // 32 * 1280)
-                capi.fill_q4_sym(b, n, kk, s, 0.02)
+                capi.fill_q4_sym(b, n, kk, s, sig)
                 self.w_dev[(l, k)] = b
         self.w_host["head"] = O.fill_q4_sym(V, D, seed * 101 + 99, 0.02)
         self.w_dev["head"] = capi.Buffer(V // 64 * D // 32 * 1280)
         capi.fill_q4_sym(self.w_dev["head"], V, D, seed * 101 + 99, 0.02)
         self.x = O.fill_randn(M * D, seed)[0]
         self.nw = np.linspace(0.8, 1.2, D).astype(np.float32)
+        if bounded:
+            self.nw *= 1 - 2 * (np.arange(D) % 2)
         st = np.zeros(2 * M + 4, np.float32)
         st[1::2][:M] = 1.0 / np.sqrt(1.0 + 1e-6)
         self.st = st
@@ -136,7 +143,9 @@ class E2B:
         lg = got["head"].reshape(M, NT, 64)
         gm = gmx[:2 * NT * M:2].reshape(M, NT)
         gi = gmx[1:2 * NT * M:2].view(np.uint32).reshape(M, NT)
-        assert np.allclose(gm, mx[:2 * NT * M:2].reshape(M, NT), rtol=1e-5, atol=1e-5), what + ": tile maxima"
+        wm = mx[:2 * NT * M:2].reshape(M, NT)
+        _check(gm, wm, what + " tile maxima")   # the maxima are logits: the logits' bar
+        print(what, "tile maxima: largest |diff|", float(np.max(np.abs(gm - wm))), flush=True)
         want_i = (np.argmax(lg, axis=2) + np.arange(NT)[None, :] * 64).astype(np.uint32)
         assert np.array_equal(gi, want_i), what + ": tile argmax"
         assert np.array_equal(gm, np.take_along_axis(lg, (gi % 64).astype(np.int64)[:, :, None], 2)[:, :, 0])
@@ -179,11 +188,13 @@ def test_config_b_decode_step_as_a_recording(e2b1):
     rec.free()
 
 
+@pytest.mark.parametrize("data", ["bounded", "large"])
 @pytest.mark.parametrize("way", ["chain", "graph"])
-def test_config_c_verify_pass_m5(dev, way):
+def test_config_c_verify_pass_m5(dev, way, data):
     """config C: the verify pass (M = 1 + 4 draft tokens) at the E2B shapes, as one pipelined chain and as a
-    recording of standalone gemvM launches (which run on the matrix cores for M >= 2)"""
-    s = E2B(5, seed=6)
+    recording of standalone gemvM launches (both run on the matrix cores for M >= 2, the chain's spread shares and its
+    lm_head alike; with large activations later ops take the VALU fallback)"""
+    s = E2B(5, seed=6, bounded=data == "bounded")
     try:
         if way == "chain":
             ch = capi.chain(s.enqueue)
