@@ -435,6 +435,20 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
     cbar();
     return ctl_ld(lctl + L::CtlGo) != 0;
   };
+  // wave c == 0: the G flags at f hold this run's tag; on a timeout it sets the stop and go words (the workgroup leaves
+  // at its next barrier)
+  auto poll_flags = [&](const unsigned* f) {
+    int go = spin_limit >= 0;
+    for (int spins = 0; go && !flags_set(f, G, tag, lane); ++spins) {
+      if (spins >= spin_limit || (spins % 64 == 63 && ld_coh(timed_out))) go = 0;
+      else __builtin_amdgcn_s_sleep(1);
+    }
+    if (!go && lane == 0) {
+      atomicOr(timed_out, 1u);
+      ctl_st(lctl + L::CtlStop, 1u);
+      ctl_st(lctl + L::CtlGo, 0u);
+    }
+  };
   // x' of groups [g0, g1) from the previous op's mailbox: each compute thread polls its own elements until all of them
   // carry this run's tag (bounded like wait_flags), then writes x' and the group sums as stage_x does (raw or rms
   // prologue: for rms the rstd slot and the thread's norm weights are loaded before the poll, as they are inputs of
@@ -553,6 +567,20 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
     const Share s = share_of<Q8>(p, b, G);
     if (s.nu > 0) {
       const EpiP e = epi_of(p);
+      // GemvP::wback: op i - wback's completion flags, loaded now by wave 0 and checked before the op's first store, so
+      // that the check costs no round trip of its own when they are set by then
+      const unsigned* const wf = mine + (size_t)(i - p.wback) * Gp;
+      unsigned w2[4] = {tag, tag, tag, tag};
+      if (p.wback && c == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w2[j] = ld_coh(wf + min(j * 64 + lane, G - 1));
+      }
+      auto check_wback = [&]() {   // wave c == 0, then a barrier of the compute waves
+        bool ok = G <= 256;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ok = ok && w2[j] == tag;
+        if (__builtin_amdgcn_ballot_w64(!ok) != 0) poll_flags(wf);
+      };
       // a spread share's epilogue: compute thread t -> row t of the share (a softcap unit is one whole wave). Its row
       // indices take integer divisions by per-op values; worked out here, before the input wait, and pinned, they
       // stay off the op's critical path.
@@ -579,14 +607,14 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
       if (wave_stage) {
         wgo = stage_mbx_wave(p, xg0, xg1, 32 * (c >> 2) + 8 * (c & 3), odd);
       } else if (p.mbxIn) {
-        // op i - 1's completion is not waited for here: its mailbox says its outputs are all written, and with them
-        // that every earlier op is complete (the planner's argument, gemv.hip plan_mailboxes)
+        // op i - 1's completion is not waited for here: the mailbox words say that the elements op i reads are
+        // written; the stores of op i wait for what the other workgroups may still be doing (GemvP::wback)
         if (!stage_mbx(p, xg0, xg1, xgps, odd)) {
           abandon = true;
           break;
         }
       } else {
-        if (i > 0 && !wait_flags(mine + (size_t)(i - 1) * Gp, p.flags2 ? mine + (size_t)(i - 2) * Gp : nullptr)) {
+        if (i > 0 && !wait_flags(mine + (size_t)(i - 1) * Gp, nullptr)) {
           abandon = true;
           break;
         }
@@ -742,8 +770,10 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
           }
         }
        }
+        // outputs that an earlier op reads or writes: that op complete in every workgroup first (GemvP::wback)
+        if (p.wback && c == 0) check_wback();
         cbar();   // every slot of the share is read, every wave's row sums are in
-        if (wave_stage && !ctl_ld(lctl + L::CtlGo)) {   // a wave's input wait gave up
+        if ((wave_stage || p.wback) && !ctl_ld(lctl + L::CtlGo)) {   // an input or flag wait gave up
           abandon = true;
           break;
         }
@@ -768,6 +798,14 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
           }
         }
       } else {
+        if (p.wback) {   // as in the spread path, before the first of this share's stores
+          if (c == 0) check_wback();
+          cbar();
+          if (!ctl_ld(lctl + L::CtlGo)) {
+            abandon = true;
+            break;
+          }
+        }
         // a large share (the lm_head), one wave per unit: lane takes pairs lane + 64 kk of each slot (group
         // 4 kk + lane / 16, row lane % 16); it copies them to registers and hands the slot back to the loaders before
         // the arithmetic, so the ring's slots spend their time in flight rather than held

@@ -218,11 +218,14 @@ static void mark_coherence(std::vector<GemvP>& ops, int M) {
 //    output (op i - 1's element f = split * ldy + n, n < N);
 //  * op i reads nothing else that an op of the chain writes (rms: the rstd slot and the norm weights), and op i and op
 //    i - 1 write nothing in common.
-// Completion needs no flags around it: each workgroup runs the ops in order and waits for its own stores of an op
-// before it moves on, so once every element of op i - 1 is in its mailbox, every workgroup that had a unit in op i - 1
-// is done with every op up to i - 1, and (by the same argument one op earlier) so is every other workgroup with every
-// op before i - 1. So a run of mailbox hand-offs needs no flag wait at all; an op that waits for flags instead still
-// sees every earlier op complete in the flags of op i - 1.
+// The mailbox words op i reads say that exactly those elements of op i - 1 are written (read-after-write), and nothing
+// about the other workgroups: a workgroup that produced none of them may still be in an earlier op, reading or writing
+// a buffer that op i writes. Every workgroup publishes its completion flag of every op after its own stores of that
+// op, so op j's flags from all workgroups mean every op up to j is complete everywhere. An op whose outputs overlap
+// what an op before i - 1 reads or writes (GemvP::wback 2) therefore waits for op i - 2's flags before it writes them
+// (by then normally long set; the flags are loaded at the op's start, so the check costs no round trip of its own), and
+// one whose outputs overlap what op i - 1 reads (wback 1) for op i - 1's. An op that waits for flags at its start (no
+// mailbox) sees every earlier op complete in the flags of op i - 1.
 static size_t plan_mailboxes(std::vector<GemvP>& ops, std::vector<int64_t>& mb_out, std::vector<int64_t>& mb_in) {
   const size_t n = ops.size();
   mb_out.assign(n, -1);
@@ -258,6 +261,9 @@ static size_t plan_mailboxes(std::vector<GemvP>& ops, std::vector<int64_t>& mb_o
       words += 2 * (size_t)((pr.nsplit - 1) * ld + pr.N);
     }
     mb_in[i] = mb_out[i - 1] + 2 * f;
+    if (meet(wr[i], rd[i - 1])) c.wback = 1;
+    for (size_t j = 0; j + 1 < i && !c.wback; ++j)
+      if (meet(wr[i], rd[j]) || meet(wr[i], wr[j])) c.wback = 2;
   }
   return words;
 }

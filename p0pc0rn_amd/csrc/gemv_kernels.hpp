@@ -72,7 +72,10 @@ struct GemvP {
   // previous op's completion flags and then loading x: one memory round trip instead of two
   unsigned long long* mbxOut;       // this op's mailbox (row n at n), or null
   const unsigned long long* mbxIn;  // x[k] of this op at mbxIn[k], or null
-  int flags2;                       // 1: op i also waits for op i - 2's flags (op i - 1 took its input from a mailbox)
+  // a mailbox op (whose mailbox says only that the elements it reads are written) whose outputs overlap what an earlier
+  // op reads or writes waits for op i - wback's completion flags before it writes them: 1 if op i - 1 reads them, 2 if
+  // only ops before i - 1 do, 0 if none does
+  int wback;
   int mf;             // standalone GEMV-M (M >= 2): the MFMA path (gemv_item), else the fp32 VALU path
 };
 
@@ -176,7 +179,10 @@ __device__ __forceinline__ float sum32(float v) {
   v += dpp_f<0x4E>(v);    // quad_perm [2, 3, 0, 1]
   v += dpp_f<0x141>(v);   // row_half_mirror
   v += dpp_f<0x140>(v);   // row_mirror
-  return v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));   // lane ^ 16
+  // lane ^ 16: the gfx950 row swap hands back the value and its partner's in two registers (a VALU lane move, where a
+  // ds_swizzle would take an LDS round trip); the two sums are the same in every lane
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // x'[m][k] of the groups [g0, g1) -> LDS xs[m * 32 gps + k - 32 g0] (odd k scaled by `odd`: 1/16 for the q4 dot
