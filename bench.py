@@ -206,16 +206,16 @@ def bench_decode(c, step, steps, warmup, breakdown=True):
     return out
 
 
-def bench_verify(c, step, Ms=(1, 2, 4, 5, 8, 16)):
+def bench_verify(c, step, Ms=(1, 2, 4, 5, 8, 16), graph=True):
     res = {}
     for M in Ms:
         step.alloc(M)
         ms_chain, _ = time_chain(c, step.ops, 3, 10)
-        ms_graph = time_recording(c, step.ops, 3, 10)
+        ms_graph = time_recording(c, step.ops, 3, 10) if graph else float("inf")
         ms = min(ms_chain, ms_graph)
         res[str(M)] = {"ms_per_pass": round(ms, 4), "tok_per_s": round(M / (ms * 1e-3), 1),
                        "GBps": round(step.step_bytes() / (ms * 1e-3) / 1e9, 1),
-                       "ms_chain": round(ms_chain, 4), "ms_graph": round(ms_graph, 4)}
+                       "ms_chain": round(ms_chain, 4), "ms_graph": round(ms_graph, 4) if graph else None}
         step.free_acts()
     return res
 
@@ -339,6 +339,8 @@ def main():
     ap.add_argument("--verify-m", default="1,2,4,5,8,16",
                     help="x rows of the verify passes timed (config C); empty: none")
     ap.add_argument("--no-config-a", action="store_true", help="skip the single-GEMV ring (config A)")
+    ap.add_argument("--verify-chain-only", action="store_true",
+                    help="time the verify passes as chains only (no recorded-graph timing)")
     ap.add_argument("--no-breakdown", action="store_true",
                     help="skip the per-projection timings (short runs under PMC counters)")
     ap.add_argument("--calibrate", action="store_true",
@@ -376,7 +378,7 @@ def main():
             log("config A", extra["config_a_gemv"])
         vm = tuple(int(v) for v in args.verify_m.split(",") if v.strip())
         if vm:
-            extra["verify_sweep"] = bench_verify(c, step, vm)
+            extra["verify_sweep"] = bench_verify(c, step, vm, graph=not args.verify_chain_only)
             log("verify sweep", extra["verify_sweep"])
     for t in step.layers:
         for (b, n, k) in t.values():
