@@ -599,8 +599,8 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
       const int xg0 = q8 ? 2 * s.gA : s.gA, xg1 = q8 ? 2 * (s.gA + s.ngs) : s.gA + s.ngs;
       const int xgps = q8 ? 16 * s.nh : 32 * s.nh;
       const float odd = q8 ? 1.0f : 0.0625f;
-      // M > 1 (q4, no mailboxes at M > 1): the slots' arithmetic on the matrix cores
-      bool mf = M >= 2 && !q8;
+      // M > 1 (q4, no mailboxes at M > 1): the slots' arithmetic on the matrix cores (GemvP::mf, p0_chain_tune knob 9)
+      bool mf = M >= 2 && !q8 && p.mf;
       // the two-slot q4 spread path stages per wave (see stage_mbx_wave)
       const bool wave_stage = M == 1 && !q8 && s.spread && s.nh == 2 && p.mbxIn;
       bool wgo = true;

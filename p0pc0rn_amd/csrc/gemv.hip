@@ -41,6 +41,7 @@ static int g_two_tiles_min_nt = 1024;   // output tiles from which a wave stream
 static int g_min_gpw = 2;               // fewest q4 groups a wave streams when K is split
 static int g_max_kw = 16;               // most waves that share one tile slot's K-slice inside a workgroup
 static int g_mf_min_m = 2;              // fewest x rows a standalone GEMV-M runs on MFMA (17: never)
+static int g_pipe_mf_min_m = 4;         // fewest x rows a pipelined chain does its slot arithmetic on MFMA (6: never)
 
 struct Plan {
   int mode, gps, nks, kw, tgw, ntb, rowsTot, waves;
@@ -617,6 +618,7 @@ extern "C" int p0_chain_end(void** out) {
     P0_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, (const void*)pk, 64 * pipe_waves(), plds), "p0_chain_end");
     std::vector<GemvP> planned = cb->ops;
     if (pc >= 1 && plan_pipe(planned, ctx().cu_count, cb->M)) {
+      for (GemvP& o : planned) o.mf = cb->M >= 2 && cb->M >= g_pipe_mf_min_m;
       cb->ops = planned;
       k = pk;
       cb->W = pipe_waves();
@@ -739,6 +741,11 @@ extern "C" int p0_chain_free(void* chain) {
 // default) or the general one (0). Returns the previous value; a value < 0 only reads (knobs 3, 4, 7 and 8 also
 // take 0).
 extern "C" int p0_chain_tune(int knob, int value) {
+  if (knob == 9) {
+    const int old = g_pipe_mf_min_m;
+    if (value > 0) g_pipe_mf_min_m = value;
+    return old;
+  }
   if (knob == 7 || knob == 8) {
     int* t = knob == 7 ? &g_chain_mbx : &g_chain_pipe_m;
     const int old = *t;

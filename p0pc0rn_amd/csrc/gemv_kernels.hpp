@@ -76,7 +76,7 @@ struct GemvP {
   // op reads or writes waits for op i - wback's completion flags before it writes them: 1 if op i - 1 reads them, 2 if
   // only ops before i - 1 do, 0 if none does
   int wback;
-  int mf;             // standalone GEMV-M (M >= 2): the MFMA path (gemv_item), else the fp32 VALU path
+  int mf;             // M >= 2: the MFMA arithmetic (standalone: gemv_item; pipelined chains: the slots), else fp32 VALU
 };
 
 // Op i of a chain's op table, read through the constant address space. The table is read-only for the whole launch,
