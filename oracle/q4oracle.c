@@ -13,6 +13,12 @@
  *   p0o_dequant_q4         equals packQ4's own dequantized output bit for bit; fp16 tile = numpy float16 of it
  *   p0o_q4_gemv/gemvM/gemm numpy float64 matmul of the dequantized matrix (textbook routine); split partials sum to the
  *                          unsplit value; gemvM row m == gemv on row m; geglu/softcap/argmax against numpy closed forms
+ *   p0o_q4_gemm branches   (tests/test_gemm_oracle.py) numpy closed forms on data far from zero mean: the lnmod
+ *                          prologue's centring and its shift base with a negative, wrapped stride; rms; bf16 -> fp16
+ *                          round-to-nearest-even; resadd's gate x (acc + bias) in store and accumulate form; the bias
+ *                          epilogue rounding once; swiglu's interleaved gate/up rows; the heads epilogue (per-head
+ *                          QK-RMSNorm, both RoPE modes, head-major fp16 rows) and a variant without norm or rotation
+ *                          that must differ
  *   p0o_lgemv_f32/gemm_f32 within fp32 rounding of the float64 results above
  */
 #include "q4oracle.h"
