@@ -208,27 +208,69 @@ __device__ __forceinline__ int share_row(const GemvP& p, const Share& s, int G, 
   return ((s.first + j * G) / p.nsplit * s.nrb + r) * kStageRows + (pt ? p.N : 0);
 }
 
-// x' of an M > 1 op's split (raw or rms prologue), every row in one batch of loads. Thread t of the NT compute threads
-// takes k = kb + j NT + t for j < KL / NT and every row m: its norm weights are loaded once for all rows, the rows' rstd
-// slots once per row, and all of its loads are in flight together (stage_x's batches of U elements each wait for a
-// memory round trip, three of them per op at M = 5). The values are prologue_batch's and the group sums sum32's. MF:
+// x' of an M > 1 op's split (raw or rms prologue), every row in one batch of loads. Thread t of the compute threads
+// takes four k of one code word: group g = t / 8 of the split, word w = (t / 2) % 4, k 8 w + {2 e, 2 e + 1, 2 e + 4,
+// 2 e + 5} with e = t % 2, which are the word's nibble positions 4 e .. 4 e + 3 (the matrix-core operand order 0, 4,
+// 1, 5 | 2, 6, 3, 7): so an MF thread writes its hi and lo halves with one 8-byte store each. Its loads for every row
+// are in flight together (norm weights once for all rows, the rows' rstd slots once per row). The group sums are
+// sum32's balanced tree over the group's 32 k, exactly: pairs in the thread, pairs of pairs with lane ^ 1, octets,
+// octet pairs with lane ^ 2, halves with the mirrored half of the 8 lanes. The values are prologue_batch's. MF:
 // stage_x_mf's fp16 hi / lo A operands and [group][16] sums (rows >= M zero), and the result is its "too large" flag;
 // else stage_x's fp32 layout (result false).
 template <int M, bool COH, bool MF>
 __device__ __forceinline__ bool stage_rows(const GemvP& p, int g0, int g1, int gps, float* xs, float* xsum, int t) {
-  constexpr int NT = 64 * kPC, J = 2048 / NT;   // splits of M > 1 ops hold at most 2048 k
-  const int lane = t & 63;
-  const int KL = gps * 32, kb = g0 * 32, ke = g1 * 32, nj = KL / NT;
+  typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+  const int KL = gps * 32, kb = g0 * 32, ke = g1 * 32;
   const bool rms = p.pro == P0_PRO_RMS;
-  float x[J][M], nw[J], st[M];
+  const int g = t >> 3, w = (t >> 1) & 3, e = t & 1;
+  const int kl = 32 * g + 8 * w + 2 * e;   // the thread's k: kl, kl + 1, kl + 4, kl + 5 of the split
+  const bool act = g < gps;                // whole 8-lane groups
+  constexpr int kOff[4] = {0, 1, 4, 5};
+  float x[M][4], nw[4], st[M];
+  bool in[4];
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    nw[j] = 1.0f;
-    if (j < nj) {
-      const int k = min(kb + j * NT + t, ke - 1);
+  for (int j = 0; j < 4; ++j) in[j] = act && kb + kl + kOff[j] < ke;
+  const bool vec = ((uintptr_t)(p.X + p.rowB) & 15) == 0 && (p.ldx & 3) == 0 &&
+                   (!rms || ((uintptr_t)(p.NW + p.nOff) & 15) == 0);
+  if (vec) {
+    // 16-byte loads of k 8w + 4e .. + 3 (one 1 KB run per row and wave), then the lane pair trades two values:
+    // e = 0 keeps k 0, 1 and takes 4, 5; e = 1 takes 2, 3 and keeps 6, 7
+    const int k4 = act && kb + 32 * g + 8 * w + 4 * e < ke ? kb + 32 * g + 8 * w + 4 * e : ke - 4;
+    auto trade = [&](const float (&r)[4], float (&o)[4]) {
+      const float s0 = e ? r[0] : r[2], s1 = e ? r[1] : r[3];
+      const float r0 = dpp_f<0xB1>(s0), r1 = dpp_f<0xB1>(s1);   // lane ^ 1
+      o[0] = e ? r0 : r[0];
+      o[1] = e ? r1 : r[1];
+      o[2] = e ? r[2] : r0;
+      o[3] = e ? r[3] : r1;
+    };
+    float raw[M][4], rn[4];
+    // a raw buffer over the rows: its 16-byte loads take the device-scope cache policy (sc1) that ldf<true> gives
+    // 4-byte loads
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)(p.X + p.rowB), (short)0, 0x7FFFFFFF,
+                                                                        0x00020000);
 #pragma unroll
-      for (int m = 0; m < M; ++m) x[j][m] = ldf<COH>(&p.X[m * p.ldx + p.rowB + k]);
-      if (rms) nw[j] = ldf<COH>(&p.NW[p.nOff + k]);
+    for (int m = 0; m < M; ++m) {
+      const auto q = __builtin_amdgcn_raw_buffer_load_b128(xr, (m * p.ldx + k4) * 4, 0, COH ? 16 : 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) raw[m][j] = __uint_as_float(q[j]);
+    }
+    if (rms) {
+      const float* a = &p.NW[p.nOff + k4];
+      const float4 q = *(const float4*)a;
+      rn[0] = q.x; rn[1] = q.y; rn[2] = q.z; rn[3] = q.w;
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) trade(raw[m], x[m]);
+    if (rms) trade(rn, nw);
+    else nw[0] = nw[1] = nw[2] = nw[3] = 1.0f;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = in[j] ? kb + kl + kOff[j] : ke - 1;
+#pragma unroll
+      for (int m = 0; m < M; ++m) x[m][j] = ldf<COH>(&p.X[m * p.ldx + p.rowB + k]);
+      nw[j] = rms ? ldf<COH>(&p.NW[p.nOff + k]) : 1.0f;
     }
   }
 #pragma unroll
@@ -236,34 +278,43 @@ __device__ __forceinline__ bool stage_rows(const GemvP& p, int g0, int g1, int g
   bool bad = false;
   _Float16* xh = (_Float16*)xs;
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    if (j >= nj) break;
-    const int kl = j * NT + t, g = kl >> 5, kk = kl & 31;
-    const bool in = kb + kl < ke;
+  for (int m = 0; m < M; ++m) {
+    float v[4];
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const float v = in ? (rms ? x[j][m] * st[m] * nw[j] : x[j][m]) : 0.0f;
-      const float gs = sum32(v);
-      const float xo = (kl & 1) ? v * 0.0625f : v;
+    for (int j = 0; j < 4; ++j) v[j] = in[j] ? (rms ? x[m][j] * st[m] * nw[j] : x[m][j]) : 0.0f;
+    float a = v[0] + v[1], c = v[2] + v[3];   // pairs (2e, 2e + 1), (2e + 4, 2e + 5)
+    a += dpp_f<0xB1>(a);                      // lane ^ 1: k 0-3 of the word
+    c += dpp_f<0xB1>(c);                      // k 4-7
+    float o = a + c;                          // the word's 8 k
+    o += dpp_f<0x4E>(o);                      // lane ^ 2: words (0, 1), (2, 3)
+    o += dpp_f<0x141>(o);                     // the other half of the 8 lanes: the group
+    if (act) {
+      const float xo[4] = {v[0], v[1] * 0.0625f, v[2], v[3] * 0.0625f};   // odd k pre-scaled 1/16
       if (MF) {
-        const int w = kk >> 3, jj = kk & 7;
-        const float xs8 = xo * kMfScale;
-        const _Float16 hi = (_Float16)xs8;
-        const _Float16 lo = (_Float16)(xs8 - (float)hi);
-        const int at = (((g * 4 + w) * 2) * M + m) * 8 + (((jj & 3) << 1) | (jj >> 2));
-        xh[at] = hi;
-        xh[at + M * 8] = lo;
-        bad = bad || !(__builtin_fabsf(xo) < kMfBig);
-        if ((lane & 31) == 0) xsum[g * 16 + m] = gs;
+        half4v hi, lo;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float xs8 = xo[j] * kMfScale;
+          hi[j] = (_Float16)xs8;
+          lo[j] = (_Float16)(xs8 - (float)hi[j]);
+          bad = bad || !(__builtin_fabsf(xo[j]) < kMfBig);
+        }
+        // word positions 4e .. 4e + 3 hold k (2e, 2e + 4, 2e + 1, 2e + 5)
+        const half4v hp = {hi[0], hi[2], hi[1], hi[3]}, lp = {lo[0], lo[2], lo[1], lo[3]};
+        const int at = (((g * 4 + w) * 2) * M + m) * 8 + 4 * e;
+        *(half4v*)(xh + at) = hp;
+        *(half4v*)(xh + at + M * 8) = lp;
+        if ((t & 7) == 0) xsum[g * 16 + m] = o;
       } else {
-        xs[m * KL + kl] = xo;
-        if ((lane & 31) == 0) xsum[m * gps + g] = gs;
+        float* xr = xs + m * KL + kl;
+        xr[0] = xo[0]; xr[1] = xo[1]; xr[4] = xo[2]; xr[5] = xo[3];
+        if ((t & 7) == 0) xsum[m * gps + g] = o;
       }
     }
-    if (MF && (lane & 31) == 0)
-#pragma unroll
-      for (int m = M; m < 16; ++m) xsum[g * 16 + m] = 0.0f;
   }
+  if (MF && act && (t & 7) == 0)
+#pragma unroll
+    for (int m = M; m < 16; ++m) xsum[g * 16 + m] = 0.0f;
   return bad;
 }
 
