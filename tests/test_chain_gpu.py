@@ -164,6 +164,29 @@ def test_chain_matches_oracle(dev, M, gemvM, pipe_m):
     s.free()
 
 
+@pytest.mark.parametrize("M", [2, 3, 5])
+def test_chain_rows_not_16_byte_aligned(dev, M):
+    """M > 1 rows are staged with 16-byte loads when an op's row start and stride allow them, else element by
+    element: the o op here reads the qkv output from element 1 of each row on, and must still match the oracle"""
+    s = MiniStep(M=M, gemvM=True, seed=40 + M)
+    base_ops = s.ops
+
+    def ops(b):
+        o = base_ops(b)
+        o[1]["x_rowB"] = 1   # K = D elements from 1 on, inside each QKV-long row
+        return o
+
+    s.ops = ops
+    ch = s.make_chain()
+    assert ch.info()["m"] == M
+    s.reset_outputs()
+    ch.run()
+    assert not ch.status()
+    s.check_against_oracle(s.read(), f"chain M={M} o at row offset 1")
+    ch.free()
+    s.free()
+
+
 def test_chain_reruns_are_identical_and_reset(dev):
     """the chain leaves its counts at zero: every run computes the same bits (fixed plan, ordered reductions)"""
     s = MiniStep(seed=21)
