@@ -15,8 +15,9 @@
 //        engine/ops/gemm.js:147-148) into LDS,
 //      - runs 4 x 2 blocks of v_mfma_f32_32x32x16_f16 per wave over its 128 x 64 sub-tile (fp32 accumulators),
 //    with two LDS stages: the next step's X loads and the next-but-one step's W records are in flight during this
-//    step's MFMAs. LDS rows are 128 B (64 k); the 16-byte chunk c of row r sits at a swizzled position (swz_key), which
-//    makes the direct-load writes, the dequant writes and the MFMA fragment reads all bank-conflict free.
+//    step's MFMAs, issued a few at a time between them (the step's memory work is paced over its MFMAs). LDS rows are
+//    128 B (64 k); the 16-byte chunk c of row r sits at a swizzled position (swz_key), which makes the direct-load
+//    writes, the dequant writes and the MFMA fragment reads all bank-conflict free.
 #include "common.hpp"
 
 namespace p0 {
@@ -366,10 +367,10 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmP p) {
   const int wr64 = (int)(wr & 63);
   const int wkey = swz_key(wrow_t);
 
-  auto x_load = [&](int k0, int buf) {
+  auto x_load = [&](int k0, int buf, int r0, int r1) {   // this wave's instructions r0 .. r1 - 1
     uint8_t* xs = lds + buf * kStage + wv * 32 * 128;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {   // a chunk past K (a last step of one group) reads k0's: finite, never used
+    for (int r = r0; r < r1; ++r) {   // a chunk past K (a last step of one group) reads k0's: finite, never used
       const int kc = k0 + xk[r] < p.K ? k0 : 0;
       __builtin_amdgcn_global_load_lds((const void*)(xsrc[r] + kc), (__attribute__((address_space(3))) void*)(xs + r * 1024),
                                        16, 0, 0);
@@ -386,11 +387,11 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmP p) {
   };
   // dequantise this thread's group of one step into a stage. The fast path is straight-line code (it interleaves with
   // the MFMAs); a group whose q s + m may not be exact in fp32 is redone by the fp32 path afterwards (rare: a branch)
-  auto w_stage_fast = [&](int k0, int buf, int set) {
+  auto w_stage_fast = [&](int k0, int buf, int set, int w0, int w1) {   // code words w0 .. w1 - 1 of the group
     uint8_t* ws = lds + buf * kStage + BM * 128 + wrow_t * 128;
     const uint32_t sm = (wvalid && k0 + 32 * wg < p.K) ? wsm[set] : 0u;   // scale 0, min 0: zero weights
 #pragma unroll
-    for (int w = 0; w < 4; ++w) *(u32x4n*)(ws + (((4 * wg + w) ^ wkey) << 4)) = deq_word(wq[set][w], sm, true);
+    for (int w = w0; w < w1; ++w) *(u32x4n*)(ws + (((4 * wg + w) ^ wkey) << 4)) = deq_word(wq[set][w], sm, true);
   };
   auto w_stage_fix = [&](int k0, int buf, int set) {
     uint8_t* ws = lds + buf * kStage + BM * 128 + wrow_t * 128;
@@ -422,43 +423,65 @@ __global__ __launch_bounds__(kThreads) void q4_gemm_kernel(GemmP p) {
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, av[h][i]),
                                                            __builtin_bit_cast(half8, bv[h][j]), acc[i][j], 0, 0, 0);
   };
+  // half a k-step's MFMAs: blocks i0, i0 + 1 of the fragment set h
+  auto mfh = [&](int h, int i0) {
+#pragma unroll
+    for (int i = i0; i < i0 + 2; ++i)
+#pragma unroll
+      for (int j = 0; j < JB; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, av[h][i]),
+                                                           __builtin_bit_cast(half8, bv[h][j]), acc[i][j], 0, 0, 0);
+  };
   // one steady-state step (all four k-steps; the next stage exists). Step j's W records live in register set j & 1:
   // on entry SET = (it + 1) & 1 holds step it + 1 (dequantised now) and the other set, free since the last step's
-  // dequant, is refilled with step it + 2 first of all: the loads then have the whole step's MFMAs to land before the
-  // wait that closes the step.
+  // dequant, is refilled with step it + 2.
+  // The step is paced: 8 scheduling regions of 4 MFMAs each (sched_barrier between them), with the step's memory
+  // work dealt out over the first six: one X load instruction per region, the W record loads and the four code words'
+  // dequant + LDS stores one per region, the next fragments where their registers come free. The vector L1 holds a
+  // bounded number of pending misses; issued together at the step's start, the loads stalled the issuing waves (and
+  // with them their MFMAs) until the misses drained, 16-19% of the cycles by TCP_PENDING_STALL_CYCLES.
   auto step = [&](int it, int set) {
     const int buf = it & 1, k0 = it * BK;
     const uint8_t* st = lds + buf * kStage;
-    w_load(min(k0 + 2 * BK, (p.K - 1) / BK * BK), set ^ 1);   // step it + 2's records (clamped: the last is re-read)
-    __builtin_amdgcn_sched_barrier(0);
     frag(st, 0, 0);
-    x_load(k0 + BK, buf ^ 1);   // the next step's X streams into the other stage meanwhile
-    w_stage_fast(k0 + BK, buf ^ 1, set);   // W of the next step (spread amid the MFMAs by the scheduler)
-    w_stage_fix(k0 + BK, buf ^ 1, set);
     frag(st, 1, 1);
-    mfmas(0);
+    __builtin_amdgcn_sched_barrier(0);
+    x_load(k0 + BK, buf ^ 1, 0, 1);   // the next step's X streams into the other stage
+    mfh(0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    w_load(min(k0 + 2 * BK, (p.K - 1) / BK * BK), set ^ 1);   // step it + 2's records (clamped: the last is re-read)
+    w_stage_fast(k0 + BK, buf ^ 1, set, 0, 1);                // W of the next step, word by word
+    mfh(0, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    x_load(k0 + BK, buf ^ 1, 1, 2);
+    w_stage_fast(k0 + BK, buf ^ 1, set, 1, 2);
+    mfh(1, 0);
+    __builtin_amdgcn_sched_barrier(0);
     frag(st, 2, 0);
-    mfmas(1);
+    x_load(k0 + BK, buf ^ 1, 2, 3);
+    w_stage_fast(k0 + BK, buf ^ 1, set, 2, 3);
+    mfh(1, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    x_load(k0 + BK, buf ^ 1, 3, 4);
+    w_stage_fast(k0 + BK, buf ^ 1, set, 3, 4);
+    mfh(0, 0);
+    __builtin_amdgcn_sched_barrier(0);
     frag(st, 3, 1);
-    mfmas(0);
+    mfh(0, 2);
+    __builtin_amdgcn_sched_barrier(0);
     mfmas(1);
-#pragma unroll
-    for (int q = 0; q < 4 * IB * JB; ++q) {   // spread VALU and LDS work between the MFMAs
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    // every memory operation of this step was issued at its start: waiting for all of them here (this wave's direct
-    // X loads of the next stage in particular) costs nothing once the MFMAs have run
+    w_stage_fix(k0 + BK, buf ^ 1, set);
+    // every memory operation of this step was issued by its sixth region: waiting for all of them here (this wave's
+    // direct X loads of the next stage in particular) costs little once the last MFMAs have run
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   };
 
   const int nk = (p.K + BK - 1) / BK;
-  x_load(0, 0);
+  x_load(0, 0, 0, 4);
   w_load(0, 0);
   if (nk > 1) w_load(BK, 1);
-  w_stage_fast(0, 0, 0);
+  w_stage_fast(0, 0, 0, 0, 4);
   w_stage_fix(0, 0, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
