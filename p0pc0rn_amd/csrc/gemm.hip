@@ -284,6 +284,8 @@ template <bool HEADS>
 __device__ __forceinline__ void gemm_epilogue(const GemmP& p, float16v (&acc)[WTM / 32][WTN / 32], uint8_t* lds, int m0,
                                               int n0, int wm, int wn, int lane) {
   const int mb = m0 + wm * WTM + 4 * (lane >> 5), nb = n0 + wn * WTN + (lane & 31);
+  // 4-byte output stores: rows of an even number of halves, an even first column, a 4-byte aligned Y
+  const bool pair_ok = ((p.ldy | p.ny0) & 1) == 0 && ((uintptr_t)p.y & 3) == 0;
 #define P0_EPI_LOOP(...)                                                    \
   _Pragma("unroll") for (int i = 0; i < IB; ++i)                            \
   _Pragma("unroll") for (int j = 0; j < JB; ++j)                            \
@@ -295,6 +297,26 @@ __device__ __forceinline__ void gemm_epilogue(const GemmP& p, float16v (&acc)[WT
   }
   if (HEADS) {
     heads_epilogue(p, acc, lds, m0, n0, wm, wn, lane);
+  } else if (p.epi == P0_GEPI_F16 && pair_ok) {
+    // lane pairs (l, l ^ 1) trade one value per pair of rows (e, e + 1): the even lane stores columns (c, c + 1) of
+    // row e, the odd lane columns (c - 1, c) of row e + 1, each as one 4-byte store
+    const bool odd = lane & 1;
+#pragma unroll
+    for (int i = 0; i < IB; ++i)
+#pragma unroll
+      for (int j = 0; j < JB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          const float a0 = acc[i][j][e], a1 = acc[i][j][e + 1];
+          const float recv = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(
+                                 __builtin_bit_cast(int, odd ? a0 : a1), 0xB1, 0xF, 0xF, true));   // lane ^ 1
+          const int m = mb + i * 32 + 8 * (e >> 2) + (e & 3) + (odd ? 1 : 0);
+          const int n = nb + j * 32 - (odd ? 1 : 0);
+          const float lo = odd ? recv : a0, hi = odd ? a1 : recv;
+          _Float16* yp = (_Float16*)p.y + (int64_t)m * p.ldy + p.ny0 + n;
+          if (m < p.M && n + 1 < p.N) *(uint32_t*)yp = pack_h2(lo, hi);
+          else if (m < p.M && n < p.N) *yp = to_h(lo);
+        }
   } else if (p.epi == P0_GEPI_F16) {
     P0_EPI_LOOP(if (m < p.M && n < p.N) ((_Float16*)p.y)[o + n] = to_h(a);)
   } else if (p.epi == P0_GEPI_F32) {
