@@ -66,6 +66,24 @@ def test_gemm_f16_out(dev):
     check(got, want, "gemm f16->f16", 2e-3)
 
 
+@pytest.mark.parametrize("M,N,y_ld,y_n0", [(96, 251, 260, 4), (70, 131, 131, 0), (33, 128, 139, 3), (33, 128, 128, 1)])
+def test_gemm_f16_out_layouts(dev, M, N, y_ld, y_n0):
+    """fp16 outputs are stored two columns per 4-byte store when Y's rows allow it (even row stride, even first
+    column) and one by one otherwise; ragged N (an odd last column) and offset rows, with every element outside the
+    written block left untouched"""
+    K = 256
+    Nw = -(-N // 64) * 64
+    w = _weights(Nw, K, 31)
+    x = O.randn(M * K, 32).astype(np.float16)
+    f = dict(w_rows=Nw, w_cols=K, M=M, N=N, K=K, x_mode=capi.XMODE["f16"], epi=capi.GEPI["f16"], y_ld=y_ld, y_n0=y_n0)
+    n_out = (M * y_ld + y_n0 + 9) // 2 * 2   # whole 4-byte words: the device buffer is NaN-filled by words
+    want, got = run(f, dict(w=w, x=x), np.float16, n_out)
+    idx = np.concatenate([y_n0 + m * y_ld + np.arange(N) for m in range(M)])
+    check(got[idx], want[idx], f"gemm f16 out M={M} N={N} ld={y_ld} n0={y_n0}", 2e-3)
+    untouched = np.setdiff1d(np.arange(n_out), idx)
+    assert np.all(np.isnan(got[untouched].astype(np.float32)))
+
+
 def test_gemm_bf16_activations(dev):
     M, N, K = 64, 128, 512
     w = _weights(N, K, 14)
