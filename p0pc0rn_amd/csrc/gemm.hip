@@ -335,14 +335,26 @@ __device__ __forceinline__ void gemm_epilogue(const GemmP& p, float16v (&acc)[WT
       *yp = to_h(r);
     })
   } else {   // swiglu: gate = even column, up = the next one, in the neighbouring lane (engine/ops/gemm.js:200-206)
-    P0_EPI_LOOP({
-      const float up = __shfl_xor(a, 1, 64);
-      if (m < p.M && n < p.N && !(n & 1)) {
-        const int jn = n >> 1;
-        const float gB = p.bv ? p.bv[p.bvOff + jn] : 0.0f, uB = p.bv ? p.bv[p.bvOff + p.bvUp + jn] : 0.0f;
-        ((_Float16*)p.y)[o + jn] = to_h(act_f(p, a + gB) * (up + uB));
+    // per pair of rows (e, e + 1) the lane pair trades one value: the even lane takes the up value of row e, the odd
+    // lane the gate value of row e + 1, and each computes and stores one output (every lane busy, one activation each)
+    const bool odd = lane & 1;
+#pragma unroll
+    for (int i = 0; i < IB; ++i)
+#pragma unroll
+      for (int j = 0; j < JB; ++j) {
+        const int n = nb + j * 32 - (odd ? 1 : 0), jn = n >> 1;   // the pair's gate column and output column
+        const bool nin = n < p.N;
+        const float gB = p.bv && nin ? p.bv[p.bvOff + jn] : 0.0f, uB = p.bv && nin ? p.bv[p.bvOff + p.bvUp + jn] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          const float a0 = acc[i][j][e], a1 = acc[i][j][e + 1];
+          const float recv = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(
+                                 __builtin_bit_cast(int, odd ? a0 : a1), 0xB1, 0xF, 0xF, true));   // lane ^ 1
+          const float gate = odd ? recv : a0, up = odd ? a1 : recv;
+          const int m = mb + i * 32 + 8 * (e >> 2) + (e & 3) + (odd ? 1 : 0);
+          if (m < p.M && nin) ((_Float16*)p.y)[(int64_t)m * p.ldy + p.ny0 + jn] = to_h(act_f(p, gate + gB) * (up + uB));
+        }
       }
-    })
   }
 #undef P0_EPI_LOOP
 }
