@@ -284,8 +284,10 @@ template <bool HEADS>
 __device__ __forceinline__ void gemm_epilogue(const GemmP& p, float16v (&acc)[WTM / 32][WTN / 32], uint8_t* lds, int m0,
                                               int n0, int wm, int wn, int lane) {
   const int mb = m0 + wm * WTM + 4 * (lane >> 5), nb = n0 + wn * WTN + (lane & 31);
-  // 4-byte output stores: rows of an even number of halves, an even first column, a 4-byte aligned Y
+  // paired accesses: rows of an even number of elements, an even first column, a 4-byte aligned Y (8-byte aligned
+  // for the 8-byte fp32 accesses)
   const bool pair_ok = ((p.ldy | p.ny0) & 1) == 0 && ((uintptr_t)p.y & 3) == 0;
+  const bool pair8 = ((uintptr_t)p.y & 7) == 0;
 #define P0_EPI_LOOP(...)                                                    \
   _Pragma("unroll") for (int i = 0; i < IB; ++i)                            \
   _Pragma("unroll") for (int j = 0; j < JB; ++j)                            \
@@ -297,26 +299,78 @@ __device__ __forceinline__ void gemm_epilogue(const GemmP& p, float16v (&acc)[WT
   }
   if (HEADS) {
     heads_epilogue(p, acc, lds, m0, n0, wm, wn, lane);
-  } else if (p.epi == P0_GEPI_F16 && pair_ok) {
-    // lane pairs (l, l ^ 1) trade one value per pair of rows (e, e + 1): the even lane stores columns (c, c + 1) of
-    // row e, the odd lane columns (c - 1, c) of row e + 1, each as one 4-byte store
+  } else if (pair_ok && p.epi != P0_GEPI_SWIGLU) {
+    // lane pairs (l, l ^ 1) trade one value per pair of rows (e, e + 1): the even lane takes columns (c, c + 1) of
+    // row e, the odd lane columns (c - 1, c) of row e + 1, each read and written with one access of two elements
     const bool odd = lane & 1;
 #pragma unroll
     for (int i = 0; i < IB; ++i)
 #pragma unroll
-      for (int j = 0; j < JB; ++j)
+      for (int j = 0; j < JB; ++j) {
+        const int n = nb + j * 32 - (odd ? 1 : 0);   // even: the pair's first column
+        const bool n0in = n < p.N, n1in = n + 1 < p.N;
+        // per-column vectors, once per block
+        float g0 = 1.0f, g1 = 1.0f, b0 = 0.0f, b1 = 0.0f;
+        if (p.epi == P0_GEPI_RESADD) {
+          if (p.ev) { g0 = n0in ? p.ev[p.evOff + n] : 0.0f; g1 = n1in ? p.ev[p.evOff + n + 1] : 0.0f; }
+          if (p.bv) { b0 = n0in ? p.bv[p.bvOff + n] : 0.0f; b1 = n1in ? p.bv[p.bvOff + n + 1] : 0.0f; }
+        } else if (p.epi == P0_GEPI_BIAS) {
+          b0 = n0in ? p.ev[p.evOff + n] : 0.0f;
+          b1 = n1in ? p.ev[p.evOff + n + 1] : 0.0f;
+        }
 #pragma unroll
         for (int e = 0; e < 16; e += 2) {
           const float a0 = acc[i][j][e], a1 = acc[i][j][e + 1];
           const float recv = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(
                                  __builtin_bit_cast(int, odd ? a0 : a1), 0xB1, 0xF, 0xF, true));   // lane ^ 1
           const int m = mb + i * 32 + 8 * (e >> 2) + (e & 3) + (odd ? 1 : 0);
-          const int n = nb + j * 32 - (odd ? 1 : 0);
           const float lo = odd ? recv : a0, hi = odd ? a1 : recv;
-          _Float16* yp = (_Float16*)p.y + (int64_t)m * p.ldy + p.ny0 + n;
-          if (m < p.M && n + 1 < p.N) *(uint32_t*)yp = pack_h2(lo, hi);
-          else if (m < p.M && n < p.N) *yp = to_h(lo);
+          if (m >= p.M || !n0in) continue;
+          const int64_t o = (int64_t)m * p.ldy + p.ny0 + n;
+          if (p.epi == P0_GEPI_F16) {
+            _Float16* yp = (_Float16*)p.y + o;
+            if (n1in) *(uint32_t*)yp = pack_h2(lo, hi);
+            else *yp = to_h(lo);
+          } else if (p.epi == P0_GEPI_BIAS) {   // fp16 y, optionally accumulated (engine/ops/gemm.js:207-211)
+            _Float16* yp = (_Float16*)p.y + o;
+            if (n1in) {
+              float r0 = lo + b0, r1 = hi + b1;
+              if (p.res) {
+                const h2 old = __builtin_bit_cast(h2, *(const uint32_t*)yp);
+                r0 += (float)old.x;
+                r1 += (float)old.y;
+              }
+              *(uint32_t*)yp = pack_h2(r0, r1);
+            } else {
+              float r = lo + b0;
+              if (p.res) r += (float)*yp;
+              *yp = to_h(r);
+            }
+          } else {   // f32 y (plain, or resadd: engine/ops/gemm.js:192-197), 8-byte accesses where aligned
+            float* yp = (float*)p.y + o;
+            float r0 = lo, r1 = hi;
+            if (p.epi == P0_GEPI_RESADD) {
+              r0 = g0 * (lo + b0);
+              r1 = g1 * (hi + b1);
+            }
+            if (n1in && pair8) {
+              if (p.epi == P0_GEPI_RESADD && !p.store) {
+                const float2 old = *(const float2*)yp;
+                r0 = old.x + r0;
+                r1 = old.y + r1;
+              }
+              *(float2*)yp = float2{r0, r1};
+            } else {
+              if (p.epi == P0_GEPI_RESADD && !p.store) r0 = yp[0] + r0;
+              yp[0] = r0;
+              if (n1in) {
+                if (p.epi == P0_GEPI_RESADD && !p.store) r1 = yp[1] + r1;
+                yp[1] = r1;
+              }
+            }
+          }
         }
+      }
   } else if (p.epi == P0_GEPI_F16) {
     P0_EPI_LOOP(if (m < p.M && n < p.N) ((_Float16*)p.y)[o + n] = to_h(a);)
   } else if (p.epi == P0_GEPI_F32) {

@@ -136,6 +136,35 @@ def test_gemm_resadd_gate_bias(dev, store):
     check(got, want, f"gemm resadd store={store}", 1e-5)
 
 
+@pytest.mark.parametrize("epi,N,y_ld,y_n0", [("f32", 131, 140, 2), ("f32", 128, 133, 1), ("resadd", 131, 140, 2),
+                                            ("resadd", 128, 133, 3), ("bias", 131, 140, 2), ("bias", 128, 129, 1)])
+def test_gemm_output_layouts(dev, epi, N, y_ld, y_n0):
+    """the f32, resadd (accumulating) and bias (with residual) epilogues read and write two adjacent columns per
+    access when Y's rows allow it and element by element otherwise; ragged N, offset rows, elements outside the block
+    keep their values"""
+    M, K = 45, 256
+    Nw = -(-N // 64) * 64
+    w = _weights(Nw, K, 41)
+    x = O.randn(M * K, 42).astype(np.float16)
+    ev = O.randn(N, 43)
+    bv = O.randn(N, 44, 0.1)
+    n_out = (M * y_ld + y_n0 + 9) // 2 * 2
+    f = dict(w_rows=Nw, w_cols=K, M=M, N=N, K=K, x_mode=0, epi=capi.GEPI[epi], y_ld=y_ld, y_n0=y_n0)
+    arrays = dict(w=w, x=x, ev=ev)
+    if epi == "resadd":
+        f.update(store=0)
+        arrays.update(bv=bv)
+    if epi == "bias":
+        f.update(res=1)
+    dt = np.float16 if epi == "bias" else np.float32
+    init = O.randn(n_out, 45)
+    want, got = run(f, arrays, dt, n_out, init=init)
+    idx = np.concatenate([y_n0 + m * y_ld + np.arange(N) for m in range(M)])
+    check(got[idx], want[idx], f"gemm {epi} out N={N} ld={y_ld} n0={y_n0}", 2e-3 if dt == np.float16 else 1e-5)
+    untouched = np.setdiff1d(np.arange(n_out), idx)
+    assert np.array_equal(got[untouched], init.astype(dt)[untouched])
+
+
 def test_gemm_bias_residual_in_place(dev):
     M, N, K = 48, 128, 128
     w = _weights(N, K, 25)
