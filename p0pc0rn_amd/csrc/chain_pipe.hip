@@ -722,10 +722,9 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
         // 16 weight rows, two v_mfma_f32_16x16x32_f16 (x' hi and lo as A, the codes as B: gemv_kernels.hpp's GEMV-M
         // operands) give D[m][n]: x row m in lanes l / 16 == m / 4 (element m % 4), weight row n = l % 16, to which
         // each lane applies its row's scale and min.
+        // A rows >= M read row M - 1 (finite); their D rows are never stored
         const _Float16* xh = (const _Float16*)xs;
         const int aw = lane >> 4, arow = min(lane & 15, M - 1), n16 = lane & 15;
-        const bool arow_live = (lane & 15) < M;
-        const half8_t hz = {};
         for (int rp = 0; rp < nrp; ++rp) {
           f4_t am = {0.0f, 0.0f, 0.0f, 0.0f};
           for (int h = 0; h < s.nh; ++h) {
@@ -738,13 +737,13 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
               const uint32_t cw = *(const uint32_t*)(slot + (gs * 16 + n16) * 16 + aw * 4);
               const uint32_t sm = *(const uint32_t*)(slot + 8192 + (gs * 16 + n16) * 4);
               const half8_t* ap = (const half8_t*)(xh + (((g * 4 + aw) * 2) * M + arow) * 8);
-              const half8_t ahi = arow_live ? ap[0] : hz, alo = arow_live ? ap[M] : hz;
+              const half8_t ahi = ap[0], alo = ap[M];
               const f4_t sx = *(const f4_t*)(xsum + g * 16 + 4 * aw);
               const half8_t bq = codes_b(cw);
               f4_t d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
               d = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bq, d, 0, 0, 0);
               const bool live = g < s.ngs;
-              const float s8 = live ? h2f_lo(sm) * (1.0f / kMfScale) : 0.0f, mn = live ? h2f_hi(sm) : 0.0f;
+              const float s8 = live ? h2f_lo(sm) * kMfDeq : 0.0f, mn = live ? h2f_hi(sm) : 0.0f;
 #pragma unroll
               for (int e = 0; e < 4; ++e) am[e] = __builtin_fmaf(s8, d[e], __builtin_fmaf(mn, sx[e], am[e]));
             }
@@ -875,10 +874,8 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
                   // the slot's 32 groups in 4 batches of 8 (each group: two v_mfma_f32_16x16x32_f16, as in the spread
                   // path); a batch's code and scale words go to registers first, and the slot goes back to the
                   // loaders once the last batch is read
-                  const _Float16* xh = (const _Float16*)xs;
+                  const _Float16* xh = (const _Float16*)xs;   // A rows >= M: row M - 1, never stored
                   const int aw = lane >> 4, arow = min(lane & 15, M - 1), n16 = lane & 15;
-                  const bool arow_live = (lane & 15) < M;
-                  const half8_t hz = {};
 #pragma unroll 1
                   for (int b8 = 0; b8 < 4; ++b8) {
                     uint32_t cw[8], smw[8];
@@ -896,13 +893,13 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
                     for (int gg = 0; gg < 8; ++gg) {
                       const int g = 32 * h + 8 * b8 + gg;
                       const half8_t* ap = (const half8_t*)(xh + (((g * 4 + aw) * 2) * M + arow) * 8);
-                      const half8_t ahi = arow_live ? ap[0] : hz, alo = arow_live ? ap[M] : hz;
+                      const half8_t ahi = ap[0], alo = ap[M];
                       const f4_t sx = *(const f4_t*)(xsum + g * 16 + 4 * aw);
                       const half8_t bq = codes_b(cw[gg]);
                       f4_t d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
                       d = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bq, d, 0, 0, 0);
                       const bool live = g < s.ngs;
-                      const float s8 = live ? h2f_lo(smw[gg]) * (1.0f / kMfScale) : 0.0f, mn = live ? h2f_hi(smw[gg]) : 0.0f;
+                      const float s8 = live ? h2f_lo(smw[gg]) * kMfDeq : 0.0f, mn = live ? h2f_hi(smw[gg]) : 0.0f;
 #pragma unroll
                       for (int e = 0; e < 4; ++e) am[e] = __builtin_fmaf(s8, d[e], __builtin_fmaf(mn, sx[e], am[e]));
                     }

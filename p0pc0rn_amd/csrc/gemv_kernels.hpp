@@ -229,9 +229,11 @@ struct Rec {
 // ---- GEMV-M on MFMA (standalone launches, M >= 2). Per q4 group and 16 weight rows, two v_mfma_f32_16x16x32_f16
 // compute D[m][n] = 2^8 sum_k x'[m][k] q[n][k]: the A operand holds 2^8 x' split into fp16 hi + lo (2^8 x' = hi + lo to
 // 2^-22), the B operand the codes as exact fp16 values q (even k) and 16 q (odd k, whose x' carry the 1/16). Every
-// operand is kept a normal fp16 number (a one-instruction probe on MI355X found fp16 subnormal inputs NOT flushed, but
-// this path does not depend on that): the codes come out of a code word as 1024 + q (OR-ing the exponent of 1024 into
-// masked nibbles) minus 1024, and the 2^8 keeps lo normal down to |x'| ~ 2^-11.
+// operand is a normal fp16 number: the codes come out of a code word as 1024 + q (the masked nibbles with the exponent
+// of 1024 OR-ed in, one v_and_or_b32 per pair) minus 1024, and the 2^8 keeps lo normal down to |x'| ~ 2^-11. (Fed as
+// subnormals, q 2^-24 straight from the mask, the codes cost 4 VALU less per word, but a GEMV-M row then moved from
+// ~3e-7 to 3.4e-6 relative L2 off the M = 1 row on MI355X: the matrix cores do not take fp16 subnormals at full
+// precision.)
 // Rounding: these rows are not bit-identical to the fp32 VALU path's (which p0_q4_gemv and the chain kernels use);
 // they agree to ~3e-7 relative L2. The VALU path for every M is p0_gemv_tune knob 4 = 17.
 // Lane l holds D[4 (l / 16) + i][l % 16]: one weight row per lane, so each lane applies its row's scale and min
@@ -239,6 +241,7 @@ struct Rec {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 constexpr float kMfScale = 256.0f;   // 2^8 x' in the A operand
+constexpr float kMfDeq = 1.0f / kMfScale;   // D back to sum x' q
 constexpr float kMfBig = 255.0f;     // |x'| from which a workgroup keeps the fp32 VALU path (fp16 hi would overflow)
 
 // x' of the slice as MFMA A operands: [group][word w][hi, lo][M rows][8 halves], the 8 halves of word w in the code
@@ -301,13 +304,20 @@ __device__ __forceinline__ RecM load_rec_mf(const GemvP& p, int64_t tile, int g,
   }
   return r;
 }
+// (v & mask) | e1024: with e1024 held in a vector register (its value hidden from the compiler) the and + or fold into
+// one v_and_or_b32 (VOP3, which takes no literal on gfx950: the mask goes to a scalar register); with both constants
+// literal the compiler keeps two instructions
+__device__ __forceinline__ uint32_t and_or_1024(uint32_t v, uint32_t mask, uint32_t e1024) { return (v & mask) | e1024; }
+// a code word's 8 codes as B operand values, in the nibble order of stage_x_mf's A operand
 __device__ __forceinline__ half8_t codes_b(uint32_t v) {
+  uint32_t e = 0x64006400u;
+  asm("" : "+v"(e));
   const uint32_t v8 = v >> 8;
   const h2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-  const h2_t a = __builtin_bit_cast(h2_t, (v & 0x000F000Fu) | 0x64006400u) - k1024;    // q: k 8w, 8w + 4
-  const h2_t b = __builtin_bit_cast(h2_t, (v & 0x00F000F0u) | 0x64006400u) - k1024;    // 16 q: k 8w + 1, 8w + 5
-  const h2_t c = __builtin_bit_cast(h2_t, (v8 & 0x000F000Fu) | 0x64006400u) - k1024;   // q: k 8w + 2, 8w + 6
-  const h2_t d = __builtin_bit_cast(h2_t, (v8 & 0x00F000F0u) | 0x64006400u) - k1024;   // 16 q: k 8w + 3, 8w + 7
+  const h2_t a = __builtin_bit_cast(h2_t, and_or_1024(v, 0x000F000Fu, e)) - k1024;    // q: k 8w, 8w + 4
+  const h2_t b = __builtin_bit_cast(h2_t, and_or_1024(v, 0x00F000F0u, e)) - k1024;    // 16 q: k 8w + 1, 8w + 5
+  const h2_t c = __builtin_bit_cast(h2_t, and_or_1024(v8, 0x000F000Fu, e)) - k1024;   // q: k 8w + 2, 8w + 6
+  const h2_t d = __builtin_bit_cast(h2_t, and_or_1024(v8, 0x00F000F0u, e)) - k1024;   // 16 q: k 8w + 3, 8w + 7
   const u32x4l u = {__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), __builtin_bit_cast(uint32_t, c),
                     __builtin_bit_cast(uint32_t, d)};
   return __builtin_bit_cast(half8_t, u);
@@ -482,9 +492,9 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
       const int arow = min(lane & 15, M - 1), aw = lane >> 4;
       auto consume_mf = [&](const RecM (&cur)[T], int g) {
         const int gl = g - g0;
-        const half8_t z = {};
         const half8_t* ap = (const half8_t*)(xh + (((gl * 4 + aw) * 2) * M + arow) * 8);
-        const half8_t ahi = (lane & 15) < M ? ap[0] : z, alo = (lane & 15) < M ? ap[M] : z;
+        // rows >= M read row M - 1 (finite); their D rows are never used
+        const half8_t ahi = ap[0], alo = ap[M];
         const f4_t sx = *(const f4_t*)(xsum + gl * 16 + 4 * aw);
 #pragma unroll
         for (int t = 0; t < T; ++t)
@@ -493,7 +503,7 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
             const half8_t bq = codes_b(cur[t].q[b]);
             f4_t d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
             d = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bq, d, 0, 0, 0);
-            const float s8 = h2f_lo(cur[t].sm[b]) * (1.0f / kMfScale), mn = h2f_hi(cur[t].sm[b]);
+            const float s8 = h2f_lo(cur[t].sm[b]) * kMfDeq, mn = h2f_hi(cur[t].sm[b]);
 #pragma unroll
             for (int i = 0; i < 4; ++i) am[t][b][i] = __builtin_fmaf(s8, d[i], __builtin_fmaf(mn, sx[i], am[t][b][i]));
           }
