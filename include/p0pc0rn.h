@@ -250,7 +250,7 @@ int p0_chain_free(void* chain);
  * input is the previous op's output polls that output, tagged with the run, instead of the previous op's completion
  * flags), 0 = every op waits for the flags; knob 8: 1 = gemvM chains of M <= 5 rows also run on the pipelined kernel
  * (the default), 0 = on the general chain kernel; knob 9: the fewest x rows for which a pipelined chain does its slot
- * arithmetic on the matrix cores (default 4: M = 2, 3 run faster on the fp32 VALU; 6 = never).
+ * arithmetic on the matrix cores (default 3: M = 2 runs faster on the fp32 VALU; 6 = never).
  * Knobs 0-1 and 4-9 apply to chains begun afterwards, 2-3 to runs. value < 0 only queries (knobs 0-2 also ignore 0);
  * returns the previous value. */
 int p0_chain_tune(int knob, int value);

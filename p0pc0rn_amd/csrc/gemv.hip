@@ -41,7 +41,7 @@ static int g_two_tiles_min_nt = 1024;   // output tiles from which a wave stream
 static int g_min_gpw = 2;               // fewest q4 groups a wave streams when K is split
 static int g_max_kw = 16;               // most waves that share one tile slot's K-slice inside a workgroup
 static int g_mf_min_m = 2;              // fewest x rows a standalone GEMV-M runs on MFMA (17: never)
-static int g_pipe_mf_min_m = 4;         // fewest x rows a pipelined chain does its slot arithmetic on MFMA (6: never)
+static int g_pipe_mf_min_m = 3;         // fewest x rows a pipelined chain does its slot arithmetic on MFMA (6: never)
 
 struct Plan {
   int mode, gps, nks, kw, tgw, ntb, rowsTot, waves;

@@ -162,8 +162,8 @@ def test_chain_tune_knobs_round_trip():
     assert capi.chain_tune(0, 9) == old and capi.chain_tune(0, -1) == 8
     assert capi.chain_tune(0, 16) == 8 and capi.chain_tune(0, -1) == 16
     capi.chain_tune(0, old)
-    assert capi.chain_tune(9, -1) == 4 and capi.chain_tune(9, 6) == 4 and capi.chain_tune(9, -1) == 6
-    capi.chain_tune(9, 4)
+    assert capi.chain_tune(9, -1) == 3 and capi.chain_tune(9, 6) == 3 and capi.chain_tune(9, -1) == 6
+    capi.chain_tune(9, 3)
     assert capi.chain_tune(3, -1) == 0 and capi.chain_tune(10, 1) == -1
     assert capi.chain_tune(4, -1) == 1 and capi.chain_tune(4, 0) == 1 and capi.chain_tune(4, -1) == 0
     assert capi.chain_tune(4, 1) == 0 and capi.chain_tune(4, -1) == 1

@@ -213,10 +213,10 @@ def test_config_c_verify_pass_m5(dev, way, data):
         s.free()
 
 
-@pytest.mark.parametrize("M,knob9", [(3, 2), (4, 6)])
+@pytest.mark.parametrize("M,knob9", [(2, 2), (3, 6), (4, 6)])
 def test_config_c_chain_both_arithmetics(dev, M, knob9):
     """the pipelined chain's two slot arithmetics at the rows where the default picks the other one (p0_chain_tune
-    knob 9: the fewest rows on the matrix cores, default 4): M = 3 on the matrix cores, M = 4 on the fp32 VALU"""
+    knob 9: the fewest rows on the matrix cores, default 3): M = 2 on the matrix cores, M = 3 and 4 on the fp32 VALU"""
     s = E2B(M, seed=7, bounded=True)
     old = capi.chain_tune(9, knob9)
     try:
