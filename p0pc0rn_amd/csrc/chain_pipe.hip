@@ -632,18 +632,25 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
         for (int j = 0; j < 4; ++j) ok = ok && w2[j] == tag;
         if (__builtin_amdgcn_ballot_w64(!ok) != 0) poll_flags(wf);
       };
-      // a spread share's epilogue: compute thread t -> row t of the share (a softcap unit is one whole wave). Its row
-      // indices take integer divisions by per-op values; worked out here, before the input wait, and pinned, they
-      // stay off the op's critical path.
+      // a spread share's epilogue: compute thread tc -> x row m = tc / rows, row tc % rows of the share (rows x M <= 512
+      // compute threads, planned so; a softcap unit is one whole wave, rows being a multiple of 64), so the M rows'
+      // epilogues run side by side. Its row indices take integer divisions by per-op values; worked out here, before
+      // the input wait, and pinned, they stay off the op's critical path.
       const int erows = s.nu * s.nrb * kStageRows;
-      int erpg = 0, er16 = 0, en = 0;
+      int erpg = 0, er16 = 0, en = 0, em = 0;
       if (s.spread) {
-        const int t = min(tc, erows - 1);
+        int t = min(tc, erows - 1);
+        if (M > 1) {
+          const int tm = min(tc, erows * M - 1);
+          em = tm / erows;
+          t = tm - em * erows;
+        }
         const int j = t / (s.nrb * kStageRows), rr = t - j * (s.nrb * kStageRows);
         erpg = (j * s.nrb + rr / kStageRows) * s.parts;
         er16 = rr & 15;
         en = share_row(p, s, G, j, 0, 0) + rr;
         asm volatile("" : "+v"(erpg), "+v"(er16), "+v"(en));
+        if (M > 1) asm volatile("" : "+v"(em));
       }
       // x' of the split in 32-k groups; the q4 dot products take odd k pre-scaled 1/16, the q8 ones plain x'
       const bool q8 = Q8 && p.enc == P0_ENC_Q8G64S_T64;
@@ -829,22 +836,19 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
         }
         if (tc < s.nslot) ctl_add(lctl + L::CtlRel + (q0 + tc) % kRing, 1u);
         // epilogue (rows and indices from the op's start)
-        const int rows = erows, rpg = erpg, r16 = er16, n = en;
+        const int rows = erows * M, rpg = erpg, r16 = er16, n = en, m = em;
         if (tc - lane < rows) {
+          float v0 = 0.0f, v1 = 0.0f;
 #pragma unroll
-          for (int m = 0; m < M; ++m) {
-            float v0 = 0.0f, v1 = 0.0f;
+          for (int w = 0; w < kPC; ++w) v0 += red[((rpg * M + m) * kPC + w) * 16 + r16];
+          if (s.parts == 2) {
 #pragma unroll
-            for (int w = 0; w < kPC; ++w) v0 += red[((rpg * M + m) * kPC + w) * 16 + r16];
-            if (s.parts == 2) {
-#pragma unroll
-              for (int w = 0; w < kPC; ++w) v1 += red[(((rpg + 1) * M + m) * kPC + w) * 16 + r16];
-            }
-            if (tc < rows) {
-              const float yv = (e.coh & 2) ? epilogue<true>(e, s.split, m, n >> 6, n & 63, v0, v1)
-                                           : epilogue<false>(e, s.split, m, n >> 6, n & 63, v0, v1);
-              if (M == 1 && e.mbxOut) post_mbx(e, s.split, n, yv);
-            }
+            for (int w = 0; w < kPC; ++w) v1 += red[(((rpg + 1) * M + m) * kPC + w) * 16 + r16];
+          }
+          if (tc < rows) {
+            const float yv = (e.coh & 2) ? epilogue<true>(e, s.split, m, n >> 6, n & 63, v0, v1)
+                                         : epilogue<false>(e, s.split, m, n >> 6, n & 63, v0, v1);
+            if (M == 1 && e.mbxOut) post_mbx(e, s.split, n, yv);
           }
         }
       } else {

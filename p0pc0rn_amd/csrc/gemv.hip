@@ -346,7 +346,8 @@ static bool plan_pipe(std::vector<GemvP>& ops, int G, int M) {
     const int64_t numax = (U + G - 1) / G;
     const int nh = p.enc == P0_ENC_Q8G64S_T64 ? (p.kPer / 64 + 7) / 8 : (p.kPer / 32 + 31) / 32;   // slots per part
     const int64_t nrp = numax * nrb * parts;
-    const bool spread = nrp * nh <= pipe_ring_slots(M) && nrp <= pipe_spread_parts(M) && numax * nrb * kStageRows <= 512;
+    // (a spread share's epilogue gives each of the 512 compute threads one (row, x row) pair)
+    const bool spread = nrp * nh <= pipe_ring_slots(M) && nrp <= pipe_spread_parts(M) && numax * nrb * kStageRows * M <= 512;
     p.su = (int)U;
     p.scur = cur;
     p.snrb = nrb;
