@@ -231,7 +231,7 @@ typedef struct {
   int32_t n_ops, m, workgroups, waves_per_workgroup;
   int64_t lds_bytes;
   int32_t mailboxes;   /* ops that take their input from the previous op's mailbox (p0_chain_tune knob 7) */
-  int32_t reserved;
+  int32_t staged;      /* M > 1: ops that take their x' staged by the previous op (p0_chain_tune knob 10) */
 } p0_chain_info_t;
 int p0_chain_begin(void);
 int p0_chain_end(void** chain_out);
@@ -250,8 +250,10 @@ int p0_chain_free(void* chain);
  * input is the previous op's output polls that output, tagged with the run, instead of the previous op's completion
  * flags), 0 = every op waits for the flags; knob 8: 1 = gemvM chains of M <= 5 rows also run on the pipelined kernel
  * (the default), 0 = on the general chain kernel; knob 9: the fewest x rows for which a pipelined chain does its slot
- * arithmetic on the matrix cores (default 3: M = 2 runs faster on the fp32 VALU; 6 = never).
- * Knobs 0-1 and 4-9 apply to chains begun afterwards, 2-3 to runs. value < 0 only queries (knobs 0-2 also ignore 0);
+ * arithmetic on the matrix cores (default 3: M = 2 runs faster on the fp32 VALU; 6 = never); knob 10: 1 = in pipelined
+ * M > 1 chains on the matrix cores an op that reads one split of the previous op's output takes its x' as that op
+ * staged it (the default), 0 = every op stages its own x' after its wait.
+ * Knobs 0-1 and 4-10 apply to chains begun afterwards, 2-3 to runs. value < 0 only queries (knobs 0-2 also ignore 0);
  * returns the previous value. */
 int p0_chain_tune(int knob, int value);
 

@@ -52,7 +52,10 @@ struct PipeL {
   static constexpr int OffCtl = OffWred + kPC * M * 2 * 64 * 4;     // control words
   static constexpr int CtlFull = 0, CtlRel = Ring, CtlBar = 2 * Ring, CtlStop = 2 * Ring + 1, CtlGo = 2 * Ring + 2,
                        CtlTag = 2 * Ring + 3, CtlBad = 2 * Ring + 4, CtlWords = 2 * Ring + 5;
-  static constexpr int Lds = OffCtl + CtlWords * 4;
+  // M > 1, an op that stages the next op's x' (GemvP::stgOut) with an rms prologue: each compute thread's norm weight
+  // [512], then the rstd of each x row [16]
+  static constexpr int OffStg = OffCtl + CtlWords * 4;
+  static constexpr int Lds = OffStg + (M > 1 ? (512 + 16) * 4 : 0);
   static_assert(Lds <= 160 * 1024 - 256, "pipelined chain LDS");
 };
 
@@ -315,6 +318,50 @@ __device__ __forceinline__ bool stage_rows(const GemvP& p, int g0, int g1, int g
   if (MF && act && (t & 7) == 0)
 #pragma unroll
     for (int m = M; m < 16; ++m) xsum[g * 16 + m] = 0.0f;
+  return bad;
+}
+
+// x' of an M > 1 op's split [g0, g1) as the previous op staged it (GemvP::stgIn, stg_half_at's layout): the split's
+// A-operand bytes are one contiguous run there, copied to LDS by LDS-DMA (16 bytes a lane, 1 KB a wave instruction, no
+// registers; device-scope policy: written by other CUs in this run), groups past the split zero; the group sums are the
+// two 16-k halves added, rows >= M zero. The values are stage_rows's (MF) bit for bit. True if a half of the split was
+// marked too large for the matrix cores (NaN). The copy has landed when the calling wave's vmcnt is 0.
+template <int M>
+__device__ __forceinline__ bool stage_stg(const GemvP& p, int g0, int g1, int gps, _Float16* xh, float* xsum, int t) {
+  constexpr int NT = 64 * kPC, CPG = 8 * M;   // 16-byte pieces per group: 4 words x (hi, lo) x M rows x 8 halves
+  constexpr int NS = (64 * 16 + NT - 1) / NT;   // group sums per thread, for splits of <= 64 groups
+  const int ng = g1 - g0, wbase = t & ~63;
+  const uint8_t* const src = (const uint8_t*)p.stgIn + (int64_t)g0 * CPG * 16;
+  const float* ps = (const float*)(p.stgIn + (int64_t)p.K * M);
+  float h[NS][2];
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    const int c = t + u * NT, gl = c >> 4, m = c & 15;
+    h[u][0] = h[u][1] = 0.0f;
+    if (gl < ng && m < M) {
+      h[u][0] = ldf<true>(&ps[((g0 + gl) * 2) * M + m]);
+      h[u][1] = ldf<true>(&ps[((g0 + gl) * 2 + 1) * M + m]);
+    }
+  }
+  for (int c0 = wbase; c0 < gps * CPG; c0 += NT) {   // a whole wave per instruction: pieces c0 .. c0 + 63
+    const int c = c0 + (t & 63);
+    if (c0 + 64 <= ng * CPG) {
+      __builtin_amdgcn_global_load_lds((const void*)(src + (int64_t)c * 16),
+                                       (__attribute__((address_space(3))) void*)((uint8_t*)xh + c0 * 16), 16, 0, 16);
+    } else if (c < gps * CPG) {   // the split's last pieces and the zero groups past it
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (c < ng * CPG) v = *P0_GLOBAL(const u32x4, (const u32x4*)(src + (int64_t)c * 16));
+      *(u32x4*)((uint8_t*)xh + c * 16) = v;
+    }
+  }
+  bool bad = false;
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    const int c = t + u * NT;
+    const float s = h[u][0] + h[u][1];
+    bad = bad || s != s;
+    if (c < gps * 16) xsum[c] = s;   // [group][16]: c = 16 gl + m
+  }
   return bad;
 }
 
@@ -652,6 +699,16 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
         asm volatile("" : "+v"(erpg), "+v"(er16), "+v"(en));
         if (M > 1) asm volatile("" : "+v"(em));
       }
+      // M > 1, the next op's x' staged here (GemvP::stgOut): that op's rms inputs for this thread's (x row, output row),
+      // loaded now, off the epilogue's path (chain inputs: no op writes them)
+      // (they are parked in LDS once the input is staged, so that they hold no registers through the slots)
+      const bool stg_rms = M > 1 && s.spread && p.stgOut && p.stgPro == P0_PRO_RMS;
+      float stg_nwv = 1.0f, stg_stv = 1.0f;
+      if (stg_rms) {
+        const int64_t k = (int64_t)en - p.stgR0;
+        if (s.split == p.stgSp && k >= 0 && k < p.stgK) stg_nwv = p.stgNW[p.stgNOff + k];
+        if (tc < M) stg_stv = p.stgST[p.stgStatOff + tc * p.stgStatLd];
+      }
       // x' of the split in 32-k groups; the q4 dot products take odd k pre-scaled 1/16, the q8 ones plain x'
       const bool q8 = Q8 && p.enc == P0_ENC_Q8G64S_T64;
       const int xg0 = q8 ? 2 * s.gA : s.gA, xg1 = q8 ? 2 * (s.gA + s.ngs) : s.gA + s.ngs;
@@ -676,14 +733,23 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
           abandon = true;
           break;
         }
+        if (stg_rms) {   // the next op's rms inputs, loaded at this op's start, to LDS (read by the epilogue)
+          float* const stgl = (float*)(lds + L::OffStg);
+          stgl[tc] = stg_nwv;
+          if (tc < M) stgl[512 + tc] = stg_stv;
+        }
         // op i - 1's outputs are read with coherent loads: no L2 invalidate
         const bool rows1 = M >= 2 && !q8 && (p.pro == P0_PRO_RAW || p.pro == P0_PRO_RMS);   // stage_rows
         if (mf) {
           // M > 1: x' as the matrix cores' fp16 hi / lo operands; a workgroup that holds an x' too large for them
           // (|x'| >= 255, see stage_x_mf) stages fp32 x' instead and runs this op on the VALU
           bool bad;
-          if (rows1) bad = (p.coh & 1) ? stage_rows<M, true, true>(p, xg0, xg1, xgps, xs, xsum, tc)
-                                       : stage_rows<M, false, true>(p, xg0, xg1, xgps, xs, xsum, tc);
+          if (M > 1 && p.stgIn) {
+            bad = stage_stg<M>(p, xg0, xg1, xgps, (_Float16*)xs, xsum, tc);
+            __builtin_amdgcn_s_waitcnt(0);   // the LDS-DMA copy has landed (vmcnt) before the barrier
+          }
+          else if (rows1) bad = (p.coh & 1) ? stage_rows<M, true, true>(p, xg0, xg1, xgps, xs, xsum, tc)
+                                            : stage_rows<M, false, true>(p, xg0, xg1, xgps, xs, xsum, tc);
           else bad = (p.coh & 1) ? stage_x_mf<M, true, 16>(p, xg0, xg1, xgps, (_Float16*)xs, xsum, tc, 64 * kPC)
                                  : stage_x_mf<M, false, 16>(p, xg0, xg1, xgps, (_Float16*)xs, xsum, tc, 64 * kPC);
           if (bad) ctl_st(lctl + L::CtlBad, (unsigned)i + 1);
@@ -703,6 +769,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
         }
       }
       const int nrp = s.nu * s.nrb * s.parts;
+      float* const stgl = (float*)(lds + L::OffStg);
       if (s.spread) {
        if (q8) {
         // q8 slots: compute wave c takes group c of every slot, lane = (row lane / 4, quarter lane % 4 of the group's
@@ -849,6 +916,30 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
             const float yv = (e.coh & 2) ? epilogue<true>(e, s.split, m, n >> 6, n & 63, v0, v1)
                                          : epilogue<false>(e, s.split, m, n >> 6, n & 63, v0, v1);
             if (M == 1 && e.mbxOut) post_mbx(e, s.split, n, yv);
+            if (M > 1 && p.stgOut) {
+              // the next op's x' of (x row m, k = n - stgR0), as stage_rows computes it: the prologue in its own order,
+              // odd k scaled 1/16, 2^8 x' as fp16 hi + lo; the group sum of each 16 k in the balanced tree of stage_rows
+              // (pairs, quads, octets, 16: a 16-row block of this share is 16 consecutive lanes, lane % 16 = k % 16), a
+              // NaN marking a half with some |x'| too large for the matrix cores. The 16-row blocks lie wholly inside or
+              // outside the next op's x (stgR0 and stgK are multiples of 32), so the lane steps see whole blocks.
+              const int64_t k = (int64_t)n - p.stgR0;
+              if (s.split == p.stgSp && k >= 0 && k < p.stgK) {
+                const float x = stg_rms ? yv * stgl[512 + m] * stgl[tc] : yv;
+                const float xo = (k & 1) ? x * 0.0625f : x;
+                const float xs8 = xo * kMfScale;
+                const _Float16 hi = (_Float16)xs8, lo = (_Float16)(xs8 - (float)hi);
+                _Float16* const sh = (_Float16*)p.stgOut;
+                *P0_GLOBAL(_Float16, sh + stg_half_at(M, k, m, 0)) = hi;
+                *P0_GLOBAL(_Float16, sh + stg_half_at(M, k, m, 1)) = lo;
+                float g = __builtin_fabsf(xo) < kMfBig ? x : __builtin_nanf("");
+                g += dpp_f<0xB1>(g);    // lane ^ 1
+                g += dpp_f<0x4E>(g);    // lane ^ 2
+                g += dpp_f<0x141>(g);   // the other quad of the 8 lanes
+                g += dpp_f<0x140>(g);   // the other 8 of the 16
+                if ((k & 15) == 0)
+                  *P0_GLOBAL(float, (float*)(p.stgOut + (int64_t)p.stgK * M) + ((k >> 5) * 2 + ((k >> 4) & 1)) * M + m) = g;
+              }
+            }
           }
         }
       } else {

@@ -117,6 +117,7 @@ static int g_chain_spin = 1 << 22;      // polls before a chain wait gives up (a
 static int g_chain_force_give_up = 0;   // tests: every wait gives up at once
 static int g_chain_stage = 1;           // staged ops (weights copied to LDS before the wait) where they fit
 static int g_chain_mbx = 1;             // pipelined chains: mailbox hand-offs where an op reads the previous op's output
+static int g_chain_stg = 1;             // pipelined M > 1 chains: x' staged by the previous op where possible
 static int g_chain_pipe_m = 1;          // gemvM chains (M <= 5) on the pipelined kernel (1) or the general one (0)
 static int g_pipe_loaders = 2;          // pipelined chain: loader waves that stream
 static int g_pipe_depth = 2;            // pipelined chain: slots in flight per loader wave
@@ -139,6 +140,7 @@ struct ChainExec {
   size_t lds;
   chain_kernel_t kernel;
   int mailboxes;     // ops that take their input from a mailbox
+  int staged;        // ops that take their x' staged by the previous op
   Keep dev;          // owns ops and st (a recording that captured a run of the chain holds it too)
 };
 static ChainBuild* g_chain = nullptr;
@@ -265,6 +267,55 @@ static size_t plan_mailboxes(std::vector<GemvP>& ops, std::vector<int64_t>& mb_o
     if (meet(wr[i], rd[i - 1])) c.wback = 1;
     for (size_t j = 0; j + 1 < i && !c.wback; ++j)
       if (meet(wr[i], rd[j]) || meet(wr[i], wr[j])) c.wback = 2;
+  }
+  return words;
+}
+
+// Producer-staged x' of a pipelined M > 1 chain on the matrix cores. Op i takes its x' as op i - 1 wrote it (GemvP::stgIn,
+// laid out by stg_half_at) when op i's prologue is raw or rms, its arithmetic runs on the matrix cores, its x lies inside
+// one split of op i - 1's store or geglu output at an offset that is a multiple of 32 rows, with the rows of x at op i -
+// 1's row stride, and nothing in the chain writes its rms inputs (rstd slots, norm weights); op i - 1 must be a spread
+// share (its epilogue gives each thread one output row). The staged words are written before op i - 1's completion
+// flags, which op i waits for as before, and the values are those stage_rows computes from op i - 1's outputs, bit for
+// bit. Returns the words to add to the chain state; stg_out / stg_in get each op's offset in them (-1: none).
+static size_t plan_staging(std::vector<GemvP>& ops, int M, std::vector<int64_t>& stg_out, std::vector<int64_t>& stg_in) {
+  const size_t n = ops.size();
+  stg_out.assign(n, -1);
+  stg_in.assign(n, -1);
+  std::vector<std::vector<Span>> rd(n), wr(n);
+  for (size_t i = 0; i < n; ++i) op_spans(ops[i], M, rd[i], wr[i]);
+  auto meet = [](const std::vector<Span>& x, const std::vector<Span>& y) {
+    for (const Span& a : x)
+      for (const Span& b : y)
+        if (a.a < b.b && b.a < a.b) return true;
+    return false;
+  };
+  size_t words = 0;
+  for (size_t i = 1; i < n; ++i) {
+    GemvP& pr = ops[i - 1];
+    const GemvP& c = ops[i];
+    if (!c.mf || c.enc != P0_ENC_Q4G32A_T64 || !pr.sngp) continue;
+    if (pr.epi != P0_EPI_STORE && pr.epi != P0_EPI_GEGLU) continue;
+    if (c.pro != P0_PRO_RAW && c.pro != P0_PRO_RMS) continue;
+    const intptr_t d = (intptr_t)(const void*)(c.X + c.rowB) - (intptr_t)(const void*)pr.Y;
+    if (d < 0 || d % 4) continue;
+    const int64_t f = d / 4, ld = pr.nsplit > 1 ? pr.ldy : (int64_t)pr.N;
+    const int64_t sp = f / ld, r = f % ld;
+    if (sp >= pr.nsplit || r + c.K > pr.N || r % 32 || (M > 1 && c.ldx != pr.ldm)) continue;
+    if (c.pro == P0_PRO_RMS) {
+      std::vector<Span> extra{rd[i].begin() + 1, rd[i].end()};
+      bool written = false;
+      for (size_t j = 0; j < n && !written; ++j) written = meet(extra, wr[j]);
+      if (written) continue;
+    }
+    stg_out[i - 1] = stg_in[i] = (int64_t)words;
+    words += (size_t)((stg_words(M, c.K) + 63) & ~(int64_t)63);
+    pr.stgR0 = r;
+    pr.stgK = c.K;
+    pr.stgSp = (int)sp;
+    pr.stgPro = c.pro;
+    pr.stgST = c.ST; pr.stgStatOff = c.statOff; pr.stgStatLd = c.statLd;
+    pr.stgNW = c.NW; pr.stgNOff = c.nOff;
   }
   return words;
 }
@@ -634,7 +685,14 @@ extern "C" int p0_chain_end(void** out) {
   }
   mark_coherence(cb->ops, cb->M);
   std::vector<int64_t> mb_out, mb_in;
-  const size_t mb_words = pipe && cb->M == 1 && g_chain_mbx ? plan_mailboxes(cb->ops, mb_out, mb_in) : 0;
+  size_t mb_words = pipe && cb->M == 1 && g_chain_mbx ? plan_mailboxes(cb->ops, mb_out, mb_in) : 0;
+  std::vector<int64_t> stg_out, stg_in;
+  size_t stg_base = 0;
+  if (pipe && cb->M > 1 && g_chain_stg) {
+    stg_base = (mb_words + 63) & ~(size_t)63;
+    const size_t w = plan_staging(cb->ops, cb->M, stg_out, stg_in);
+    if (w) mb_words = stg_base + w;   // the staged x' follows the mailboxes (none at M > 1) in the chain state
+  }
   auto* ex = new ChainExec{};
   ex->n_ops = (int)cb->ops.size();
   ex->M = cb->M;
@@ -655,9 +713,12 @@ extern "C" int p0_chain_end(void** out) {
   if (e == hipSuccess) e = state_alloc(&ex->st, sb);
   if (e == hipSuccess && mb_words) {
     for (size_t i = 0; i < cb->ops.size(); ++i) {
-      if (mb_out[i] >= 0) cb->ops[i].mbxOut = (unsigned long long*)(ex->st + mb_base + mb_out[i]);
-      if (mb_in[i] >= 0) cb->ops[i].mbxIn = (const unsigned long long*)(ex->st + mb_base + mb_in[i]);
-      if (mb_in[i] >= 0) ++ex->mailboxes;
+      if (!mb_out.empty() && mb_out[i] >= 0) cb->ops[i].mbxOut = (unsigned long long*)(ex->st + mb_base + mb_out[i]);
+      if (!mb_in.empty() && mb_in[i] >= 0) cb->ops[i].mbxIn = (const unsigned long long*)(ex->st + mb_base + mb_in[i]);
+      if (!mb_in.empty() && mb_in[i] >= 0) ++ex->mailboxes;
+      if (!stg_out.empty() && stg_out[i] >= 0) cb->ops[i].stgOut = ex->st + mb_base + stg_base + stg_out[i];
+      if (!stg_in.empty() && stg_in[i] >= 0) cb->ops[i].stgIn = ex->st + mb_base + stg_base + stg_in[i];
+      if (!stg_in.empty() && stg_in[i] >= 0) ++ex->staged;
     }
   }
   if (e == hipSuccess) e = hipMemcpy(ex->ops, cb->ops.data(), ob, hipMemcpyHostToDevice);
@@ -723,7 +784,7 @@ extern "C" int p0_chain_info(void* chain, p0_chain_info_t* out) {
   out->waves_per_workgroup = ex->W;
   out->lds_bytes = (int64_t)ex->lds;
   out->mailboxes = ex->mailboxes;
-  out->reserved = 0;
+  out->staged = ex->staged;
   return P0_OK;
 }
 
@@ -745,6 +806,11 @@ extern "C" int p0_chain_tune(int knob, int value) {
   if (knob == 9) {
     const int old = g_pipe_mf_min_m;
     if (value > 0) g_pipe_mf_min_m = value;
+    return old;
+  }
+  if (knob == 10) {
+    const int old = g_chain_stg;
+    if (value >= 0) g_chain_stg = value ? 1 : 0;
     return old;
   }
   if (knob == 7 || knob == 8) {

@@ -77,7 +77,27 @@ struct GemvP {
   // only ops before i - 1 do, 0 if none does
   int wback;
   int mf;             // M >= 2: the MFMA arithmetic (standalone: gemv_item; pipelined chains: the slots), else fp32 VALU
+  // pipelined M > 1 chains on the matrix cores: an op whose input is one split of the previous op's output takes its x'
+  // already staged by that op (stgIn), which writes, besides its outputs, the next op's prologue values as the matrix
+  // cores' fp16 hi / lo A operands and the group sums as 16-row halves (stgOut, layout at stg_half_at): the consumer
+  // copies bytes where it would otherwise split and sum M rows of values on the VALU after its wait
+  uint32_t* stgOut;             // the next op's staged x', or null
+  const uint32_t* stgIn;        // this op's staged x', or null
+  int64_t stgR0;                // output row of the split stgSp that is the next op's k = 0
+  int stgK, stgSp, stgPro;      // the next op's K, the split it reads, its prologue (raw or rms)
+  const float* stgST; int64_t stgStatOff, stgStatLd;   // the next op's rstd slots (rms)
+  const float* stgNW; int64_t stgNOff;                  // the next op's norm weights (rms)
 };
+// staged x' of an op of K inputs and M x rows: per group g = k / 32 and code word w = (k / 8) % 4, the hi halves of the
+// M rows then their lo halves, 8 halves each in the word's nibble order (k 8w + 0, 4, 1, 5, 2, 6, 3, 7) (the LDS layout
+// of stage_x_mf / stage_rows, group by group); then the group sums as [g][half of 16 k][M] floats, a NaN half meaning
+// some |x'| of it reached kMfBig (or was not finite)
+__host__ __device__ inline int64_t stg_half_at(int M, int64_t k, int m, int lo) {
+  const int64_t g = k >> 5;
+  const int w = (int)(k >> 3) & 3, j = (int)k & 7;
+  return (((g * 4 + w) * 2 + lo) * M + m) * 8 + (((j & 3) << 1) | (j >> 2));
+}
+__host__ __device__ inline int64_t stg_words(int M, int64_t K) { return K * M + (K >> 5) * 2 * M; }
 
 // Op i of a chain's op table, read through the constant address space. The table is read-only for the whole launch,
 // so every field read at a uniform op index becomes a scalar load. Through a global pointer the compiler has to

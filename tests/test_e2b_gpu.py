@@ -256,3 +256,38 @@ def test_config_c_sweep_standalone(dev, M, op):
     _check(yb.read(np.float32), want, f"gemvM M={M} {op}")
     for b in list(d.values()) + [yb]:
         b.free()
+
+
+@pytest.mark.parametrize("M", [3, 5])
+def test_config_c_chain_staged_hand_off(dev, M):
+    """a pipelined M > 1 chain on the matrix cores takes each op's x' as its predecessor staged it (p0_chain_tune knob
+    10): every op after the first reads one split of its predecessor's output, so all of them are staged, and the
+    outputs are bit-identical to the chain whose ops stage their own x' (the staged values are stage_rows's, computed
+    in the same order), and within the bars of the oracle; with large activations (the VALU fallback marked through the
+    staged group sums) as well"""
+    for bounded in (True, False):
+        s = E2B(M, seed=8, bounded=bounded)
+        try:
+            outs, infos = [], []
+            for knob in (1, 0):
+                old = capi.chain_tune(10, knob)
+                try:
+                    ch = capi.chain(s.enqueue)
+                finally:
+                    capi.chain_tune(10, old)
+                try:
+                    infos.append(ch.info())
+                    s.reset()
+                    ch.run()
+                    assert not ch.status()
+                    outs.append({k: s.out[k].read(np.float32, n) for k, n in s.out_len.items()})
+                    outs[-1]["mx"] = s.dev["mx"].read(np.float32, s.mx_len)
+                finally:
+                    ch.free()
+            print("staged chain", infos[0], "unstaged", infos[1], flush=True)
+            assert infos[0]["staged"] == 4 * s.L and infos[1]["staged"] == 0
+            for k in outs[0]:
+                assert np.array_equal(outs[0][k].view(np.uint32), outs[1][k].view(np.uint32)), (M, bounded, k)
+            s.check(f"config C M={M} staged chain, {'bounded' if bounded else 'large'}")
+        finally:
+            s.free()
