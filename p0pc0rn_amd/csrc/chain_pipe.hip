@@ -913,9 +913,19 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
             for (int w = 0; w < kPC; ++w) v1 += red[(((rpg + 1) * M + m) * kPC + w) * 16 + r16];
           }
           if (tc < rows) {
-            const float yv = (e.coh & 2) ? epilogue<true>(e, s.split, m, n >> 6, n & 63, v0, v1)
-                                         : epilogue<false>(e, s.split, m, n >> 6, n & 63, v0, v1);
-            if (M == 1 && e.mbxOut) post_mbx(e, s.split, n, yv);
+            float yv;
+            if (M == 1 && e.mbxOut && e.epi != P0_EPI_SOFTCAP) {
+              // the mailbox word (what the next op waits on) goes out before the output itself
+              yv = e.epi == P0_EPI_GEGLU ? gelu_tanh(v0) * v1 : v0;
+              post_mbx(e, s.split, n, yv);
+              float* const yp = e.epi == P0_EPI_GEGLU ? &e.Y[n] : &e.Y[s.split * e.ldy + n];
+              if (e.coh & 2) stf<true>(yp, yv);
+              else stf<false>(yp, yv);
+            } else {
+              yv = (e.coh & 2) ? epilogue<true>(e, s.split, m, n >> 6, n & 63, v0, v1)
+                               : epilogue<false>(e, s.split, m, n >> 6, n & 63, v0, v1);
+              if (M == 1 && e.mbxOut) post_mbx(e, s.split, n, yv);
+            }
             if (M > 1 && p.stgOut) {
               // the next op's x' of (x row m, k = n - stgR0), as stage_rows computes it: the prologue in its own order,
               // odd k scaled 1/16, 2^8 x' as fp16 hi + lo; the group sum of each 16 k in the balanced tree of stage_rows
