@@ -897,21 +897,26 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
         // outputs that an earlier op reads or writes: that op complete in every workgroup first (GemvP::wback)
         if (p.wback && c == 0) check_wback();
         cbar();   // every slot of the share is read, every wave's row sums are in
-        if ((wave_stage || p.wback) && !ctl_ld(lctl + L::CtlGo)) {   // an input or flag wait gave up
-          abandon = true;
-          break;
-        }
+        // did an input or flag wait give up? (read with the row sums, checked before the first store: one LDS round
+        // trip for both)
+        const unsigned go = (wave_stage || p.wback) ? ctl_ld(lctl + L::CtlGo) : 1u;
         if (tc < s.nslot) ctl_add(lctl + L::CtlRel + (q0 + tc) % kRing, 1u);
         // epilogue (rows and indices from the op's start)
         const int rows = erows * M, rpg = erpg, r16 = er16, n = en, m = em;
+        float v0 = 0.0f, v1 = 0.0f;
         if (tc - lane < rows) {
-          float v0 = 0.0f, v1 = 0.0f;
 #pragma unroll
           for (int w = 0; w < kPC; ++w) v0 += red[((rpg * M + m) * kPC + w) * 16 + r16];
           if (s.parts == 2) {
 #pragma unroll
             for (int w = 0; w < kPC; ++w) v1 += red[(((rpg + 1) * M + m) * kPC + w) * 16 + r16];
           }
+        }
+        if (!go) {
+          abandon = true;
+          break;
+        }
+        if (tc - lane < rows) {
           if (tc < rows) {
             float yv;
             if (M == 1 && e.mbxOut && e.epi != P0_EPI_SOFTCAP) {
