@@ -246,14 +246,15 @@ int p0_chain_free(void* chain);
  * default: M = 1 chains run on the pipelined kernel, whose loader waves stream every op's weights into an LDS ring
  * ops ahead of the arithmetic; other chains stage the ops whose share fits), 0 = every op streams its weights after
  * the wait; knob 5: loader waves of the pipelined kernel that stream (1..4, default 2); knob 6: LDS slots each loader
- * keeps in flight (1 or 2, default 2); knob 7: 1 = mailbox hand-offs in pipelined chains (the default: an op whose only
+ * keeps in flight in M = 1 chains (1 or 2, default 2); knob 7: 1 = mailbox hand-offs in pipelined chains (the default: an op whose only
  * input is the previous op's output polls that output, tagged with the run, instead of the previous op's completion
  * flags), 0 = every op waits for the flags; knob 8: 1 = gemvM chains of M <= 5 rows also run on the pipelined kernel
  * (the default), 0 = on the general chain kernel; knob 9: the fewest x rows for which a pipelined chain does its slot
  * arithmetic on the matrix cores (default 3: M = 2 runs faster on the fp32 VALU; 6 = never); knob 10: 1 = in pipelined
  * M > 1 chains on the matrix cores an op that reads one split of the previous op's output takes its x' as that op
- * staged it (the default), 0 = every op stages its own x' after its wait.
- * Knobs 0-1 and 4-10 apply to chains begun afterwards, 2-3 to runs. value < 0 only queries (knobs 0-2 also ignore 0);
+ * staged it (the default), 0 = every op stages its own x' after its wait; knob 11: LDS slots each loader keeps in
+ * flight in chains of M > 1 rows (1 or 2, default 1).
+ * Knobs 0-1 and 4-11 apply to chains begun afterwards, 2-3 to runs. value < 0 only queries (knobs 0-2 also ignore 0);
  * returns the previous value. */
 int p0_chain_tune(int knob, int value);
 

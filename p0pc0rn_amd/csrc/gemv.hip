@@ -120,7 +120,8 @@ static int g_chain_mbx = 1;             // pipelined chains: mailbox hand-offs w
 static int g_chain_stg = 1;             // pipelined M > 1 chains: x' staged by the previous op where possible
 static int g_chain_pipe_m = 1;          // gemvM chains (M <= 5) on the pipelined kernel (1) or the general one (0)
 static int g_pipe_loaders = 2;          // pipelined chain: loader waves that stream
-static int g_pipe_depth = 2;            // pipelined chain: slots in flight per loader wave
+static int g_pipe_depth = 2;            // pipelined M = 1 chain: slots in flight per loader wave
+static int g_pipe_depth_m = 1;          // pipelined M > 1 chain: the same (measured: 1 is 1-2.5% faster at M = 2-5)
 static constexpr size_t kChainLds = 64 * 1024;
 static constexpr size_t kChainLdsMax = 160 * 1024 - 256;   // gfx950: LDS per CU, less the kernel's static LDS
 
@@ -702,7 +703,7 @@ extern "C" int p0_chain_end(void** out) {
   ex->kernel = k;
   if (pipe) {
     ex->pipe_cfg[0] = g_pipe_loaders;
-    ex->pipe_cfg[1] = g_pipe_depth;
+    ex->pipe_cfg[1] = cb->M > 1 ? g_pipe_depth_m : g_pipe_depth;
   }
   // chain state: last tag, timed out, the workgroups' lines and the completion counters (one 128-byte line each)
   const size_t mb_base = (chain_state_words((int)cb->ops.size(), grid) + 63) & ~(size_t)63;   // 256-byte aligned
@@ -829,8 +830,8 @@ extern "C" int p0_chain_tune(int knob, int value) {
     if (value >= 0) g_chain_stage = value ? 1 : 0;
     return old;
   }
-  if (knob == 5 || knob == 6) {
-    int* t = knob == 5 ? &g_pipe_loaders : &g_pipe_depth;
+  if (knob == 5 || knob == 6 || knob == 11) {
+    int* t = knob == 5 ? &g_pipe_loaders : knob == 6 ? &g_pipe_depth : &g_pipe_depth_m;
     const int old = *t;
     if (value > 0) *t = knob == 5 ? (value > 4 ? 4 : value) : (value >= 2 ? 2 : 1);
     return old;

@@ -164,6 +164,26 @@ def test_chain_matches_oracle(dev, M, gemvM, pipe_m):
     s.free()
 
 
+@pytest.mark.parametrize("M,knob", [(1, 6), (3, 11), (5, 11)])
+def test_chain_loader_depth_not_default(dev, M, knob):
+    """the pipelined chain with the loader depth its rows do not take by default (p0_chain_tune knob 6: M = 1,
+    default 2 slots in flight per loader; knob 11: M > 1, default 1)"""
+    s = MiniStep(M=M, gemvM=M > 1, seed=60 + M)
+    old = capi.chain_tune(knob, 1 if knob == 6 else 2)
+    try:
+        ch = s.make_chain()
+    finally:
+        capi.chain_tune(knob, old)
+    assert ch.info()["waves_per_workgroup"] == 12
+    for r in range(2):
+        s.reset_outputs()
+        ch.run()
+        assert not ch.status()
+        s.check_against_oracle(s.read(), f"chain M={M} knob {knob} run {r}")
+    ch.free()
+    s.free()
+
+
 @pytest.mark.parametrize("M", [2, 3, 5])
 def test_chain_rows_not_16_byte_aligned(dev, M):
     """M > 1 rows are staged with 16-byte loads when an op's row start and stride allow them, else element by
