@@ -220,18 +220,21 @@ int p0_gemv_tune(int knob, int value);
 /* ---- GEMV chains: a decode step's GEMVs in ONE persistent launch (engine/llm/drunner.js:1-8, 83-101) ------------- */
 /* Between p0_chain_begin and p0_chain_end, p0_q4_gemv / p0_q4_gemvM calls are validated and planned as usual but
  * appended to the chain instead of launched (all ops of a chain have the same M). p0_chain_run enqueues the whole
- * chain as one kernel: op i starts its arithmetic once op i - 1 has written all of its outputs (so op i may read
- * anything earlier ops wrote), and each workgroup streams op i's first weights while it waits. Buffers are bound at
- * p0_chain_end; a chain runs any number of times, also inside p0_record_begin / p0_record_end. Every wait is bounded:
- * a wait that gives up (which needs another kernel holding the GPU's CUs meanwhile) marks the chain, and
- * p0_chain_status (which waits for the stream) returns 1 once in *timed_out and resets the chain and the split-K
- * counters; the results of that run are invalid, and runs of the chain started before that call do nothing.
- * Runs of one chain, or of chains sharing the context's workspace, must not overlap (one stream). */
+ * chain as one kernel (a chain of 6-16 rows whose rows use disjoint memory, i.e. no row of a buffer that one row group
+ * writes is touched by another, as one pipelined kernel per group of at most 5 rows, launched back to back): op i
+ * starts its arithmetic once op i - 1 has written all of its outputs (so op i may read anything earlier ops wrote),
+ * and each workgroup streams op i's first weights while it waits. Buffers are bound at p0_chain_end; a chain runs any
+ * number of times, also inside p0_record_begin / p0_record_end. Every wait is bounded: a wait that gives up (which
+ * needs another kernel holding the GPU's CUs meanwhile) marks the chain, and p0_chain_status (which waits for the
+ * stream) returns 1 once in *timed_out and resets the chain and the split-K counters; the results of that run are
+ * invalid, and runs of the chain started before that call do nothing. Runs of one chain, or of chains sharing the
+ * context's workspace, must not overlap (one stream). */
 typedef struct {
   int32_t n_ops, m, workgroups, waves_per_workgroup;
   int64_t lds_bytes;
   int32_t mailboxes;   /* ops that take their input from the previous op's mailbox (p0_chain_tune knob 7) */
   int32_t staged;      /* M > 1: ops that take their x' staged by the previous op (p0_chain_tune knob 10) */
+  int32_t passes;      /* launches per run: 1, or, for M = 6-16 rows on the pipelined kernel, one per row group */
 } p0_chain_info_t;
 int p0_chain_begin(void);
 int p0_chain_end(void** chain_out);
@@ -239,23 +242,23 @@ int p0_chain_run(void* chain);
 int p0_chain_status(void* chain, int32_t* timed_out);
 int p0_chain_info(void* chain, p0_chain_info_t* out);
 int p0_chain_free(void* chain);
-/* knob 0: waves per chain workgroup for M = 1 (8 or 16, default 16); knob 1: largest wave share in q4 groups before
- * a chain op splits K across workgroups (default 16); knob 2: polls before a chain wait gives up (default 2^22);
- * knob 3: 1 = every wait of later runs gives up at once (for tests of the timed-out path), 0 = normal; knob 4: 1 =
- * staged ops (each workgroup copies its share of an op's weights into LDS before it waits for the previous op; the
- * default: M = 1 chains run on the pipelined kernel, whose loader waves stream every op's weights into an LDS ring
- * ops ahead of the arithmetic; other chains stage the ops whose share fits), 0 = every op streams its weights after
- * the wait; knob 5: loader waves of the pipelined kernel that stream (1..4, default 2); knob 6: LDS slots each loader
- * keeps in flight in M = 1 chains (1 or 2, default 2); knob 7: 1 = mailbox hand-offs in pipelined chains (the default: an op whose only
+/* knob 0: waves per chain workgroup for M = 1 (8 or 16, default 16); knob 1: largest wave share in q4 groups before a
+ * chain op splits K across workgroups (default 16); knob 2: polls before a chain wait gives up (default 2^22); knob 3:
+ * 1 = every wait of later runs gives up at once (for tests of the timed-out path), 0 = normal; knob 4: 1 = staged ops
+ * (each workgroup copies its share of an op's weights into LDS before it waits for the previous op; the default: M = 1
+ * chains run on the pipelined kernel, whose loader waves stream every op's weights into an LDS ring ops ahead of the
+ * arithmetic; other chains stage the ops whose share fits), 0 = every op streams its weights after the wait; knob 5:
+ * loader waves of the pipelined kernel that stream (1..4, default 2); knob 6: LDS slots each loader keeps in flight in
+ * M = 1 chains (1 or 2, default 2); knob 7: 1 = mailbox hand-offs in pipelined chains (the default: an op whose only
  * input is the previous op's output polls that output, tagged with the run, instead of the previous op's completion
- * flags), 0 = every op waits for the flags; knob 8: 1 = gemvM chains of M <= 5 rows also run on the pipelined kernel
- * (the default), 0 = on the general chain kernel; knob 9: the fewest x rows for which a pipelined chain does its slot
- * arithmetic on the matrix cores (default 3: M = 2 runs faster on the fp32 VALU; 6 = never); knob 10: 1 = in pipelined
- * M > 1 chains on the matrix cores an op that reads one split of the previous op's output takes its x' as that op
- * staged it (the default), 0 = every op stages its own x' after its wait; knob 11: LDS slots each loader keeps in
- * flight in chains of M > 1 rows (1 or 2, default 1).
- * Knobs 0-1 and 4-11 apply to chains begun afterwards, 2-3 to runs. value < 0 only queries (knobs 0-2 also ignore 0);
- * returns the previous value. */
+ * flags), 0 = every op waits for the flags; knob 8: 1 = gemvM chains of M <= 5 rows also run on the pipelined kernel,
+ * and chains of 6-16 rows as pipelined passes over row groups where their rows are independent (the default), 0 = on
+ * the general chain kernel; knob 9: the fewest x rows for which a pipelined chain does its slot arithmetic on the
+ * matrix cores (default 3: M = 2 runs faster on the fp32 VALU; 6 = never); knob 10: 1 = in pipelined M > 1 chains on
+ * the matrix cores an op that reads one split of the previous op's output takes its x' as that op staged it (the
+ * default), 0 = every op stages its own x' after its wait; knob 11: LDS slots each loader keeps in flight in chains of
+ * M > 1 rows (1 or 2, default 1). Knobs 0-1 and 4-11 apply to chains begun afterwards, 2-3 to runs. value < 0 only
+ * queries (knobs 0-2 also ignore 0); returns the previous value. */
 int p0_chain_tune(int knob, int value);
 
 /* ---- the GEMV's producer and consumers: row statistics, split-K sum + residual RMS, argmax over tile maxima ------- */

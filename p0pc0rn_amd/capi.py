@@ -41,7 +41,7 @@ class DeviceInfo(C.Structure):
 
 class ChainInfo(C.Structure):
     _fields_ = [("n_ops", i32), ("m", i32), ("workgroups", i32), ("waves_per_workgroup", i32), ("lds_bytes", i64),
-                ("mailboxes", i32), ("staged", i32)]
+                ("mailboxes", i32), ("staged", i32), ("passes", i32)]
 
 
 class GemvArgs(C.Structure):

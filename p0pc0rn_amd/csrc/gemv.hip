@@ -6,6 +6,7 @@
 // The kernels and their mapping onto MI355X are described in gemv_kernels.hpp.
 #include "gemv_kernels.hpp"
 
+#include <algorithm>
 #include <map>
 #include <memory>
 #include <string>
@@ -143,6 +144,9 @@ struct ChainExec {
   int mailboxes;     // ops that take their input from a mailbox
   int staged;        // ops that take their x' staged by the previous op
   Keep dev;          // owns ops and st (a recording that captured a run of the chain holds it too)
+  // a gemvM chain of more rows than the pipelined kernel holds, run as pipelined passes over row groups (one chain
+  // each, launched back to back; see build_row_groups); empty for a chain of one launch
+  std::vector<ChainExec*> parts;
 };
 static ChainBuild* g_chain = nullptr;
 bool building_chain() { return g_chain != nullptr; }
@@ -616,6 +620,109 @@ extern "C" int p0_chain_begin(void) {
   return P0_OK;
 }
 
+static int build_exec(ChainBuild* cb, bool pipe_only, ChainExec** out);
+
+// The rows of a gemvM chain are independent: row m of an op reads row m of its x (its rstd slot, its pleg row) and
+// writes row m of its outputs, so a chain of more rows than the pipelined kernel holds can run as pipelined passes
+// over row groups, each pass the whole chain for its rows, one after another on the stream. That holds for the buffers
+// as the caller laid them out only if no byte that one row group writes is read or written by another group: checked
+// here on exact byte spans (rows of one buffer may share cache lines; the passes do not overlap in time), with the
+// weights and norm weights, which every row reads, counted for every group. gs: the groups' first rows, then M.
+struct RowSpan {
+  uintptr_t a, b;
+  int g;
+  bool w;
+};
+static bool rows_independent(const std::vector<GemvP>& ops, const std::vector<int>& gs) {
+  const int ng = (int)gs.size() - 1;
+  std::vector<RowSpan> sp;
+  auto add = [&](const void* base, int64_t lo, int64_t hi, int g, bool w) {   // bytes [lo, hi) of base
+    sp.push_back({(uintptr_t)base + (uintptr_t)lo, (uintptr_t)base + (uintptr_t)hi, g, w});
+  };
+  for (const GemvP& p : ops) {
+    const int64_t rows = p.epi == P0_EPI_GEGLU ? 2 * (int64_t)p.N : p.N;
+    const int64_t wbytes = (rows + 63) / 64 * p.wG * 1280;
+    for (int g = 0; g < ng; ++g) {
+      add(p.w, 0, wbytes, g, false);
+      if (p.pro == P0_PRO_RMS) add(p.NW, p.nOff * 4, (p.nOff + p.K) * 4, g, false);
+      for (int64_t m = gs[g]; m < gs[g + 1]; ++m) {
+        if (p.pro == P0_PRO_RAW || p.pro == P0_PRO_RMS) {
+          add(p.X, (m * p.ldx + p.rowB) * 4, (m * p.ldx + p.rowB + p.K) * 4, g, false);
+        } else {
+          for (int64_t j = 0; j < p.nsrc; ++j) add(p.X, (j * p.ldp + m * p.ldx) * 4, (j * p.ldp + m * p.ldx + p.K) * 4, g, false);
+        }
+        if (p.pro == P0_PRO_RMS) add(p.ST, (p.statOff + m * p.statLd) * 4, (p.statOff + m * p.statLd + 1) * 4, g, false);
+        if (p.pro == P0_PRO_PLEG) add(p.EV, (p.evOff + m * p.evLd) * 4, (p.evOff + m * p.evLd + p.K) * 4, g, false);
+        const int64_t ns = p.epi == P0_EPI_STORE ? p.nsplit : 1;
+        for (int64_t sp0 = 0; sp0 < ns; ++sp0) add(p.Y, (sp0 * p.ldy + m * p.ldm) * 4, (sp0 * p.ldy + m * p.ldm + p.N) * 4, g, true);
+        if (p.epi == P0_EPI_SOFTCAP) add(p.MX, m * p.NT * 8, (m + 1) * p.NT * 8, g, true);
+      }
+    }
+  }
+  // in order of their first byte, a span meets an earlier one of another group iff it starts before that one ends
+  std::sort(sp.begin(), sp.end(), [](const RowSpan& x, const RowSpan& y) { return x.a < y.a; });
+  std::vector<uintptr_t> end_w(ng, 0), end_any(ng, 0);
+  for (const RowSpan& x : sp) {
+    for (int h = 0; h < ng; ++h)
+      if (h != x.g && (end_w[h] > x.a || (x.w && end_any[h] > x.a))) return false;
+    end_any[x.g] = std::max(end_any[x.g], x.b);
+    if (x.w) end_w[x.g] = std::max(end_w[x.g], x.b);
+  }
+  return true;
+}
+
+// A chain of M > pipe_max_m() rows (at most 16) as ceil(M / pipe_max_m()) pipelined passes of near-equal row groups
+// (8 = 4 + 4, 16 = 4 x 4): each group's ops are the chain's with their row bases moved to the group's first row. *out
+// stays null (the general kernel takes the chain) when the rows are not independent or a group cannot be planned.
+static int build_row_groups(const ChainBuild* cb, ChainExec** out) {
+  *out = nullptr;
+  const int M = cb->M, ng = (M + pipe_max_m() - 1) / pipe_max_m();
+  std::vector<int> gs(ng + 1, 0);
+  for (int g = 0; g < ng; ++g) gs[g + 1] = gs[g] + M / ng + (g < M % ng ? 1 : 0);
+  if (!rows_independent(cb->ops, gs)) return P0_OK;
+  std::vector<ChainExec*> parts;
+  auto drop = [&]() {
+    for (ChainExec* e : parts) delete e;
+  };
+  for (int g = 0; g < ng; ++g) {
+    ChainBuild sub;
+    sub.M = gs[g + 1] - gs[g];
+    sub.W = cb->W;
+    sub.G = cb->G;
+    sub.lds = cb->lds;
+    const int64_t m0 = gs[g];
+    for (GemvP p : cb->ops) {
+      p.X += m0 * p.ldx;
+      if (p.pro == P0_PRO_RMS) p.statOff += m0 * p.statLd;
+      if (p.pro == P0_PRO_PLEG) p.evOff += m0 * p.evLd;
+      p.Y += m0 * p.ldm;
+      if (p.epi == P0_EPI_SOFTCAP) p.MX += m0 * p.NT * 2;
+      p.mrows = sub.M;
+      sub.ops.push_back(p);
+    }
+    ChainExec* e = nullptr;
+    if (int r = build_exec(&sub, true, &e)) {
+      drop();
+      return r;
+    }
+    if (!e) {
+      drop();
+      return P0_OK;
+    }
+    parts.push_back(e);
+  }
+  auto* ex = new ChainExec{};
+  ex->n_ops = (int)cb->ops.size();
+  ex->M = M;
+  ex->W = parts[0]->W;
+  ex->grid = parts[0]->grid;
+  ex->lds = parts[0]->lds;
+  for (ChainExec* e : parts) ex->staged += e->staged;
+  ex->parts = parts;
+  *out = ex;
+  return P0_OK;
+}
+
 extern "C" int p0_chain_end(void** out) {
   ChainBuild* cb = g_chain;
   g_chain = nullptr;
@@ -626,6 +733,21 @@ extern "C" int p0_chain_end(void** out) {
   if (!cb->error.empty()) { set_error("p0_chain_end: %s", cb->error.c_str()); return P0_EINVAL; }
   if (cb->ops.empty()) { set_error("p0_chain_end: the chain holds no ops"); return P0_EINVAL; }
   if (!out) { set_error("p0_chain_end: no output"); return P0_EINVAL; }
+  ChainExec* ex = nullptr;
+  if (cb->M > pipe_max_m() && g_chain_stage && g_chain_pipe_m && !cb->q8) {
+    if (int r = build_row_groups(cb, &ex)) return r;
+  }
+  if (!ex) {
+    if (int r = build_exec(cb, false, &ex)) return r;
+  }
+  *out = ex;
+  return P0_OK;
+}
+
+// One launch for the chain cb: the pipelined kernel where every op can be planned for it, else the general chain
+// kernel; with pipe_only, *out stays null instead of taking the general kernel.
+static int build_exec(ChainBuild* cb, bool pipe_only, ChainExec** out) {
+  *out = nullptr;
   chain_kernel_t k = pick_chain(cb->M, cb->W);
   int per_cu = 0;
   P0_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k, 64 * cb->W, cb->lds), "p0_chain_end");
@@ -634,7 +756,7 @@ extern "C" int p0_chain_end(void** out) {
   if (grid > cb->G) grid = cb->G;   // the plans were made for G workgroups; never more than are resident
   if (grid > kChainMaxGrid) grid = kChainMaxGrid;
   size_t lds = cb->lds;
-  if (g_chain_stage && cb->M != 1) {
+  if (g_chain_stage && cb->M != 1 && !pipe_only) {
     // staged ops are dealt over exactly `grid` workgroups, so the grid must stay resident with their LDS: plan, check
     // the occupancy, and plan again on a smaller grid if it shrank
     std::vector<GemvP> staged;
@@ -680,6 +802,7 @@ extern "C" int p0_chain_end(void** out) {
       pipe = true;
     }
   }
+  if (pipe_only && !pipe) return P0_OK;
   if (cb->q8 && !pipe) {
     set_error("p0_chain_end: q8g64s.t64 ops join only pipelined chains (M = 1, 16-byte aligned weights, knob 4 on)");
     return P0_EINVAL;
@@ -749,10 +872,14 @@ extern "C" int p0_chain_run(void* chain) {
   if (!chain) { set_error("p0_chain_run: no chain"); return P0_EINVAL; }
   if (g_chain) { set_error("p0_chain_run: a chain is being built"); return P0_EINVAL; }
   auto* ex = (ChainExec*)chain;
-  hipLaunchKernelGGL(ex->kernel, dim3((unsigned)ex->grid), dim3(64 * ex->W), ex->lds, ctx().cur, ex->ops, ex->n_ops,
-                     ex->st, g_chain_force_give_up ? -1 : g_chain_spin);
-  P0_LAUNCHED("p0_chain_run");
-  keep_for_recording(ex->dev);
+  const size_t np = ex->parts.size();
+  for (size_t i = 0; i < (np ? np : 1); ++i) {   // row-group passes in order, each after the one before on the stream
+    ChainExec* e = np ? ex->parts[i] : ex;
+    hipLaunchKernelGGL(e->kernel, dim3((unsigned)e->grid), dim3(64 * e->W), e->lds, ctx().cur, e->ops, e->n_ops,
+                       e->st, g_chain_force_give_up ? -1 : g_chain_spin);
+    P0_LAUNCHED("p0_chain_run");
+    keep_for_recording(e->dev);
+  }
   return P0_OK;
 }
 
@@ -761,18 +888,24 @@ extern "C" int p0_chain_status(void* chain, int32_t* timed_out) {
   if (!chain || !timed_out) { set_error("p0_chain_status: no chain or output"); return P0_EINVAL; }
   auto* ex = (ChainExec*)chain;
   P0_HIP(hipStreamSynchronize(ctx().cur), "p0_chain_status");
-  unsigned v = 0;
-  P0_HIP(hipMemcpy(&v, ex->st + kCtrStride, sizeof v, hipMemcpyDeviceToHost), "p0_chain_status");
-  if (v) {
-    // an abandoned run can leave split-K arrival counters mid-way: clear them, and the chain state with them
-    P0_HIP(hipMemset(ex->st, 0, ex->st_words * sizeof(unsigned)), "p0_chain_status");
-    if (ex->pipe_cfg[0])
-      P0_HIP(hipMemcpy(ex->st + pipe_cfg_word(), ex->pipe_cfg, sizeof ex->pipe_cfg, hipMemcpyHostToDevice),
-             "p0_chain_status");
-    P0_HIP(hipMemset(ctx().counters, 0, ctx().n_counters * sizeof(unsigned)), "p0_chain_status");
-    P0_HIP(hipDeviceSynchronize(), "p0_chain_status");
+  unsigned any = 0;
+  const size_t np = ex->parts.size();
+  for (size_t i = 0; i < (np ? np : 1); ++i) {   // every row-group pass reports and resets its own state
+    ChainExec* e = np ? ex->parts[i] : ex;
+    unsigned v = 0;
+    P0_HIP(hipMemcpy(&v, e->st + kCtrStride, sizeof v, hipMemcpyDeviceToHost), "p0_chain_status");
+    if (v) {
+      // an abandoned run can leave split-K arrival counters mid-way: clear them, and the chain state with them
+      P0_HIP(hipMemset(e->st, 0, e->st_words * sizeof(unsigned)), "p0_chain_status");
+      if (e->pipe_cfg[0])
+        P0_HIP(hipMemcpy(e->st + pipe_cfg_word(), e->pipe_cfg, sizeof e->pipe_cfg, hipMemcpyHostToDevice),
+               "p0_chain_status");
+      P0_HIP(hipMemset(ctx().counters, 0, ctx().n_counters * sizeof(unsigned)), "p0_chain_status");
+      P0_HIP(hipDeviceSynchronize(), "p0_chain_status");
+      any = 1;
+    }
   }
-  *timed_out = v ? 1 : 0;
+  *timed_out = any ? 1 : 0;
   return P0_OK;
 }
 
@@ -786,6 +919,7 @@ extern "C" int p0_chain_info(void* chain, p0_chain_info_t* out) {
   out->lds_bytes = (int64_t)ex->lds;
   out->mailboxes = ex->mailboxes;
   out->staged = ex->staged;
+  out->passes = ex->parts.empty() ? 1 : (int32_t)ex->parts.size();
   return P0_OK;
 }
 
@@ -793,6 +927,7 @@ extern "C" int p0_chain_free(void* chain) {
   if (!chain) return P0_OK;
   auto* ex = (ChainExec*)chain;
   if (ctx().device >= 0) hipStreamSynchronize(ctx().cur);
+  for (ChainExec* e : ex->parts) delete e;
   delete ex;   // the op table and state go once no recording that ran the chain holds them
   return P0_OK;
 }

@@ -137,7 +137,8 @@ class MiniStep:
 @pytest.mark.parametrize("M,gemvM,pipe_m", [(1, False, 1), (1, True, 1), (2, True, 1), (3, True, 1), (5, True, 1),
                                              (5, True, 0), (8, True, 1)])
 def test_chain_matches_oracle(dev, M, gemvM, pipe_m):
-    """M <= 5 rows run on the pipelined kernel (knob 8 on), M = 8 and knob 8 off on the general one"""
+    """M <= 5 rows run on the pipelined kernel in one launch and M = 8 as two row-group passes (knob 8 on); knob 8 off
+    puts M = 5 on the general kernel"""
     s = MiniStep(M=M, gemvM=gemvM, seed=10 + M)
     old = capi.chain_tune(8, pipe_m)
     try:
@@ -147,10 +148,10 @@ def test_chain_matches_oracle(dev, M, gemvM, pipe_m):
     info = ch.info()
     print("chain", info, flush=True)
     assert info["n_ops"] == 6 and info["m"] == M
-    if M <= 5 and pipe_m:
-        assert info["waves_per_workgroup"] == 12
-    elif M > 1:
-        assert info["waves_per_workgroup"] == 8
+    if pipe_m:   # M > 5: pipelined passes over row groups of at most 5 rows
+        assert info["waves_per_workgroup"] == 12 and info["passes"] == (M + 4) // 5
+    else:
+        assert info["waves_per_workgroup"] == 8 and info["passes"] == 1
     if M == 1 and info["waves_per_workgroup"] == 12:
         # o takes qkv's output, gate_up (rms) o's, down the geglu output, the head (rms) the 'sum' op's; qkv and the
         # 'sum' op (two partials per element) wait for flags. As gemvM calls, op 4 reads down's first split raw (gemvM
@@ -162,6 +163,83 @@ def test_chain_matches_oracle(dev, M, gemvM, pipe_m):
     s.check_against_oracle(s.read(), f"chain M={M} gemvM={gemvM}")
     ch.free()
     s.free()
+
+
+@pytest.mark.parametrize("M", [6, 11, 16])
+def test_chain_row_group_passes(dev, M):
+    """a gemvM chain of 6-16 rows runs as pipelined passes over row groups of at most 5 rows (6 = 3 + 3,
+    11 = 4 + 4 + 3, 16 = 4 x 4), one launch each: every op against the oracle, a rerun, and replays of a recording of
+    the run (bit-identical to the eager run)"""
+    s = MiniStep(M=M, gemvM=True, seed=70 + M)
+    ch = s.make_chain()
+    info = ch.info()
+    print("chain", info, flush=True)
+    assert info["passes"] == (M + 4) // 5 and info["waves_per_workgroup"] == 12 and info["m"] == M
+    for r in range(2):
+        s.reset_outputs()
+        ch.run()
+        assert not ch.status()
+        s.check_against_oracle(s.read(), f"chain M={M} run {r}")
+    want = s.read()
+    rec = capi.record(ch.run)
+    for r in range(2):
+        s.reset_outputs()
+        rec.replay()
+        capi.done()
+        got = s.read()
+        for k in want:
+            assert np.array_equal(want[k].view(np.uint32), got[k].view(np.uint32)), f"replay {r}: {k}"
+    assert not ch.status()
+    rec.free()
+    ch.free()
+    s.free()
+
+
+def test_chain_rows_sharing_memory_take_the_general_kernel(dev):
+    """rows of different row groups that share memory (op 1 reads x rows 128 floats apart, each 256 long: row m reads
+    op 0's output around its row m / 2, so rows 4-7 read rows 2-3) cannot run as row-group passes: the chain takes the
+    general kernel, one launch, and matches the oracle"""
+    M, N0, K = 8, 256, 256
+    w0, w1 = _w(N0, K, 81), _w(128, K, 82)
+    x = O.randn(M * K, 83)
+    dv = {"w0": capi.to_device(w0), "w1": capi.to_device(w1), "x": capi.to_device(x),
+          "y0": capi.Buffer(4 * M * N0), "y1": capi.Buffer(4 * M * 128)}
+    raw, store = capi.PRO["raw"], capi.EPI["store"]
+
+    def ops(b):
+        return [dict(w=b["w0"], w_rows=N0, w_cols=K, x=b["x"], N=N0, K=K, pro=raw, epi=store, y=b["y0"], M=M,
+                     x_ldx=K, y_ldm=N0, y_ldy=M * N0),
+                dict(w=b["w1"], w_rows=128, w_cols=K, x=b["y0"], N=128, K=K, pro=raw, epi=store, y=b["y1"], M=M,
+                     x_ldx=128, y_ldm=128, y_ldy=M * 128)]
+
+    def enqueue():
+        for f in ops(dv):
+            capi.q4_gemvM(capi.gemvm_args(**f))
+
+    for k in ("y0", "y1"):
+        dv[k].fill_u32(NAN)
+    ch = capi.chain(enqueue)
+    info = ch.info()
+    print("chain", info, flush=True)
+    assert info["passes"] == 1 and info["waves_per_workgroup"] == 8
+    ch.run()
+    assert not ch.status()
+    g0 = dv["y0"].read(np.float32, M * N0)
+    g1 = dv["y1"].read(np.float32, M * 128)
+    # op 1 reads rows up to (M - 1) * 128 + K floats of y0: inside its M * N0 floats
+    want0 = np.full(M * N0, np.nan, np.float32)
+    want1 = np.full(M * 128, np.nan, np.float32)
+    host = {"w0": w0.ctypes.data, "w1": w1.ctypes.data, "x": x.ctypes.data, "y0": want0.ctypes.data,
+            "y1": want1.ctypes.data}
+    f0, f1 = ops(host)
+    O.q4_gemvM(capi.gemvm_args(**f0))
+    _check(g0, want0, "op 0")
+    g0c = np.ascontiguousarray(g0)
+    O.q4_gemvM(capi.gemvm_args(**dict(f1, x=g0c.ctypes.data)))
+    _check(g1, want1, "op 1")
+    ch.free()
+    for b in dv.values():
+        b.free()
 
 
 @pytest.mark.parametrize("M,knob", [(1, 6), (3, 11), (5, 11)])
