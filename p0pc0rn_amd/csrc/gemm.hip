@@ -216,8 +216,11 @@ __device__ __forceinline__ void heads_epilogue(const GemmP& p, float16v (&acc)[W
     if (!(lane & 1)) red[wn * 256 + wm * 128 + 32 * i + 8 * (e >> 2) + (e & 3) + 4 * hh] = tot;
   }
   __syncthreads();
+  // when N / 128 is odd, the last column tile's second head (waves wn = 2, 3) does not exist: those waves stay in the
+  // barriers, read no norm weights or RoPE entries (treated as a value head) and store nothing
   const int hd = (n0 >> 7) + (wn >> 1);
-  const int sec = hd < p.hq ? 0 : hd < p.hq + p.hkv ? 1 : 2;
+  const bool live = hd < (p.N >> 7);
+  const int sec = !live ? 2 : hd < p.hq ? 0 : hd < p.hq + p.hkv ? 1 : 2;
   const int c0 = (wn & 1) * 64 + (lane & 31);   // head column of j = 0 (j = 1: + 32)
   float nw[JBh];
 #pragma unroll
@@ -270,7 +273,7 @@ __device__ __forceinline__ void heads_epilogue(const GemmP& p, float16v (&acc)[W
             out = (c & 1) ? pv[j][e] * rp[1] + v * rp[0] : v * rp[0] - pv[j][e] * rp[1];
           }
         }
-        if (m < p.M) y[(hd * p.hLtot + p.hRow0 + m) * 128 + c] = to_h(out);
+        if (live && m < p.M) y[(hd * p.hLtot + p.hRow0 + m) * 128 + c] = to_h(out);
       }
     }
   }

@@ -91,6 +91,9 @@ def rope_table(L, seed, mode):
     ("inter", 300, 2, 2, 520, 200, "lnmod"),     # FLUX: Hq = Hkv, lnmod prologue, img rows after txt rows
     ("half", 257, 4, 1, 257, 0, "rms"),          # Qwen3 TE: 4 query heads per kv head, rms prologue
     ("inter", 64, 1, 0, 64, 0, "f16"),           # one query head, no key / value heads
+    ("half", 64, 1, 0, 64, 0, "f16"),            # odd head counts: the last column tile holds one real head
+    ("half", 100, 1, 1, 120, 20, "f16"),         # H = 3
+    ("inter", 130, 3, 1, 150, 10, "lnmod"),      # H = 5
 ])
 def test_heads_epilogue_vs_oracle(dev, mode, M, Hq, Hkv, Ltot, row0, xmode):
     H = Hq + 2 * Hkv
@@ -118,9 +121,14 @@ def test_heads_epilogue_vs_oracle(dev, mode, M, Hq, Hkv, Ltot, row0, xmode):
     want = np.full(n_out, np.nan, np.float16)
     O.q4_gemm(capi.gemm_args(**f, **{k: v.ctypes.data for k, v in arrays.items()}, y=want.ctypes.data))
     devb = {k: capi.to_device(v) for k, v in arrays.items()}
-    yb = capi.Buffer(n_out * 2).fill_u32(NAN16x2)
+    # Y with a tail of one more head's rows: a head past N / 128 (a 256-column tile's second head when H is odd) must
+    # not be written
+    tail = Ltot * 128
+    yb = capi.Buffer((n_out + tail) * 2).fill_u32(NAN16x2)
     capi.q4_gemm(capi.gemm_args(**f, **devb, y=yb))
-    got = yb.read(np.float16).reshape(H, Ltot, 128)
+    full = yb.read(np.uint16)
+    assert np.all(full[n_out:] == 0x7E00), "the heads epilogue wrote past the last head"
+    got = full[:n_out].view(np.float16).reshape(H, Ltot, 128)
     want = want.reshape(H, Ltot, 128)
     inside = got[:, row0:row0 + M].astype(np.float32)
     check(inside, want[:, row0:row0 + M].astype(np.float32), f"heads {mode}", 2e-3)

@@ -16,17 +16,20 @@ pytestmark = pytest.mark.gpu
 SCRATCH = 32 << 20
 
 
-def _pair(fields, arrays, out_bytes):
-    """the same call through both entry points -> (gemm output bytes, noalloc output bytes, noalloc flops)"""
+def _pair(fields, arrays, out_bytes, tail=0):
+    """the same call through both entry points -> (gemm output bytes, noalloc output bytes, noalloc flops); Y is
+    allocated with `tail` more bytes after the output, which neither call may write"""
     d = {k: capi.to_device(v) for k, v in arrays.items()}
-    ya = capi.Buffer(out_bytes).fill_u32(0x7FC00000)
-    yb = capi.Buffer(out_bytes).fill_u32(0x7FC00000)
+    ya = capi.Buffer(out_bytes + tail).fill_u32(0x7FC00000)
+    yb = capi.Buffer(out_bytes + tail).fill_u32(0x7FC00000)
     capi.q4_gemm(capi.gemm_args(**fields, **d, y=ya))
     fl = capi.q4_gemm_noalloc(capi.gemm_args(**fields, **d, y=yb))
     a, b = ya.read(np.uint8), yb.read(np.uint8)
     for buf in list(d.values()) + [ya, yb]:
         buf.free()
-    return a, b, fl
+    for out in (a, b):
+        assert np.all(out[out_bytes:].view(np.uint32) == 0x7FC00000), "written past the output"
+    return a[:out_bytes], b[:out_bytes], fl
 
 
 def test_noalloc_matches_gemm_two_calls_second_smaller(dev):
@@ -57,7 +60,7 @@ def test_noalloc_lnmod_heads_two_calls(dev):
         rope = np.random.default_rng(seed).uniform(-1, 1, (M, 128)).astype(np.float32)
         f = dict(w_rows=N, w_cols=K, M=M, N=N, K=K, x_mode=capi.XMODE["lnmod"], pv_off=K, pv_stride=(1 << 32) - K,
                  epi=capi.GEPI["heads"], heads_ltot=M, heads_hq=H // 3, heads_hkv=H // 3, heads_rope=0)
-        a, b, _ = _pair(f, dict(w=w, x=x, stats=st, pv=pv, ev=ev, rope=rope), N * M * 2)
+        a, b, _ = _pair(f, dict(w=w, x=x, stats=st, pv=pv, ev=ev, rope=rope), N * M * 2, tail=M * 128 * 2)
         assert np.all(np.isfinite(b.view(np.float16).astype(np.float32)))
         assert np.array_equal(a, b), "noalloc heads output differs from p0_q4_gemm's"
 
