@@ -3,11 +3,13 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemm] [--json-only]
 
-Headline (`value`): tokens/s of the Gemma-4-E2B-shaped decode step at M=1 (config B): 30 layers x {qkv 3072x2048 rms,
-o 2048x2048 raw kPer 2048, gate_up 2x8192x2048 rms+geglu, down 2048x8192 raw kPer 2048} + lm_head 262144x2048
-rms+softcap (tile max/argmax) = 121 GEMV ops, run per token both ways the library offers (the DecodeRunner
-analogue): planned once into a chain that runs as ONE persistent launch, and recorded as a graph of 121 launches;
-the faster is the headline and both are reported.
+Headline (`value`): tokens/s of the Gemma-4-E2B-shaped decode token at M=1 (config B): 30 layers x {qkv 3072x2048
+rms, o 2048x2048 raw kPer 2048, gate_up 2x8192x2048 rms+geglu, down 2048x8192 raw kPer 2048} + the token's tail as
+engine/llm/gemma4.js:503-511 and engine/llm/drunner.js:82-90 run it: the rstd copy into the head's stat slot, the
+lm_head 262144x2048 rms+softcap (tile max/argmax), the argmax over the 4096 tile maxima and the copy of the result
+words into the staging buffer = 121 GEMV ops + 3 others. Run per token both ways the library offers (the
+DecodeRunner analogue): planned once into a chain that runs as ONE persistent launch, and recorded as a graph of 124
+launches; the faster is the headline and both are reported (also the 121 GEMVs alone).
 Attention, norms and the PLE projections are not part of the step.
 
 Also reported: the step's weight-streaming GB/s, config A (one 8192x2048 GEMV, weight ring of 32 copies), the
@@ -89,13 +91,19 @@ class Step:
         mx[M * (VOCAB // 64) * 2 + 1::2] = 1.0
         self.mx = c.to_device(mx)
         self.mx_stat_off = M * (VOCAB // 64) * 2 + 1
+        # the token's tail: the final norm's rstd per row (what the token copies into the head's stat slot), the
+        # argmax words and the staging buffer the result is copied to
+        self.rsrc = c.to_device(np.tile(np.array([0.0, 1.0], np.float32), M))
+        self.arg = c.Buffer(max(16, 8 * M))
+        self.stage = c.Buffer(max(16, 8 * M))
 
     def rms_off(self, j):
         """stat_off of rms op j (qkv of layer l: j = 2 l, gate_up: 2 l + 1)"""
         return 2 * self.M * j + 1
 
     def free_acts(self):
-        for b in (self.x, self.st, self.qkvp, self.obuf, self.mbuf, self.dpart, self.logits, self.mx):
+        for b in (self.x, self.st, self.qkvp, self.obuf, self.mbuf, self.dpart, self.logits, self.mx, self.rsrc,
+                  self.arg, self.stage):
             b.free()
 
     # one projection, M = 1 through gemv, M > 1 through gemvM (the reference's decode / verify call pairs)
@@ -110,17 +118,29 @@ class Step:
                          epi=c.EPI[epi], y=y, stat=stat, stat_off=stat_off, stat_ld=2, norm=self.nw, mx=mx)
         return c.q4_gemvM(a)
 
-    def ops(self, only=None):
+    def ops(self, only=None, token=False):
         """enqueue the step (or only one projection kind over all layers). Every op reads its predecessor's output:
         o the q rows of qkv, gate_up o's output, down gate_up's, the next layer's qkv (and the head) the first K-split
-        partial of down. In the model a norm sits between some of them (normadd / rowstats, not GEMVs, not part of
-        the step); their rstd slots are fixed inputs here."""
+        partial of down. In the model a norm sits between some of them (normadd / rowstats, not part of the step);
+        their rstd slots are fixed inputs here. token: the whole token, with the tail of engine/llm/gemma4.js:503-511
+        (the rstd copy into the head's stat slot before the head, the argmax after it) and DecodeRunner.end's copy of
+        the result words (engine/llm/drunner.js:82-90)."""
+        c, M = self.c, self.M
         for li in range(LAYERS):
             self.ops_layer(li, ("qkv", "o", "gu", "down") if only is None else (only,))
         if only in (None, "head"):
+            if token:
+                for m in range(M):
+                    c.copy(self.rsrc, (2 * m + 1) * 4, self.mx, (self.mx_stat_off + 2 * m) * 4, 4)
             # the head's rms slot lives in the mx buffer past the tile maxima (engine/llm/gemma4.js:505-508)
             self.proj(self.head, VOCAB, D, self.dpart, self.logits, "rms", "softcap", stat=self.mx,
                       stat_off=self.mx_stat_off, mx=self.mx)
+            if token:
+                if M == 1:
+                    c.argmax(self.mx, VOCAB // 64, self.arg)
+                else:
+                    c.argmaxM(self.mx, VOCAB // 64, M, self.arg)
+                c.copy(self.arg, 0, self.stage, 0, 8 * M)
 
     def ops_layer(self, li, kinds):
         """enqueue the projections `kinds` of layer li"""
@@ -139,9 +159,11 @@ class Step:
             b, n, k = t["down"]
             self.proj(b, n, k, self.mbuf, self.dpart, "raw", kPer=2048)
 
-    def step_bytes(self, only=None):
+    def step_bytes(self, only=None, token=False):
         M = self.M
         tot = 0
+        if token:   # the tail: the rstd copies, the argmax's read of the tile maxima, its words and their copy
+            tot += M * 8 + M * (VOCAB // 64) * 8 + M * 8 + M * 16
         shapes = {"qkv": (QKV, D), "o": (D, D), "gu": (2 * MLP, D), "down": (D, MLP)}
         for kind, (n, k) in shapes.items():
             if only in (None, kind):
@@ -188,8 +210,9 @@ def bench_decode(c, step, steps, warmup, breakdown=True):
     """the M=1 step two ways, both product paths: one chain launch per token (p0_chain_*) and a recording of 121
     launches (p0_record_*); the faster is the headline"""
     step.alloc(1)
-    ms_chain, info = time_chain(c, step.ops, warmup, steps)
-    ms_graph = time_recording(c, step.ops, warmup, steps)
+    ms_chain, info = time_chain(c, lambda: step.ops(token=True), warmup, steps)
+    ms_graph = time_recording(c, lambda: step.ops(token=True), warmup, steps)
+    ms_gemv, _ = time_chain(c, step.ops, warmup, steps)   # the 121 GEMVs alone, as one chain
     by_kind = {}
     for kind in ("qkv", "o", "gu", "down", "head") if breakdown else ():
         kms, _ = time_chain(c, lambda: step.ops(kind), 3, 20)
@@ -201,7 +224,7 @@ def bench_decode(c, step, steps, warmup, breakdown=True):
                          "GBps": round(step.step_bytes(kind) / (kms_graph * 1e-3) / 1e9, 1)}
     mode = "chain" if ms_chain <= ms_graph else "graph"
     out = {"ms": min(ms_chain, ms_graph), "mode": mode, "ms_chain": ms_chain, "ms_graph": ms_graph,
-           "bytes": step.step_bytes(), "by_kind": by_kind, "chain": info}
+           "ms_gemv_chain": ms_gemv, "bytes": step.step_bytes(token=True), "by_kind": by_kind, "chain": info}
     step.free_acts()
     return out
 
@@ -370,8 +393,8 @@ def main():
     extra = {"decode_step": {"ms": round(ms, 4), "algorithmic_bytes": int(dec["bytes"]),
                              "GBps": round(step_gbps, 1), "frac_hbm_peak": round(step_gbps / HBM_PEAK_GBPS, 4),
                              "mode": dec["mode"], "ms_chain": round(dec["ms_chain"], 4),
-                             "ms_graph": round(dec["ms_graph"], 4), "chain": dec["chain"],
-                             "by_projection": dec["by_kind"]}}
+                             "ms_graph": round(dec["ms_graph"], 4), "ms_gemv_chain": round(dec["ms_gemv_chain"], 4),
+                             "chain": dec["chain"], "by_projection": dec["by_kind"]}}
     if not args.no_extra:
         if not args.no_config_a:
             extra["config_a_gemv"] = bench_config_a(c)
@@ -401,10 +424,8 @@ def main():
     if dec["mode"] == "chain":
         roofline = {"bound": "hbm", "achieved": round(step_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                     "frac": round(step_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                    "kernel": ("q4_chain_pipe_kernel (the whole M=1 decode step: 121 GEMV ops, one launch)"
-                               if dec["chain"]["waves_per_workgroup"] == 12 else
-                               "q4_gemv_chain_kernel<1,%d> (the whole M=1 decode step: 121 GEMV ops, one launch)"
-                               % dec["chain"]["waves_per_workgroup"]),
+                    "kernel": ("q4_chain_pipe_kernel (the whole M=1 decode token: 121 GEMV ops, the rstd copy, the "
+                               "argmax and the result copy, one launch)"),
                     "bytes_per_launch": int(dec["bytes"]), "us_per_launch": round(ms * 1e3, 2)}
         traffic_key = "decode_chain_bytes_per_launch"
     elif not dec["by_kind"]:
@@ -435,10 +456,13 @@ def main():
         "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "gemma4-e2b-shaped decode step, M=1: 30 x {qkv 3072x2048 rms, o 2048x2048, "
-                               "gate_up 2x8192x2048 rms+geglu, down 2048x8192 kPer 2048} + lm_head 262144x2048 "
-                               "rms+softcap; q4g32a.t64 int4 weights (0.625 B/weight), fp32 accumulate",
-                   "weights_GB": round(step.weight_bytes / 1e9, 3), "launches_per_step": 1 if dec["mode"] == "chain" else 121, "gemv_ops_per_step": 121,
+        "config": {"workload": "gemma4-e2b-shaped decode token, M=1: 30 x {qkv 3072x2048 rms, o 2048x2048, "
+                               "gate_up 2x8192x2048 rms+geglu, down 2048x8192 kPer 2048} + rstd copy, lm_head "
+                               "262144x2048 rms+softcap, argmax over 4096 tile maxima, result copy; q4g32a.t64 int4 "
+                               "weights (0.625 B/weight), fp32 accumulate",
+                   "weights_GB": round(step.weight_bytes / 1e9, 3),
+                   "launches_per_step": 1 if dec["mode"] == "chain" else 124, "gemv_ops_per_step": 121,
+                   "ops_per_token": 124,
                    "decode_path": dec["mode"],
                    "gemv_GBps": round(step_gbps, 1),
                    "gemm_TFLOPS_M4608": extra.get("gemm_flux2_klein_M4608", {}).get("TFLOPS")},

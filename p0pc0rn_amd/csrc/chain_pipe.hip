@@ -23,7 +23,7 @@
 // codes [32 groups][16 rows][16 B] then their scale words [32][16][4 B]. A small share (at most a ring of slots) is
 // computed by all 8 compute waves together, one (group, row) pair per lane per slot, and reduced once; a large one
 // (the lm_head) by one wave per unit, each lane taking 8 pairs per slot, so the waves stream independently.
-#include "gemv_kernels.hpp"
+#include "chain_aux.hpp"
 
 namespace p0 {
 
@@ -57,6 +57,7 @@ struct PipeL {
   static constexpr int OffStg = OffCtl + CtlWords * 4;
   static constexpr int Lds = OffStg + (M > 1 ? (512 + 16) * 4 : 0);
   static_assert(Lds <= 160 * 1024 - 256, "pipelined chain LDS");
+  static_assert(RedRp * M * kPC * 16 >= kAuxLdsFloats, "the aux ops' trees use the reduction area");
 };
 
 __host__ int pipe_lds_bytes(int M) {
@@ -87,7 +88,6 @@ __device__ __forceinline__ void asm_lds_st(unsigned a, unsigned v) {
 
 // The compute waves' control words, through an LDS-typed pointer: a volatile access through a generic pointer
 // compiles to a flat load, which also waits for every outstanding global access of the wave (vmcnt(0)).
-typedef __attribute__((address_space(3))) unsigned lds_u32;
 __device__ __forceinline__ unsigned ctl_ld(lds_u32* a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
 __device__ __forceinline__ void ctl_st(lds_u32* a, unsigned v) { __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
 __device__ __forceinline__ void ctl_add(lds_u32* a, unsigned v) {
@@ -667,6 +667,22 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
   bool abandon = false;
   for (int i = 0; i < n_ops; ++i) {
     const GemvP& p = op_at(ops, i);
+    if (p.kind != kOpGemv) {
+      // copy / argmax / rowstats / normadd (chain_aux.hpp): the workgroups that take part wait for op i - 1 in every
+      // workgroup, run the op in the reduction area and publish once their stores are acknowledged; the others publish
+      // at once (their flag of op i says, as always, that they are done with every op up to i)
+      if (aux_worker(p, b)) {
+        if (i > 0 && !wait_flags(mine + (size_t)(i - 1) * Gp, nullptr)) {
+          abandon = true;
+          break;
+        }
+        gen = aux_run(&p, b, G, tc, (lds_f32*)red, lctl + L::CtlBar, gen);
+        __builtin_amdgcn_s_waitcnt(0);
+        cbar();
+      }
+      if (c == 0 && lane < kFlagCopies) st_coh(flags + ((size_t)lane * n_ops + i) * Gp + b, tag);
+      continue;
+    }
     const Share s = share_of<Q8>(p, b, G);
     if (s.nu > 0) {
       const EpiP e = epi_of(p);

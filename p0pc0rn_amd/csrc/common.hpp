@@ -63,12 +63,20 @@ inline int require_open(const char* op) {
   }
   return P0_OK;
 }
-// true between p0_chain_begin and p0_chain_end (gemv.hip): only gemv / gemvM calls join a chain, every other op
-// refuses to run meanwhile instead of running out of order
+// true between p0_chain_begin and p0_chain_end (gemv.hip): gemv / gemvM, copy, argmax / argmaxM, rowstats and normadd
+// calls join a chain; every other op (the GEMM, the dequant, uploads) refuses to run meanwhile instead of running out of
+// order
 bool building_chain();
+// ops that are not GEMVs join the chain being built (gemv.hip; the pipelined chain kernel runs them, chain_aux.hpp)
+int chain_add_copy(const void* src, void* dst, int64_t words);
+int chain_add_argmax(const float* mx, int64_t n, int64_t M, uint32_t* out);
+int chain_add_rowstats(const float* x, int64_t ld, int64_t c0, int64_t rows, int64_t cols, int mode, float eps,
+                       float* st, int64_t st_off);
+int chain_add_normadd(const float* t, int64_t nsrc, int64_t ldp, const float* w, int64_t w_off, float* x, float* st,
+                      int64_t st_off, int64_t D, int64_t M, float eps, float scale, int mode);
 inline int refuse_in_chain(const char* op) {
   if (building_chain()) {
-    set_error("%s: only gemv / gemvM calls join a chain (a chain is being built)", op);
+    set_error("%s: only gemv / gemvM, copy, argmax, rowstats and normadd calls join a chain (a chain is being built)", op);
     return P0_EINVAL;
   }
   return P0_OK;

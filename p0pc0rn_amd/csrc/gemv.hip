@@ -129,6 +129,7 @@ static constexpr size_t kChainLdsMax = 160 * 1024 - 256;   // gfx950: LDS per CU
 struct ChainBuild {
   int M = 0, W = 0, G = 0;
   bool q8 = false;     // holds q8g64s.t64 ops (the pipelined kernel only)
+  bool aux = false;    // holds copy / argmax / rowstats / normadd ops (the pipelined kernel only)
   size_t lds = 0;
   std::vector<GemvP> ops;
   std::string error;   // the first failed append (reported again by p0_chain_end)
@@ -188,6 +189,27 @@ static Span span_of(const float* base, int64_t lo, int64_t hi) {   // floats [lo
 }
 static void op_spans(const GemvP& p, int M, std::vector<Span>& rd, std::vector<Span>& wr) {
   const int64_t m1 = M - 1;
+  switch (p.kind) {   // ops that are not GEMVs: what they read first, then the rest (chain_aux.hpp)
+    case kOpCopy:
+      rd.push_back(span_of(p.asrc, 0, p.an));
+      wr.push_back(span_of(p.adst, 0, p.an));
+      return;
+    case kOpArgmax:
+      rd.push_back(span_of(p.asrc, 0, p.arows * p.acols * 2));
+      wr.push_back(span_of(p.adst, 0, p.arows * 2));
+      return;
+    case kOpRowstats:
+      rd.push_back(span_of(p.asrc, p.ac0, (p.arows - 1) * p.ald + p.ac0 + p.acols));
+      wr.push_back(span_of(p.adst, p.astOff * 2, (p.astOff + p.arows) * 2));
+      return;
+    case kOpNormadd:
+      rd.push_back(span_of(p.asrc, 0, (p.an - 1) * p.aldp + p.arows * p.acols));
+      if (p.amode == 0) rd.push_back(span_of(p.aw, p.awOff, p.awOff + p.acols));
+      rd.push_back(span_of(p.adst, 0, p.arows * p.acols));
+      wr.push_back(span_of(p.adst, 0, p.arows * p.acols));
+      wr.push_back(span_of(p.ast, p.astOff, p.astOff + p.arows));
+      return;
+  }
   if (p.pro == P0_PRO_RAW || p.pro == P0_PRO_RMS) rd.push_back(span_of(p.X, p.rowB, m1 * p.ldx + p.rowB + p.K));
   else rd.push_back(span_of(p.X, 0, (int64_t)(p.nsrc - 1) * p.ldp + m1 * p.ldx + p.K));   // X[j ldp + m ldx + k]
   if (p.pro == P0_PRO_RMS) {
@@ -250,6 +272,7 @@ static size_t plan_mailboxes(std::vector<GemvP>& ops, std::vector<int64_t>& mb_o
   for (size_t i = 1; i < n; ++i) {
     const GemvP& pr = ops[i - 1];
     GemvP& c = ops[i];
+    if (pr.kind != kOpGemv || c.kind != kOpGemv) continue;
     if (pr.epi != P0_EPI_STORE && pr.epi != P0_EPI_GEGLU) continue;
     if (c.pro != P0_PRO_RAW && c.pro != P0_PRO_RMS) continue;
     const intptr_t d = (intptr_t)(const void*)(c.X + c.rowB) - (intptr_t)(const void*)pr.Y;
@@ -299,6 +322,7 @@ static size_t plan_staging(std::vector<GemvP>& ops, int M, std::vector<int64_t>&
   for (size_t i = 1; i < n; ++i) {
     GemvP& pr = ops[i - 1];
     const GemvP& c = ops[i];
+    if (pr.kind != kOpGemv || c.kind != kOpGemv) continue;
     if (!c.mf || c.enc != P0_ENC_Q4G32A_T64 || !pr.sngp) continue;
     if (pr.epi != P0_EPI_STORE && pr.epi != P0_EPI_GEGLU) continue;
     if (c.pro != P0_PRO_RAW && c.pro != P0_PRO_RMS) continue;
@@ -394,6 +418,11 @@ static size_t plan_staged(GemvP& p, int M, int W, int G, int& cur) {
 static bool plan_pipe(std::vector<GemvP>& ops, int G, int M) {
   int cur = 0;
   for (GemvP& p : ops) {
+    if (p.kind != kOpGemv) {   // no units: every workgroup's share is empty
+      p.su = 0;
+      p.scur = cur;
+      continue;
+    }
     if ((uintptr_t)p.w & 15) return false;
     if (M > 1 && (p.kPer > 2048 || p.enc != P0_ENC_Q4G32A_T64)) return false;
     const int nrb = p.epi == P0_EPI_SOFTCAP ? 4 : 1, parts = p.epi == P0_EPI_GEGLU ? 2 : 1;
@@ -433,7 +462,7 @@ static int launch_q8(GemvP& p, int M, const char* op) {
 static int launch(GemvP& p, int M, const char* op) {
   ChainBuild* cb = g_chain;
   if (p.enc == P0_ENC_Q8G64S_T64 && !cb) return launch_q8(p, M, op);
-  if (cb && cb->ops.empty()) {   // the chain's first op fixes M and the workgroup shape
+  if (cb && cb->M == 0) {   // the chain's first GEMV fixes M and the workgroup shape
     cb->M = M;
     cb->W = M == 1 ? g_chain_waves : 8;
     cb->G = ctx().cu_count * (cb->W == 16 ? 1 : 2);
@@ -482,6 +511,71 @@ static int launch(GemvP& p, int M, const char* op) {
   hipLaunchKernelGGL(k, grid, dim3(64 * pl.waves), pl.lds, ctx().cur, p);
   P0_LAUNCHED(op);
   return P0_OK;
+}
+
+// ---- ops that are not GEMVs, appended to the chain being built instead of launched (p0_copy, p0_argmax / p0_argmaxM,
+// p0_rowstats, p0_normadd; chain_aux.hpp runs them). The callers have validated the arguments. Such an op has no units
+// (su = 0), so no workgroup streams weights for it; only the pipelined kernel runs it (p0_chain_end refuses others).
+static int add_aux(GemvP& p) {
+  ChainBuild* cb = g_chain;
+  p.nsplit = 1;   // share_of's arithmetic on an empty share
+  p.kPer = p.K = 32;
+  p.snrb = p.sngp = 1;
+  p.enc = P0_ENC_Q4G32A_T64;
+  cb->ops.push_back(p);
+  cb->aux = true;
+  return P0_OK;
+}
+int chain_add_copy(const void* src, void* dst, int64_t words) {
+  GemvP p{};
+  p.kind = kOpCopy;
+  p.asrc = (const float*)src;
+  p.adst = (float*)dst;
+  p.an = words;
+  return add_aux(p);
+}
+int chain_add_argmax(const float* mx, int64_t n, int64_t M, uint32_t* out) {
+  GemvP p{};
+  p.kind = kOpArgmax;
+  p.asrc = mx;
+  p.adst = (float*)out;
+  p.acols = n;
+  p.arows = M;
+  return add_aux(p);
+}
+int chain_add_rowstats(const float* x, int64_t ld, int64_t c0, int64_t rows, int64_t cols, int mode, float eps,
+                       float* st, int64_t st_off) {
+  GemvP p{};
+  p.kind = kOpRowstats;
+  p.asrc = x;
+  p.ald = ld;
+  p.ac0 = c0;
+  p.arows = rows;
+  p.acols = cols;
+  p.amode = mode;
+  p.aeps = eps;
+  p.adst = st;
+  p.astOff = st_off;
+  return add_aux(p);
+}
+int chain_add_normadd(const float* t, int64_t nsrc, int64_t ldp, const float* w, int64_t w_off, float* x, float* st,
+                      int64_t st_off, int64_t D, int64_t M, float eps, float scale, int mode) {
+  GemvP p{};
+  p.kind = kOpNormadd;
+  p.asrc = t;
+  p.an = nsrc;
+  p.aldp = ldp;
+  p.aw = w;
+  p.awOff = w_off;
+  p.adst = x;
+  p.ast = st;
+  p.astOff = st_off;
+  p.acols = D;
+  p.arows = M;
+  p.aeps = eps;
+  p.ascale = scale;
+  p.amode = mode;
+  return add_aux(p);
 }
 
 // engine/llm/lops.js:113-114: q4g32a.t64 (groups of 32 k) and q8g64s.t64 (groups of 64 k)
@@ -639,7 +733,29 @@ static bool rows_independent(const std::vector<GemvP>& ops, const std::vector<in
   auto add = [&](const void* base, int64_t lo, int64_t hi, int g, bool w) {   // bytes [lo, hi) of base
     sp.push_back({(uintptr_t)base + (uintptr_t)lo, (uintptr_t)base + (uintptr_t)hi, g, w});
   };
+  const int64_t M = gs[ng];
   for (const GemvP& p : ops) {
+    if (p.kind != kOpGemv) {   // row-wise only with one row per x row: argmax, rowstats, normadd over the chain's M
+      if (p.kind == kOpCopy || p.arows != M) return false;
+      for (int g = 0; g < ng; ++g) {
+        if (p.kind == kOpNormadd && p.amode == 0) add(p.aw, p.awOff * 4, (p.awOff + p.acols) * 4, g, false);
+        for (int64_t m = gs[g]; m < gs[g + 1]; ++m) {
+          if (p.kind == kOpArgmax) {
+            add(p.asrc, m * p.acols * 8, (m + 1) * p.acols * 8, g, false);
+            add(p.adst, m * 8, (m + 1) * 8, g, true);
+          } else if (p.kind == kOpRowstats) {
+            add(p.asrc, (m * p.ald + p.ac0) * 4, (m * p.ald + p.ac0 + p.acols) * 4, g, false);
+            add(p.adst, (p.astOff + m) * 8, (p.astOff + m + 1) * 8, g, true);
+          } else {
+            for (int64_t j = 0; j < p.an; ++j)
+              add(p.asrc, (j * p.aldp + m * p.acols) * 4, (j * p.aldp + (m + 1) * p.acols) * 4, g, false);
+            add(p.adst, m * p.acols * 4, (m + 1) * p.acols * 4, g, true);
+            add(p.ast, (p.astOff + m) * 4, (p.astOff + m + 1) * 4, g, true);
+          }
+        }
+      }
+      continue;
+    }
     const int64_t rows = p.epi == P0_EPI_GEGLU ? 2 * (int64_t)p.N : p.N;
     const int64_t wbytes = (rows + 63) / 64 * p.wG * 1280;
     for (int g = 0; g < ng; ++g) {
@@ -690,8 +806,25 @@ static int build_row_groups(const ChainBuild* cb, ChainExec** out) {
     sub.W = cb->W;
     sub.G = cb->G;
     sub.lds = cb->lds;
+    sub.aux = cb->aux;
     const int64_t m0 = gs[g];
     for (GemvP p : cb->ops) {
+      if (p.kind != kOpGemv) {   // argmax / rowstats / normadd over the chain's rows (rows_independent checked)
+        if (p.kind == kOpArgmax) {
+          p.asrc += m0 * p.acols * 2;
+          p.adst += m0 * 2;
+        } else if (p.kind == kOpRowstats) {
+          p.asrc += m0 * p.ald;
+          p.astOff += m0;
+        } else {
+          p.asrc += m0 * p.acols;
+          p.adst += m0 * p.acols;
+          p.astOff += m0;
+        }
+        p.arows = sub.M;
+        sub.ops.push_back(p);
+        continue;
+      }
       p.X += m0 * p.ldx;
       if (p.pro == P0_PRO_RMS) p.statOff += m0 * p.statLd;
       if (p.pro == P0_PRO_PLEG) p.evOff += m0 * p.evLd;
@@ -733,6 +866,11 @@ extern "C" int p0_chain_end(void** out) {
   if (!cb->error.empty()) { set_error("p0_chain_end: %s", cb->error.c_str()); return P0_EINVAL; }
   if (cb->ops.empty()) { set_error("p0_chain_end: the chain holds no ops"); return P0_EINVAL; }
   if (!out) { set_error("p0_chain_end: no output"); return P0_EINVAL; }
+  if (cb->M == 0) {   // no GEMV (only copy / argmax / rowstats / normadd ops): the M = 1 kernel runs them
+    cb->M = 1;
+    cb->W = g_chain_waves;
+    cb->G = ctx().cu_count * (cb->W == 16 ? 1 : 2);
+  }
   ChainExec* ex = nullptr;
   if (cb->M > pipe_max_m() && g_chain_stage && g_chain_pipe_m && !cb->q8) {
     if (int r = build_row_groups(cb, &ex)) return r;
@@ -803,6 +941,11 @@ static int build_exec(ChainBuild* cb, bool pipe_only, ChainExec** out) {
     }
   }
   if (pipe_only && !pipe) return P0_OK;
+  if (cb->aux && !pipe) {
+    set_error("p0_chain_end: copy, argmax, rowstats and normadd ops join only pipelined chains (M <= 5 or rows that "
+              "share no memory, 16-byte aligned weights, splits of at most 2048 k for M > 1, knobs 4 and 8 on)");
+    return P0_EINVAL;
+  }
   if (cb->q8 && !pipe) {
     set_error("p0_chain_end: q8g64s.t64 ops join only pipelined chains (M = 1, 16-byte aligned weights, knob 4 on)");
     return P0_EINVAL;

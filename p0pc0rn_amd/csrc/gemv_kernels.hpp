@@ -87,7 +87,21 @@ struct GemvP {
   int stgK, stgSp, stgPro;      // the next op's K, the split it reads, its prologue (raw or rms)
   const float* stgST; int64_t stgStatOff, stgStatLd;   // the next op's rstd slots (rms)
   const float* stgNW; int64_t stgNOff;                  // the next op's norm weights (rms)
+  // ops of a pipelined chain that are not GEMVs (kind != kOpGemv): p0_copy, p0_argmax / p0_argmaxM, p0_rowstats and
+  // p0_normadd called while a chain is being built (chain_aux.hpp). They have no units and stream no weights (su = 0):
+  // the workgroups that take part wait for op i - 1 in every workgroup, do the op and publish their flags.
+  //   copy:     an words from asrc to adst
+  //   argmax:   arows rows of acols (max, index) pairs at asrc -> adst[2 m], adst[2 m + 1]
+  //   rowstats: arows rows of acols floats at asrc[r ald + ac0 + c] -> (mean, rstd) pairs at adst[(astOff + r) 2]
+  //   normadd:  arows rows of acols floats: t = sum of the an partials asrc[j aldp + m acols + i], the residual adst
+  //             updated (amode 0, norm weights aw + awOff) or replaced (amode 1), ast[astOff + m] = its rstd
+  int kind;
+  const float* asrc; float* adst; float* ast; const float* aw;
+  int64_t arows, acols, ald, ac0, an, aldp, astOff, awOff;
+  float aeps, ascale;
+  int amode;
 };
+constexpr int kOpGemv = 0, kOpCopy = 1, kOpArgmax = 2, kOpRowstats = 3, kOpNormadd = 4;
 // staged x' of an op of K inputs and M x rows: per group g = k / 32 and code word w = (k / 8) % 4, the hi halves of the
 // M rows then their lo halves, 8 halves each in the word's nibble order (k 8w + 0, 4, 1, 5, 2, 6, 3, 7) (the LDS layout
 // of stage_x_mf / stage_rows, group by group); then the group sums as [g][half of 16 k][M] floats, a NaN half meaning

@@ -135,9 +135,11 @@ extern "C" int p0_rowstats(const p0_rowstats_args_t* a) {
   if (!a->x || !a->st) { set_error("rowstats: missing x or st buffer"); return P0_EINVAL; }
   if (a->x_off % 4) { set_error("rowstats: x offset"); return P0_EINVAL; }
   if (int r = require_open("rowstats")) return r;
-  if (int r = refuse_in_chain("rowstats")) return r;
   if (a->rows == 0) return P0_OK;
   const int64_t ld = a->x_ld ? a->x_ld : a->cols;
+  if (building_chain())   // a chain op (chain_aux.hpp): the same sums in the same order
+    return chain_add_rowstats((const float*)((const uint8_t*)a->x + a->x_off), ld, a->x_c0, a->rows, a->cols,
+                              (int)a->mode, a->eps, a->st, a->st_off);
   const unsigned grid = (unsigned)(a->rows < 65536 * 4 ? a->rows : 65536 * 4);
   hipLaunchKernelGGL(rowstats_kernel, dim3(grid), dim3(kRowThreads), 0, ctx().cur,
                      (const float*)((const uint8_t*)a->x + a->x_off), ld, a->x_c0, a->rows, a->cols, (int)a->mode,
@@ -154,9 +156,10 @@ extern "C" int p0_normadd(const p0_normadd_args_t* a) {
   if (!a->t || !a->x || !a->st || (a->mode == 0 && !a->w)) { set_error("normadd: missing t, w, x or st buffer"); return P0_EINVAL; }
   if (D * (int64_t)sizeof(float) > 150 * 1024) { set_error("normadd: D %lld exceeds this build's row buffer", (long long)D); return P0_EINVAL; }
   if (int r = require_open("normadd")) return r;
-  if (int r = refuse_in_chain("normadd")) return r;
   const int64_t nsrc = a->t_n ? a->t_n : 1, ldp = a->t_ld ? a->t_ld : D * M;
   const float eps = a->eps != 0.0f ? a->eps : 1e-6f;
+  if (building_chain())
+    return chain_add_normadd(a->t, nsrc, ldp, a->w, a->w_off, a->x, a->st, a->st_off, D, M, eps, a->scale, (int)a->mode);
   const size_t lds = (size_t)D * sizeof(float);
   hipLaunchKernelGGL(normadd_kernel, dim3((unsigned)M), dim3(kRowThreads), lds, ctx().cur, a->t, nsrc, ldp, a->w,
                      a->w_off, a->x, a->st, a->st_off, D, eps, a->scale, (int)a->mode);
@@ -168,7 +171,7 @@ extern "C" int p0_argmaxM(const float* mx, int64_t n, int64_t M, uint32_t* out) 
   if (!mx || !out) { set_error("argmax: missing mx or out buffer"); return P0_EINVAL; }
   if (n < 0 || M < 1) { set_error("argmax: n %lld, M %lld", (long long)n, (long long)M); return P0_EINVAL; }
   if (int r = require_open("argmax")) return r;
-  if (int r = refuse_in_chain("argmax")) return r;
+  if (building_chain()) return chain_add_argmax(mx, n, M, out);
   hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)M), dim3(kRowThreads), 0, ctx().cur, mx, n, out);
   P0_LAUNCHED("argmax");
   return P0_OK;

@@ -217,7 +217,6 @@ int p0_fill(void* dst, size_t dst_off, uint32_t value, size_t words) {
 
 int p0_copy(const void* src, size_t src_off, void* dst, size_t dst_off, size_t bytes) {
   if (int r = require_open("p0_copy")) return r;
-  if (int r = refuse_in_chain("p0_copy")) return r;
   const char* a = (const char*)src + src_off;
   char* b = (char*)dst + dst_off;
   if (((uintptr_t)a | (uintptr_t)b | bytes) & 3) {   // copyBufferToBuffer's rule: offsets and size multiples of 4
@@ -229,6 +228,7 @@ int p0_copy(const void* src, size_t src_off, void* dst, size_t dst_off, size_t b
     set_error("p0_copy: source and destination overlap");
     return P0_EINVAL;
   }
+  if (building_chain()) return chain_add_copy(a, b, (int64_t)(bytes / 4));   // a chain op (chain_aux.hpp)
   const bool wide = !(((uintptr_t)a | (uintptr_t)b | bytes) & 15);
   const size_t n = wide ? bytes / 16 : bytes / 4;
   size_t blocks = (n + 255) / 256;

@@ -9,9 +9,11 @@
 // What a token becomes on this device:
 //   mode 'graph' (default): the token's ops are captured as a HIP graph (p0_record_*), one kernel per op, any op kind;
 //                           end() records the copy of the result words into the parity's staging buffer;
-//   mode 'chain':           the token's gemv / gemvM calls become ONE persistent kernel (p0_chain_*) that streams the
-//                           next op's weights while the previous op finishes; only GEMV ops join a chain (the library
-//                           refuses others while a chain is being built), and submit() copies the result after the run.
+//   mode 'chain':           the token's ops become ONE persistent kernel (p0_chain_*) that streams the next op's
+//                           weights while the previous op finishes: gemv / gemvM, copy, argmax / argmaxM, rowstats and
+//                           normadd join a chain (the library refuses others, e.g. gemm, while a chain is being built);
+//                           end() appends the copy of the result words into the parity's staging buffer, so the token
+//                           and its result copy are one launch.
 // A token is submitted once, as a command buffer is, and released when its result has been read; with {reuse: true}
 // tokens stay until forget() / destroy() and may be submitted again (their buffers must still hold the token's inputs).
 'use strict';
@@ -47,10 +49,9 @@ export class DecodeRunner {
   }
   /** the core Runner's signature: the ops of this build call the library directly, never through a runner */
   dispatch() { throw new Error('DecodeRunner: the MI355X ops record themselves; dispatch() is not used'); }
-  /** copy between buffers inside the token (recorded into a graph token; a chain holds GEMV ops only) */
+  /** copy between buffers inside the token (recorded into a graph token, or an op of a chain token) */
   copy(src, srcOff, dst, dstOff, size) {
     if (!this.cur) throw new Error('DecodeRunner: copy outside a token');
-    if (this.mode === 'chain') throw new Error('DecodeRunner: a chain token holds gemv / gemvM ops only (copy)');
     native().copy(src.ptr, srcOff, dst.ptr, dstOff, size);
   }
   split() {}
@@ -64,7 +65,7 @@ export class DecodeRunner {
     this.cur = null;
     if (!c) throw new Error('DecodeRunner: end without begin');
     const nb = Math.min(this.stageBytes, Math.ceil(bytes / 4) * 4);
-    if (this.mode === 'graph' && argBuf) native().copy(argBuf.ptr, 0, this.stage[c.parity].ptr, 0, nb);
+    if (argBuf) native().copy(argBuf.ptr, 0, this.stage[c.parity].ptr, 0, nb);   // recorded / a chain op
     this.open = false;
     const h = this.mode === 'chain' ? native().chainEnd() : native().recordEnd();
     const n = this.mode === 'chain' ? native().chainInfo(h) : native().recordInfo(h);
@@ -83,10 +84,8 @@ export class DecodeRunner {
     if (!tk || !tk.h) return Promise.reject(new Error('DecodeRunner: the token was released (submitted once, or forgotten)'));
     const n = native();
     if (this.timer) n.timerStart();
-    if (tk.mode === 'chain') {
-      n.chainRun(tk.h);
-      if (tk.arg) n.copy(tk.arg.ptr, 0, this.stage[tk.parity].ptr, 0, tk.bytes);
-    } else n.replay(tk.h);
+    if (tk.mode === 'chain') n.chainRun(tk.h);
+    else n.replay(tk.h);
     this.submits++;
     return Promise.resolve().then(() => {
       if (this.timer) {

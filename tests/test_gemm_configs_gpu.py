@@ -270,8 +270,8 @@ def test_recording_keeps_its_staging_workspace(dev):
 
 
 def test_chain_refuses_other_ops(dev):
-    """only gemv / gemvM calls join a chain: a GEMM (or any other op) called while one is being built is refused
-    instead of running out of order"""
+    """gemv / gemvM, copy, argmax, rowstats and normadd calls join a chain: a GEMM called while one is being built is
+    refused instead of running out of order"""
     w = capi.Buffer(1280)
     x = capi.Buffer(256)
     y = capi.Buffer(256)
@@ -280,8 +280,7 @@ def test_chain_refuses_other_ops(dev):
         a = capi.gemm_args(w=w, w_rows=64, w_cols=32, x=x, M=1, N=64, K=32, epi=capi.GEPI["f32"], y=y)
         fl = capi.C.c_double()
         assert capi.lib().p0_q4_gemm(capi.C.byref(a), capi.C.byref(fl)) == capi.P0_EINVAL
-        assert "only gemv / gemvM calls join a chain" in capi.last_error()
-        assert capi.lib().p0_copy(x.ptr, 0, y.ptr, 0, 16) == capi.P0_EINVAL
+        assert "calls join a chain" in capi.last_error()
     finally:
         h = capi.vp()
         capi.lib().p0_chain_end(capi.C.byref(h))   # an empty chain: refused, nothing to free

@@ -164,7 +164,7 @@ const tk = r.end(y2, 16);
 """ % (mode, "q4g32a.t64" if enc2 == "q4" else "q8g64s.t64"))
     res = json.loads(out.strip().splitlines()[-1])
     assert res["same"] and res["submits"] == 3
-    assert res["dispatches"] == (2 if mode == "chain" else 3)   # chain: 2 ops; graph: 2 launches + the result copy
+    assert res["dispatches"] == 3   # 2 GEMVs + the result copy (graph: 3 launches; chain: 3 ops of one launch)
     y1 = np.fromfile(str(tmp_path / "y1.bin"), np.float32)
     y2 = np.fromfile(str(tmp_path / "y2.bin"), np.float32)
     want1 = np.zeros(N1, np.float32)
@@ -448,8 +448,9 @@ def test_js_decode_loop_gemma4_shaped(tmp_path, mode):
     """engine/llm/gemma4.js:547-590's overlapped loop, unchanged in shape: token i is recorded with begin(parity) ...
     end(argBuf), submitted once its input is written, and `o32 = await pend; o32[0]` is the next id. A token is
     x = table[id] (written by the host before the submit, as the loop writes s.pler), h = W1 x' (rms), logits =
-    softcap(W2 h') (rms) with per-tile maxima, then (graph mode) argmax over the tiles into the result words; in chain
-    mode (GEMV ops only) the result is tile 0's (max, index) pair. Three tokens; each id must be the oracle's."""
+    softcap(W2 h') (rms) with per-tile maxima, then the argmax over the tiles into the result words, which end() copies
+    to the parity's staging buffer: in graph mode four recorded launches, in chain mode one launch of four chain ops.
+    Three tokens; each id must be the oracle's."""
     D, H, V = 256, 512, 1024
     w1, _ = O.pack_q4(O.randn(H * D, 41, 0.05), H, D)
     w2, _ = O.pack_q4(O.randn(V * H, 42, 0.05), V, H)
@@ -473,7 +474,6 @@ const encodeStep = () => {
   P.gemv(g, { w: { buf: w2, off: 0, enc: 'q4g32a.t64', rows: V, cols: H }, x: { buf: s.h, rowB: 0 }, N: V, K: H,
               pro: 'rms', stat: { buf: s.mx, off: (V / 64) * 2 + 1 }, norm: { buf: nw2, off: 0 }, epi: 'softcap',
               cap: 30, mx: { buf: s.mx }, y: { buf: s.logits } });
-  if (mode === 'chain') return s.mx;
   P.argmax(g, { mx: { buf: s.mx }, n: V / 64, out: { buf: s.arg } });
   return s.arg;
 };
@@ -491,10 +491,9 @@ const feed = async (id, i) => {
   tk = rec(1, 1);
   for (let i = 0; i < 3; i++) {
     const o32 = await pend; pend = null;
-    // graph: the argmax words [index, max bits]; chain: tile 0's [max bits, index] pair, its index mapped to an id
-    const idx = mode === 'chain' ? o32[1] : o32[0], bits = mode === 'chain' ? o32[0] : o32[1];
+    const idx = o32[0], bits = o32[1];   // the argmax words [index, max bits]
     words.push([idx, bits]);
-    const nxt = mode === 'chain' ? (idx * 3 + 1) %% V : idx;
+    const nxt = idx;
     ids.push(nxt);
     if (i + 1 < 3) await feed(nxt, i + 1);
     if (i + 2 < 3) tk = rec(i + 2, i & 1);
@@ -520,19 +519,15 @@ const feed = async (id, i) => {
         O.q4_gemv(capi.gemv_args(w=w2.ctypes.data, w_rows=V, w_cols=H, x=h.ctypes.data, N=V, K=H,
                                  pro=capi.PRO["rms"], epi=capi.EPI["softcap"], y=lg.ctypes.data, mx=mx.ctypes.data,
                                  stat_off=(V // 64) * 2 + 1, norm=nw2.ctypes.data, cap=30.0))
-        if mode == "chain":
-            idx, val = int(mx[1:2].view(np.uint32)[0]), mx[0]
-            nxt = (idx * 3 + 1) % V
-        else:
-            idx = int(np.argmax(lg))
-            val = lg[idx]
-            nxt = idx
+        idx = int(np.argmax(lg))
+        val = lg[idx]
+        nxt = idx
         got_idx, got_bits = res["words"][i]
         assert got_idx == idx, (i, got_idx, idx)
         assert abs(np.uint32(got_bits).view(np.float32) - val) <= 1e-4 * max(1.0, abs(val))
         assert res["ids"][i] == nxt
         cur = nxt
-    assert res["dispatches"] == 3 * (2 if mode == "chain" else 4)   # graph: 2 GEMVs + argmax + the result copy
+    assert res["dispatches"] == 3 * 4   # 2 GEMVs + argmax + the result copy (launches, or ops of one chain launch)
 
 
 def test_js_fp16_helpers_exhaustive(tmp_path):
