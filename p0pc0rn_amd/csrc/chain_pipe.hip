@@ -510,10 +510,20 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
     __builtin_amdgcn_s_waitcnt(0xC07F);
   };
   // false if the compute waves gave up meanwhile (a wave that stages its own x' gives up on its own, and the
-  // loaders then stop publishing)
+  // loaders then stop publishing), or if this wait gave up: bounded like every other wait (the loaders run at a lower
+  // wave priority; a starved loader would otherwise hold the waves here), it then marks the run timed out and stops
+  // the loaders and the other waves' waits
   auto wait_slot = [&](int q) -> bool {
-    while (ctl_ld(lctl + L::CtlFull + q % kRing) != (unsigned)q + 1) {
+    for (int spins = 0; ctl_ld(lctl + L::CtlFull + q % kRing) != (unsigned)q + 1; ++spins) {
       if (ctl_ld(lctl + L::CtlStop)) return false;
+      if (spins >= spin_limit) {
+        if (lane == 0) {
+          atomicOr(timed_out, 1u);
+          ctl_st(lctl + L::CtlStop, 1u);
+          ctl_st(lctl + L::CtlGo, 0u);
+        }
+        return false;
+      }
       __builtin_amdgcn_s_sleep(0);
     }
     return true;

@@ -68,7 +68,11 @@ class E2B:
         self.mx = mx
         self.mx_stat_off = M * NT * 2 + 1
         self.dev = {"x": capi.to_device(self.x), "nw": capi.to_device(self.nw), "st": capi.to_device(st),
-                    "mx": capi.to_device(mx)}
+                    "mx": capi.to_device(mx),
+                    # the token's tail: the rstd the token copies into the head's slot (mx's), the argmax words and
+                    # the staging buffer they are copied to
+                    "rsrc": capi.to_device(np.tile(np.array([0.0, 0.9], np.float32), M)),
+                    "arg": capi.Buffer(8 * M + 8), "stage": capi.Buffer(8 * M + 8)}
         self.out_len = {}
         for l in range(layers):
             self.out_len.update({("qkv", l): M * QKV, ("o", l): M * D, ("gu", l): M * MLP, ("dn", l): 4 * M * D})
@@ -109,17 +113,45 @@ class E2B:
             out.append((name, wk, xk, f))
         return out
 
-    def enqueue(self):
+    def enqueue(self, tail=False):
+        """the ops; tail: the whole token as bench.py times it, with the head's rstd copied into its stat slot before
+        it, the argmax over its tile maxima after it and the copy of the result words (engine/llm/gemma4.js:503-511,
+        engine/llm/drunner.js:82-90)"""
+        M = self.M
         for name, wk, xk, f in self.fields({**self.dev, **self.out}, self.w_dev):
-            if self.M == 1:
+            if name == "head" and tail:
+                for m in range(M):
+                    capi.copy(self.dev["rsrc"], (2 * m + 1) * 4, self.dev["mx"], (self.mx_stat_off + 2 * m) * 4, 4)
+            if M == 1:
                 capi.q4_gemv(capi.gemv_args(**f))
             else:
                 capi.q4_gemvM(capi.gemvm_args(**f))
+        if tail:
+            capi.argmaxM(self.dev["mx"], V // 64, M, self.dev["arg"])
+            capi.copy(self.dev["arg"], 0, self.dev["stage"], 0, 8 * M)
 
-    def reset(self):
+    def reset(self, tail=False):
         for b in self.out.values():
             b.fill_u32(NAN)
         self.dev["mx"].upload(self.mx)
+        if tail:   # the rstd slots and the result words must be written by this run
+            mx = self.mx.copy()
+            mx[self.mx_stat_off::2][:self.M] = np.nan
+            self.dev["mx"].upload(mx)
+            self.dev["arg"].fill_u32(NAN)
+            self.dev["stage"].fill_u32(NAN)
+
+    def check_tail(self, what):
+        """the argmax words and their copy against the oracle's argmax over the tile maxima the chain wrote"""
+        M, NT = self.M, V // 64
+        gmx = self.dev["mx"].read(np.float32, self.mx_len)
+        np.testing.assert_array_equal(gmx[self.mx_stat_off::2][:M], np.float32(0.9))
+        want = np.asarray(O.argmaxM(gmx, NT, M), np.uint32).ravel()
+        assert np.array_equal(self.dev["arg"].read(np.uint32, 2 * M), want), what + ": argmax"
+        assert np.array_equal(self.dev["stage"].read(np.uint32, 2 * M), want), what + ": result copy"
+        lg = self.out["head"].read(np.float32, M * V).reshape(M, V)
+        assert np.array_equal(want[0::2], np.argmax(lg, axis=1).astype(np.uint32)), what + ": argmax of the logits"
+        print(what, "argmax", want[0::2].tolist(), flush=True)
 
     def check(self, what):
         got = {k: self.out[k].read(np.float32, n) for k, n in self.out_len.items()}
@@ -186,6 +218,52 @@ def test_config_b_decode_step_as_a_recording(e2b1):
     rec.replay()
     s.check("config B graph")
     rec.free()
+
+
+def test_config_b_full_token_as_one_chain(dev):
+    """config B at full depth, as bench.py times it: 30 layers (bench.py's weight scales) + the rstd copy, the head,
+    the argmax and the result copy = 124 ops in one pipelined launch (120 mailbox hand-offs, ring wrap-arounds across
+    the whole step), twice; every op against the oracle on the input it read, the argmax and its copy exactly"""
+    s = E2B(1, layers=30, seed=9, bounded=True)
+    try:
+        ch = capi.chain(lambda: s.enqueue(tail=True))
+        info = ch.info()
+        print("chain", info, flush=True)
+        assert info["n_ops"] == 4 * 30 + 4 and info["passes"] == 1 and info["mailboxes"] == 119
+        for run in range(2):
+            s.reset(tail=True)
+            ch.run()
+            assert not ch.status()
+            s.check(f"config B full token run {run}")
+            s.check_tail(f"config B full token run {run}")
+        ch.free()
+    finally:
+        s.free()
+
+
+@pytest.mark.parametrize("M,data", [(8, "bounded"), (8, "large"), (16, "bounded")])
+def test_config_c_verify_chain_m8_m16(dev, M, data):
+    """config C's M = 8 and 16 verify chains at the E2B shapes (two layers + the head, then argmaxM over the head's tile
+    maxima), each op against the oracle on the input it read"""
+    s = E2B(M, seed=10 + M, bounded=data == "bounded")
+    try:
+        def token():
+            s.enqueue()
+            capi.argmaxM(s.dev["mx"], V // 64, M, s.dev["arg"])
+        ch = capi.chain(token)
+        info = ch.info()
+        print("chain", info, flush=True)
+        s.reset()
+        s.dev["arg"].fill_u32(NAN)
+        ch.run()
+        assert not ch.status()
+        ch.free()
+        s.check(f"config C M={M} chain {data}")
+        gmx = s.dev["mx"].read(np.float32, s.mx_len)
+        want = np.asarray(O.argmaxM(gmx, V // 64, M), np.uint32).ravel()
+        assert np.array_equal(s.dev["arg"].read(np.uint32, 2 * M), want)
+    finally:
+        s.free()
 
 
 @pytest.mark.parametrize("data", ["bounded", "large"])
