@@ -153,6 +153,31 @@ __device__ __forceinline__ float dot16_q8(const u32x4 q, const float* __restrict
   }
   return da + db;
 }
+// the 16 biased codes of q as floats, once for all M x rows (dot16_q8's conversions)
+__device__ __forceinline__ void codes16_q8(const u32x4 q, float (&f)[16]) {
+  const uint32_t u[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    f[4 * w] = (float)(u[w] & 0xFFu);
+    f[4 * w + 1] = (float)((u[w] >> 8) & 0xFFu);
+    f[4 * w + 2] = (float)((u[w] >> 16) & 0xFFu);
+    f[4 * w + 3] = (float)(u[w] >> 24);
+  }
+}
+// dot16_q8 on codes16_q8's floats: the same products in the same order
+__device__ __forceinline__ float dot16f_q8(const float (&f)[16], const float* __restrict__ x) {
+  const float4* x4 = (const float4*)x;
+  float da = 0.0f, db = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float4 xv = x4[w];
+    da = __builtin_fmaf(f[4 * w], xv.x, da);
+    db = __builtin_fmaf(f[4 * w + 1], xv.y, db);
+    da = __builtin_fmaf(f[4 * w + 2], xv.z, da);
+    db = __builtin_fmaf(f[4 * w + 3], xv.w, db);
+  }
+  return da + db;
+}
 __device__ __forceinline__ float h2f_u16(const uint8_t* p) { return (float)*(const _Float16*)p; }
 // v summed over lanes l, l ^ 8, l ^ 16, l ^ 24, ... (lane bits 3-5), with VALU lane moves only: a DPP rotation by 8
 // inside each 16-lane row, then the gfx950 row and half swaps (permlane16 / permlane32), each of which hands back
@@ -804,10 +829,13 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
       if (s.spread) {
        if (q8) {
         // q8 slots: compute wave c takes group c of every slot, lane = (row lane / 4, quarter lane % 4 of the group's
-        // 64 k); the quarters are added across the lane quad, the groups across the waves (red), as for q4
+        // 64 k); the quarters are added across the lane quad, the groups across the waves (red), as for q4; x row m's
+        // x' starts at m xgps 32 (fp32, staged by stage_x), its 32-k group sums at m xgps
         const int rr = lane >> 2, qq = lane & 3;
         for (int rp = 0; rp < nrp; ++rp) {
-          float acc = 0.0f;
+          float acc[M];
+#pragma unroll
+          for (int m = 0; m < M; ++m) acc[m] = 0.0f;
           for (int h = 0; h < s.nh; ++h) {
             const int q = q0 + rp * s.nh + h;
             wait_slot(q);
@@ -815,12 +843,20 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
             const int g = 8 * h + c;   // group of the split (< 8 nh: inside the staged x')
             const u32x4 qv = *(const u32x4l*)(slot + c * 1024 + rr * 64 + qq * 16);
             const float sc = h2f_u16(slot + 8192 + c * 32 + rr * 2);
-            float d = dot16_q8(qv, xs + g * 64 + qq * 16);
-            d += __shfl_xor(d, 1, 64);
-            d += __shfl_xor(d, 2, 64);
-            if (g < s.ngs) acc = __builtin_fmaf(sc, d - 128.0f * (xsum[2 * g] + xsum[2 * g + 1]), acc);
+            float cf[16];
+            codes16_q8(qv, cf);
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+              float d = dot16f_q8(cf, xs + m * xgps * 32 + g * 64 + qq * 16);
+              d += __shfl_xor(d, 1, 64);
+              d += __shfl_xor(d, 2, 64);
+              if (g < s.ngs)
+                acc[m] = __builtin_fmaf(sc, d - 128.0f * (xsum[m * xgps + 2 * g] + xsum[m * xgps + 2 * g + 1]), acc[m]);
+            }
           }
-          if (qq == 0) red[(rp * M * kPC + c) * 16 + rr] = acc;   // q8 chains have M = 1
+          if (qq == 0)
+#pragma unroll
+            for (int m = 0; m < M; ++m) red[((rp * M + m) * kPC + c) * 16 + rr] = acc[m];
         }
        } else if (M >= 2 && mf) {
         // M > 1 on the matrix cores: compute wave c takes groups 4c .. 4c + 3 of every slot. Per group and the slot's
@@ -1062,10 +1098,17 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
 #pragma unroll
                   for (int gl = 0; gl < 8; ++gl) {
                     const int g = 8 * h + gl;
-                    float d = dot16_q8(qv[gl], xs + g * 64 + qq * 16);
-                    d += __shfl_xor(d, 1, 64);
-                    d += __shfl_xor(d, 2, 64);
-                    if (g < s.ngs) acc[0] = __builtin_fmaf(sc[gl], d - 128.0f * (xsum[2 * g] + xsum[2 * g + 1]), acc[0]);
+                    float cf[16];
+                    codes16_q8(qv[gl], cf);
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                      float d = dot16f_q8(cf, xs + m * xgps * 32 + g * 64 + qq * 16);
+                      d += __shfl_xor(d, 1, 64);
+                      d += __shfl_xor(d, 2, 64);
+                      if (g < s.ngs)
+                        acc[m] = __builtin_fmaf(sc[gl], d - 128.0f * (xsum[m * xgps + 2 * g] + xsum[m * xgps + 2 * g + 1]),
+                                                acc[m]);
+                    }
                   }
                   continue;
                 }
@@ -1092,7 +1135,9 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
                 }
               }
               if (q8) {
-                if ((lane & 3) == 0) wred[pt * 64 + r * 16 + (lane >> 2)] = acc[0];   // q8 chains have M = 1
+                if ((lane & 3) == 0)
+#pragma unroll
+                  for (int m = 0; m < M; ++m) wred[(m * 2 + pt) * 64 + r * 16 + (lane >> 2)] = acc[m];
                 continue;
               }
               if (M >= 2 && mf) {   // D[m][n] -> wred: x row m in lanes l / 16 == m / 4, weight row n = l % 16
@@ -1143,10 +1188,10 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
 chain_kernel_t pipe_chain_kernel(int M, bool q8) {
   switch (M) {
     case 1: return q8 ? q4_chain_pipe_kernel<1, true> : q4_chain_pipe_kernel<1, false>;
-    case 2: return q4_chain_pipe_kernel<2, false>;
-    case 3: return q4_chain_pipe_kernel<3, false>;
-    case 4: return q4_chain_pipe_kernel<4, false>;
-    case 5: return q4_chain_pipe_kernel<5, false>;
+    case 2: return q8 ? q4_chain_pipe_kernel<2, true> : q4_chain_pipe_kernel<2, false>;
+    case 3: return q8 ? q4_chain_pipe_kernel<3, true> : q4_chain_pipe_kernel<3, false>;
+    case 4: return q8 ? q4_chain_pipe_kernel<4, true> : q4_chain_pipe_kernel<4, false>;
+    case 5: return q8 ? q4_chain_pipe_kernel<5, true> : q4_chain_pipe_kernel<5, false>;
   }
   return nullptr;
 }

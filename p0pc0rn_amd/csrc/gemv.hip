@@ -414,7 +414,7 @@ static size_t plan_staged(GemvP& p, int M, int W, int G, int& cur) {
 // where the previous op stopped so each workgroup streams about the same bytes over a step. A share of at most a
 // ring's worth of slots (and few enough rows) is computed by all compute waves together, a larger one by one wave per
 // unit. Returns false (the chain then runs on q4_gemv_chain_kernel) when the weights are not 16-byte aligned
-// (LDS-DMA loads), a workgroup would get units of two splits, or (M > 1) a split exceeds 2048 k or an op is q8.
+// (LDS-DMA loads), a workgroup would get units of two splits, or (M > 1) a split exceeds 2048 k.
 static bool plan_pipe(std::vector<GemvP>& ops, int G, int M) {
   int cur = 0;
   for (GemvP& p : ops) {
@@ -424,7 +424,7 @@ static bool plan_pipe(std::vector<GemvP>& ops, int G, int M) {
       continue;
     }
     if ((uintptr_t)p.w & 15) return false;
-    if (M > 1 && (p.kPer > 2048 || p.enc != P0_ENC_Q4G32A_T64)) return false;
+    if (M > 1 && p.kPer > 2048) return false;
     const int nrb = p.epi == P0_EPI_SOFTCAP ? 4 : 1, parts = p.epi == P0_EPI_GEGLU ? 2 : 1;
     const int64_t U = (int64_t)(p.N / (kStageRows * nrb)) * p.nsplit;
     if (U > G && G % p.nsplit) return false;
@@ -473,7 +473,7 @@ static int launch(GemvP& p, int M, const char* op) {
     return P0_EINVAL;
   }
   if (cb && p.enc == P0_ENC_Q8G64S_T64) {
-    // q8g64s.t64 ops run only on the pipelined M = 1 kernel (p0_chain_end refuses a chain that cannot take them)
+    // q8g64s.t64 ops run only on the pipelined kernel (p0_chain_end refuses a chain that cannot take them)
     p.coh = 0;
     cb->ops.push_back(p);
     cb->q8 = true;
@@ -807,6 +807,7 @@ static int build_row_groups(const ChainBuild* cb, ChainExec** out) {
     sub.G = cb->G;
     sub.lds = cb->lds;
     sub.aux = cb->aux;
+    sub.q8 = cb->q8;   // the kernel instantiation that carries the q8 code
     const int64_t m0 = gs[g];
     for (GemvP p : cb->ops) {
       if (p.kind != kOpGemv) {   // argmax / rowstats / normadd over the chain's rows (rows_independent checked)
@@ -872,7 +873,7 @@ extern "C" int p0_chain_end(void** out) {
     cb->G = ctx().cu_count * (cb->W == 16 ? 1 : 2);
   }
   ChainExec* ex = nullptr;
-  if (cb->M > pipe_max_m() && g_chain_stage && g_chain_pipe_m && !cb->q8) {
+  if (cb->M > pipe_max_m() && g_chain_stage && g_chain_pipe_m) {
     if (int r = build_row_groups(cb, &ex)) return r;
   }
   if (!ex) {
@@ -947,7 +948,8 @@ static int build_exec(ChainBuild* cb, bool pipe_only, ChainExec** out) {
     return P0_EINVAL;
   }
   if (cb->q8 && !pipe) {
-    set_error("p0_chain_end: q8g64s.t64 ops join only pipelined chains (M = 1, 16-byte aligned weights, knob 4 on)");
+    set_error("p0_chain_end: q8g64s.t64 ops join only pipelined chains (M <= 5 or rows that share no memory, "
+              "16-byte aligned weights, splits of at most 2048 k for M > 1, knobs 4 and 8 on)");
     return P0_EINVAL;
   }
   mark_coherence(cb->ops, cb->M);

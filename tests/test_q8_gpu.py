@@ -3,8 +3,9 @@
 Every q8 shape the reference ships (engine/tune/kshipped.js:14, run as kshipped.js:17-41 runs it: 128 rows at the real
 K, its kPer rule, seeds 33 + K / 34 + K / 35 + K) under the reference's own acceptance (cos > 0.99999, the tile argmax)
 and this build's bars (relative L2 <= 1e-3 and <= 2e-5), the expected rows in float64 from numpy over the decoded
-records (tests/test_q8_oracle.py pins the packer and the decode); gemvM with M rows against the oracle; q8 ops inside a
-pipelined chain, mixed with q4 ops, against the oracle; and a gemvM chain holding a q8 op is refused."""
+records (tests/test_q8_oracle.py pins the packer and the decode); gemvM with M rows against the oracle; q8 ops inside
+pipelined chains of M = 1 (decode) and M = 3, 5, 8 (verify) rows, mixed with q4 ops, against the oracle; and a chain
+holding a q8 op is refused where only the general chain kernel would run it."""
 import math
 
 import numpy as np
@@ -182,12 +183,92 @@ def test_q8_ops_in_a_pipelined_chain(dev):
         v.free()
 
 
+@pytest.mark.parametrize("M", [3, 5, 8])
+def test_q8_ops_in_a_verify_chain(dev, M):
+    """A verify-pass chain (gemvM, M rows) mixing q4g32a.t64 and q8g64s.t64 ops as the real E2B pack does
+    (p0pc0rn.config.json:207, its q8 shapes at engine/tune/tunecore.js:17-21): q8 ops with raw and rms prologues, a q8
+    geglu, a q8 op reading one K-split of a q4 op, a large q8 softcap share (one wave per unit) and argmaxM after it;
+    M = 3 and 5 as one pipelined launch, M = 8 as pipelined row-group passes. Each op against the oracle on the input it
+    read on the GPU, every intermediate NaN-filled before the run."""
+    ops = [   # (name, enc, w rows, N, K, kPer, pro, epi, input, x row stride)
+        ("a", "q4", 768, 768, 512, 0, "rms", "store", "x", 512),
+        ("b", "q8", 512, 512, 512, 0, "raw", "store", "a", 768),      # the first 512 of a's 768 outputs per row
+        ("c", "q8", 2048, 1024, 512, 0, "rms", "geglu", "b", 512),
+        ("d", "q4", 512, 512, 1024, 512, "raw", "store", "c", 1024),  # 2 K-splits
+        ("e", "q8", 512, 512, 512, 0, "rms", "store", "d", 512),      # d's first split
+        ("f", "q8", 32768, 32768, 512, 0, "rms", "softcap", "e", 512),
+    ]
+    host = {n: (_q8 if enc == "q8" else _q4)(rows, K, 610 + i)
+            for i, (n, enc, rows, N, K, kPer, pro, epi, src, ld) in enumerate(ops)}
+    x0 = O.randn(M * 512, 620)
+    nw = nw_of(1024)
+    st = np.zeros(2 * M, np.float32)
+    st[1::2] = 0.8
+    NT = 32768 // 64
+    mx0 = np.zeros(M * NT * 2 + 2 * M, np.float32)
+    mx0[M * NT * 2 + 1::2] = 0.9
+    nsplit = {o[0]: (-(-o[4] // o[5]) if o[5] else 1) for o in ops}
+    olen = {o[0]: M * o[3] * (nsplit[o[0]] if o[7] == "store" else 1) for o in ops}
+    dw = {n: capi.to_device(w) for n, w in host.items()}
+    d = {"x": capi.to_device(x0), "nw": capi.to_device(nw), "st": capi.to_device(st), "mx": capi.to_device(mx0),
+         "arg": capi.Buffer(8 * M)}
+    out = {n: capi.Buffer(4 * olen[n]) for n in olen}
+
+    def fields(o, b, w):
+        n, enc, rows, N, K, kPer, pro, epi, src, ld = o
+        f = dict(w=w[n], w_enc=1 if enc == "q4" else 2, w_rows=rows, w_cols=K, x=b[src], x_ldx=ld, M=M, N=N, K=K,
+                 kPer=kPer, pro=capi.PRO[pro], epi=capi.EPI[epi], y=b[n], y_ldm=N, y_ldy=M * N, norm=b["nw"],
+                 stat=b["st"], stat_off=1, stat_ld=2)
+        if epi == "softcap":
+            f.update(mx=b["mx"], stat=b["mx"], stat_off=M * NT * 2 + 1, cap=30.0)
+        return f
+
+    def token():
+        for o in ops:
+            capi.q4_gemvM(capi.gemvm_args(**fields(o, {**d, **out}, dw)))
+        capi.argmaxM(d["mx"], NT, M, d["arg"])
+
+    ch = capi.chain(token)
+    info = ch.info()
+    print("mixed q4 / q8 verify chain", info, flush=True)
+    assert info["workgroups"] == capi.device_info()["cu_count"] and info["passes"] == (1 if M <= 5 else 2)
+    for b in out.values():
+        b.fill_u32(0x7FC00000)
+    d["arg"].fill_u32(0x7FC00000)
+    ch.run()
+    assert not ch.status()
+    got = {n: out[n].read(np.float32) for n in out}
+    gmx = d["mx"].read(np.float32)
+    mxh = mx0.copy()
+    for o in ops:
+        n, src = o[0], o[8]
+        xin = np.ascontiguousarray(x0 if src == "x" else got[src], np.float32)
+        y = np.full(olen[n], np.nan, np.float32)
+        hb = {"x": xin.ctypes.data, src: xin.ctypes.data, n: y.ctypes.data, "nw": nw.ctypes.data,
+              "st": st.ctypes.data, "mx": mxh.ctypes.data}
+        O.q4_gemvM(capi.gemvm_args(**fields(o, hb, {n: host[n].ctypes.data})))
+        r = rel_l2(got[n], y)
+        print(f"M={M} op {n} ({o[1]} {o[6]}.{o[7]} {o[3]}x{o[4]}): rel_l2 {r:.3e}", flush=True)
+        assert np.all(np.isfinite(got[n])) and r <= 2e-5, n
+    assert np.allclose(gmx[:2 * M * NT:2], mxh[:2 * M * NT:2], rtol=1e-5, atol=1e-5)
+    want = np.asarray(O.argmaxM(gmx, NT, M), np.uint32).ravel()
+    assert np.array_equal(d["arg"].read(np.uint32), want)
+    ch.free()
+    for v in list(dw.values()) + list(d.values()) + list(out.values()):
+        v.free()
+
+
 def test_q8_ops_join_only_pipelined_chains(dev):
-    """q8 ops need the pipelined M = 1 kernel: a gemvM chain holding one is refused at p0_chain_end"""
+    """q8 ops need the pipelined kernel: with it switched off (p0_chain_tune knob 4) a chain holding one is refused at
+    p0_chain_end"""
     N, K, M = 128, 256, 2
     wb, xb, yb = capi.to_device(_q8(N, K, 5)), capi.Buffer(M * K * 4), capi.Buffer(M * N * 4)
-    with pytest.raises(capi.P0Error, match="q8g64s.t64 ops join only pipelined chains"):
-        capi.chain(lambda: capi.q4_gemvM(capi.gemvm_args(w=wb, w_enc=2, w_rows=N, w_cols=K, x=xb, M=M, N=N, K=K,
-                                                         y=yb)))
+    old = capi.chain_tune(4, 0)
+    try:
+        with pytest.raises(capi.P0Error, match="q8g64s.t64 ops join only pipelined chains"):
+            capi.chain(lambda: capi.q4_gemvM(capi.gemvm_args(w=wb, w_enc=2, w_rows=N, w_cols=K, x=xb, M=M, N=N, K=K,
+                                                             y=yb)))
+    finally:
+        capi.chain_tune(4, old)
     for v in (wb, xb, yb):
         v.free()
