@@ -219,11 +219,16 @@ int p0_gemv_tune(int knob, int value);
 
 /* ---- GEMV chains: a decode step's GEMVs in ONE persistent launch (engine/llm/drunner.js:1-8, 83-101) ------------- */
 /* Between p0_chain_begin and p0_chain_end, p0_q4_gemv / p0_q4_gemvM calls are validated and planned as usual but
- * appended to the chain instead of launched (all ops of a chain have the same M). p0_chain_run enqueues the whole
- * chain as one kernel (a chain of 6-16 rows whose rows use disjoint memory, i.e. no row of a buffer that one row group
- * writes is touched by another, as one pipelined kernel per group of at most 5 rows, launched back to back): op i
- * starts its arithmetic once op i - 1 has written all of its outputs (so op i may read anything earlier ops wrote),
- * and each workgroup streams op i's first weights while it waits. Buffers are bound at p0_chain_end; a chain runs any
+ * appended to the chain instead of launched (all GEMV ops of a chain have the same M); p0_copy, p0_argmax /
+ * p0_argmaxM, p0_rowstats and p0_normadd calls join the chain too (their results equal the standalone ops' bit for
+ * bit), so a whole decode token, its argmax and result copy included, is one launch. Every other op (the GEMM, the
+ * dequant, uploads) is refused while a chain is being built. p0_chain_run enqueues the whole chain as one kernel: the
+ * pipelined kernel for M <= 5, the wide pipelined kernel for 6 - 16 rows (q4g32a.t64 ops with raw or rms prologues;
+ * otherwise, where the rows use disjoint memory, i.e. no row of a buffer that one row group writes is touched by
+ * another, one pipelined kernel per group of at most 5 rows, launched back to back): op i starts its arithmetic once
+ * op i - 1 has written all of its outputs (so op i may read anything earlier ops wrote), and each workgroup streams op
+ * i's first weights while it waits. Chains holding copy / argmax / rowstats / normadd or q8g64s.t64 ops run only on the
+ * pipelined kernels (p0_chain_end refuses them otherwise). Buffers are bound at p0_chain_end; a chain runs any
  * number of times, also inside p0_record_begin / p0_record_end. Every wait is bounded: a wait that gives up (which
  * needs another kernel holding the GPU's CUs meanwhile) marks the chain, and p0_chain_status (which waits for the
  * stream) returns 1 once in *timed_out and resets the chain and the split-K counters; the results of that run are
@@ -234,7 +239,7 @@ typedef struct {
   int64_t lds_bytes;
   int32_t mailboxes;   /* ops that take their input from the previous op's mailbox (p0_chain_tune knob 7) */
   int32_t staged;      /* M > 1: ops that take their x' staged by the previous op (p0_chain_tune knob 10) */
-  int32_t passes;      /* launches per run: 1, or, for M = 6-16 rows on the pipelined kernel, one per row group */
+  int32_t passes;      /* launches per run: 1, or, for 6-16 rows as row-group passes, one per row group */
 } p0_chain_info_t;
 int p0_chain_begin(void);
 int p0_chain_end(void** chain_out);
@@ -257,8 +262,10 @@ int p0_chain_free(void* chain);
  * matrix cores (default 3: M = 2 runs faster on the fp32 VALU; 6 = never); knob 10: 1 = in pipelined M > 1 chains on
  * the matrix cores an op that reads one split of the previous op's output takes its x' as that op staged it (the
  * default), 0 = every op stages its own x' after its wait; knob 11: LDS slots each loader keeps in flight in chains of
- * M > 1 rows (1 or 2, default 1). Knobs 0-1 and 4-11 apply to chains begun afterwards, 2-3 to runs. value < 0 only
- * queries (knobs 0-2 also ignore 0); returns the previous value. */
+ * M = 2-5 rows (1 or 2, default 1); knob 12: 1 = chains of 6-16 rows on the wide pipelined kernel, one pass (the
+ * default), 0 = as row-group passes; knob 13: LDS slots each loader keeps in flight in the wide kernel (1 or 2, default
+ * 2). Knobs 0-1 and 4-13 apply to chains begun afterwards, 2-3 to runs. value < 0 only queries (knobs 0-2 also ignore
+ * 0); returns the previous value. */
 int p0_chain_tune(int knob, int value);
 
 /* ---- the GEMV's producer and consumers: row statistics, split-K sum + residual RMS, argmax over tile maxima ------- */

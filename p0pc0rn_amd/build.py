@@ -23,7 +23,7 @@ NAPI = os.path.join(PKG, "js", "p0pc0rn.node")
 ORACLE_DIR = os.path.join(ROOT, "oracle")
 ORACLE = os.path.join(ORACLE_DIR, "libq4oracle.so")
 
-HIP_SOURCES = ["runtime.hip", "gemv.hip", "chain_pipe.hip", "gemv_m01_04.hip", "gemv_m05_08.hip", "gemv_m09_12.hip",
+HIP_SOURCES = ["runtime.hip", "gemv.hip", "chain_pipe.hip", "chain_wide.hip", "gemv_m01_04.hip", "gemv_m05_08.hip", "gemv_m09_12.hip",
                "gemv_m13_16.hip", "gemm.hip", "util.hip", "misc.hip", "gemv_q8.hip", "pack.hip"]
 # packed-fp32 instructions are disabled on purpose: hipcc -O3 would otherwise pair fp32 ops into v_pk_*_f32
 HIPCC_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",

@@ -123,6 +123,8 @@ static int g_chain_pipe_m = 1;          // gemvM chains (M <= 5) on the pipeline
 static int g_pipe_loaders = 2;          // pipelined chain: loader waves that stream
 static int g_pipe_depth = 2;            // pipelined M = 1 chain: slots in flight per loader wave
 static int g_pipe_depth_m = 1;          // pipelined M > 1 chain: the same (measured: 1 is 1-2.5% faster at M = 2-5)
+static int g_chain_wide = 1;            // chains of 6-16 rows in one pass of the wide kernel (1) or as row groups (0)
+static int g_wide_depth = 2;            // wide chain: slots in flight per loader wave (measured: 2 is 2% faster at M >= 12)
 static constexpr size_t kChainLds = 64 * 1024;
 static constexpr size_t kChainLdsMax = 160 * 1024 - 256;   // gfx950: LDS per CU, less the kernel's static LDS
 
@@ -437,6 +439,34 @@ static bool plan_pipe(std::vector<GemvP>& ops, int G, int M) {
     p.scur = cur;
     p.snrb = nrb;
     p.sngp = spread ? 1 : 0;
+    cur = (int)((cur + U) % G);
+  }
+  return true;
+}
+
+// Plan of a chain of 6 - 16 rows for the wide pipelined kernel (chain_wide.hip) on G workgroups: the pipelined
+// kernel's units and positions, every share computed by all compute waves (in rounds of at most 4 16-row parts).
+// Returns false (row-group passes, or the general kernel, take the chain) when an op is q8, has a prologue other than
+// raw or rms, a split of more than 2048 k, weights not 16-byte aligned (LDS-DMA loads), or a workgroup would get units
+// of two splits.
+static bool plan_wide(std::vector<GemvP>& ops, int G) {
+  int cur = 0;
+  for (GemvP& p : ops) {
+    if (p.kind != kOpGemv) {
+      p.su = 0;
+      p.scur = cur;
+      continue;
+    }
+    if ((uintptr_t)p.w & 15) return false;
+    if (p.enc != P0_ENC_Q4G32A_T64 || p.kPer > 2048 || (p.pro != P0_PRO_RAW && p.pro != P0_PRO_RMS)) return false;
+    const int nrb = p.epi == P0_EPI_SOFTCAP ? 4 : 1;
+    const int64_t U = (int64_t)(p.N / (kStageRows * nrb)) * p.nsplit;
+    if (U > G && G % p.nsplit) return false;
+    p.su = (int)U;
+    p.scur = cur;
+    p.snrb = nrb;
+    p.sngp = 1;
+    p.mf = 1;
     cur = (int)((cur + U) % G);
   }
   return true;
@@ -873,8 +903,10 @@ extern "C" int p0_chain_end(void** out) {
     cb->G = ctx().cu_count * (cb->W == 16 ? 1 : 2);
   }
   ChainExec* ex = nullptr;
-  if (cb->M > pipe_max_m() && g_chain_stage && g_chain_pipe_m) {
-    if (int r = build_row_groups(cb, &ex)) return r;
+  if (cb->M > pipe_max_m()) {   // one pass of the wide kernel, else passes over row groups, else the general kernel
+    if (int r = build_exec(cb, true, &ex)) return r;
+    if (!ex && g_chain_stage && g_chain_pipe_m)
+      if (int r = build_row_groups(cb, &ex)) return r;
   }
   if (!ex) {
     if (int r = build_exec(cb, false, &ex)) return r;
@@ -941,6 +973,23 @@ static int build_exec(ChainBuild* cb, bool pipe_only, ChainExec** out) {
       pipe = true;
     }
   }
+  // 6 - 16 rows: the wide pipelined kernel, one workgroup per CU, when every op can be planned for it
+  if (!pipe && cb->M > pipe_max_m() && cb->M <= wide_max_m() && g_chain_stage && g_chain_wide && !cb->q8) {
+    chain_kernel_t wk = wide_chain_kernel(cb->M);
+    const int wlds = wide_lds_bytes(cb->M);
+    P0_HIP(hipFuncSetAttribute((const void*)wk, hipFuncAttributeMaxDynamicSharedMemorySize, wlds), "p0_chain_end");
+    int pc = 0;
+    P0_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, (const void*)wk, 64 * pipe_waves(), wlds), "p0_chain_end");
+    std::vector<GemvP> planned = cb->ops;
+    if (pc >= 1 && plan_wide(planned, ctx().cu_count)) {
+      cb->ops = planned;
+      k = wk;
+      cb->W = pipe_waves();
+      grid = ctx().cu_count;
+      lds = wlds;
+      pipe = true;
+    }
+  }
   if (pipe_only && !pipe) return P0_OK;
   if (cb->aux && !pipe) {
     set_error("p0_chain_end: copy, argmax, rowstats and normadd ops join only pipelined chains (M <= 5 or rows that "
@@ -971,7 +1020,7 @@ static int build_exec(ChainBuild* cb, bool pipe_only, ChainExec** out) {
   ex->kernel = k;
   if (pipe) {
     ex->pipe_cfg[0] = g_pipe_loaders;
-    ex->pipe_cfg[1] = cb->M > 1 ? g_pipe_depth_m : g_pipe_depth;
+    ex->pipe_cfg[1] = cb->M > pipe_max_m() ? g_wide_depth : cb->M > 1 ? g_pipe_depth_m : g_pipe_depth;
   }
   // chain state: last tag, timed out, the workgroups' lines and the completion counters (one 128-byte line each)
   const size_t mb_base = (chain_state_words((int)cb->ops.size(), grid) + 63) & ~(size_t)63;   // 256-byte aligned
@@ -1084,6 +1133,11 @@ extern "C" int p0_chain_free(void* chain) {
 // default) or the general one (0). Returns the previous value; a value < 0 only reads (knobs 3, 4, 7 and 8 also
 // take 0).
 extern "C" int p0_chain_tune(int knob, int value) {
+  if (knob == 12) {
+    const int old = g_chain_wide;
+    if (value >= 0) g_chain_wide = value ? 1 : 0;
+    return old;
+  }
   if (knob == 9) {
     const int old = g_pipe_mf_min_m;
     if (value > 0) g_pipe_mf_min_m = value;
@@ -1110,8 +1164,8 @@ extern "C" int p0_chain_tune(int knob, int value) {
     if (value >= 0) g_chain_stage = value ? 1 : 0;
     return old;
   }
-  if (knob == 5 || knob == 6 || knob == 11) {
-    int* t = knob == 5 ? &g_pipe_loaders : knob == 6 ? &g_pipe_depth : &g_pipe_depth_m;
+  if (knob == 5 || knob == 6 || knob == 11 || knob == 13) {
+    int* t = knob == 5 ? &g_pipe_loaders : knob == 6 ? &g_pipe_depth : knob == 11 ? &g_pipe_depth_m : &g_wide_depth;
     const int old = *t;
     if (value > 0) *t = knob == 5 ? (value > 4 ? 4 : value) : (value >= 2 ? 2 : 1);
     return old;

@@ -1043,6 +1043,11 @@ int pipe_ring_slots(int M);
 int pipe_spread_parts(int M);
 int pipe_max_m();
 int pipe_cfg_word();   // state word of the loader count (the next word: slots in flight per loader)
+// the wide pipelined chain (chain_wide.hip) for pipe_max_m() < M <= wide_max_m() rows of x, one pass
+chain_kernel_t wide_chain_kernel(int M);
+int wide_lds_bytes(int M);
+int wide_ring_slots(int M);
+int wide_max_m();
 
 #define P0_GEMV_EXTERN(M) \
   extern template gemv_kernel_t pick_m<M>(int); \

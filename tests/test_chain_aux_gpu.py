@@ -120,9 +120,10 @@ class TokenStep(MiniStep):
             b.free()
 
 
-@pytest.mark.parametrize("M", [1, 3, 5])
+@pytest.mark.parametrize("M", [1, 3, 5, 8, 16])
 def test_token_chain_ends_in_argmax_and_result_copy(dev, M):
-    """a whole token as one chain (M = 1 decode, M = 3 and 5 verify passes on the pipelined kernel): the
+    """a whole token as one chain (M = 1 decode, M = 3 and 5 verify passes on the pipelined kernel, 8 and 16 on the wide
+    one): the
     head reads the rstd the chain copied, the argmax reads the head's tile maxima, the staging buffer gets the argmax
     words; each op against the oracle on the input it read, the argmax against the oracle's over the head's maxima"""
     print("case token chain M", M, flush=True)
@@ -153,9 +154,11 @@ def test_token_chain_ends_in_argmax_and_result_copy(dev, M):
     s.free_token()
 
 
-def test_row_group_passes_end_in_argmaxM(dev):
-    """M = 8 verify rows as row-group passes (rows that share no memory): argmaxM over the head's tile maxima is a row op
-    and moves with each group's rows; against the oracle's argmax of the maxima the chain wrote"""
+@pytest.mark.parametrize("wide", [1, 0])
+def test_row_group_passes_end_in_argmaxM(dev, wide):
+    """M = 8 verify rows in one pass of the wide kernel, and (knob 12 off) as row-group passes (rows that share no
+    memory: argmaxM over the head's tile maxima is a row op and moves with each group's rows); against the oracle's
+    argmax of the maxima the chain wrote"""
     M = 8
     s = MiniStep(M=M, gemvM=True)
     NT = s.V // 64
@@ -165,8 +168,12 @@ def test_row_group_passes_end_in_argmaxM(dev):
         s._enqueue()
         capi.argmaxM(s.dev["mx"], NT, M, arg)
 
-    ch = capi.chain(token)
-    assert ch.info()["passes"] == 2, ch.info()
+    old = capi.chain_tune(12, wide)
+    try:
+        ch = capi.chain(token)
+    finally:
+        capi.chain_tune(12, old)
+    assert ch.info()["passes"] == (1 if wide else 2), ch.info()
     s.reset_outputs()
     arg.fill_u32(NAN)
     ch.run()

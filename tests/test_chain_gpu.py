@@ -137,8 +137,8 @@ class MiniStep:
 @pytest.mark.parametrize("M,gemvM,pipe_m", [(1, False, 1), (1, True, 1), (2, True, 1), (3, True, 1), (5, True, 1),
                                              (5, True, 0), (8, True, 1)])
 def test_chain_matches_oracle(dev, M, gemvM, pipe_m):
-    """M <= 5 rows run on the pipelined kernel in one launch and M = 8 as two row-group passes (knob 8 on); knob 8 off
-    puts M = 5 on the general kernel"""
+    """M <= 5 rows run on the pipelined kernel in one launch and M = 8 on the wide pipelined kernel, also one launch
+    (knob 8 on); knob 8 off puts M = 5 on the general kernel"""
     s = MiniStep(M=M, gemvM=gemvM, seed=10 + M)
     old = capi.chain_tune(8, pipe_m)
     try:
@@ -148,8 +148,8 @@ def test_chain_matches_oracle(dev, M, gemvM, pipe_m):
     info = ch.info()
     print("chain", info, flush=True)
     assert info["n_ops"] == 6 and info["m"] == M
-    if pipe_m:   # M > 5: pipelined passes over row groups of at most 5 rows
-        assert info["waves_per_workgroup"] == 12 and info["passes"] == (M + 4) // 5
+    if pipe_m:
+        assert info["waves_per_workgroup"] == 12 and info["passes"] == 1
     else:
         assert info["waves_per_workgroup"] == 8 and info["passes"] == 1
     if M == 1 and info["waves_per_workgroup"] == 12:
@@ -165,16 +165,21 @@ def test_chain_matches_oracle(dev, M, gemvM, pipe_m):
     s.free()
 
 
-@pytest.mark.parametrize("M", [6, 11, 16])
-def test_chain_row_group_passes(dev, M):
-    """a gemvM chain of 6-16 rows runs as pipelined passes over row groups of at most 5 rows (6 = 3 + 3,
-    11 = 4 + 4 + 3, 16 = 4 x 4), one launch each: every op against the oracle, a rerun, and replays of a recording of
-    the run (bit-identical to the eager run)"""
+@pytest.mark.parametrize("M,wide", [(6, 0), (11, 0), (16, 0), (6, 1), (8, 1), (11, 1), (16, 1)])
+def test_chain_row_group_passes(dev, M, wide):
+    """a gemvM chain of 6-16 rows runs in one launch of the wide pipelined kernel (p0_chain_tune knob 12 on, the
+    default), or, with it off, as pipelined passes over row groups of at most 5 rows (6 = 3 + 3, 11 = 4 + 4 + 3,
+    16 = 4 x 4), one launch each: every op against the oracle, a rerun, and replays of a recording of the run
+    (bit-identical to the eager run)"""
     s = MiniStep(M=M, gemvM=True, seed=70 + M)
-    ch = s.make_chain()
+    old = capi.chain_tune(12, wide)
+    try:
+        ch = s.make_chain()
+    finally:
+        capi.chain_tune(12, old)
     info = ch.info()
     print("chain", info, flush=True)
-    assert info["passes"] == (M + 4) // 5 and info["waves_per_workgroup"] == 12 and info["m"] == M
+    assert info["passes"] == (1 if wide else (M + 4) // 5) and info["waves_per_workgroup"] == 12 and info["m"] == M
     for r in range(2):
         s.reset_outputs()
         ch.run()
@@ -195,10 +200,12 @@ def test_chain_row_group_passes(dev, M):
     s.free()
 
 
-def test_chain_rows_sharing_memory_take_the_general_kernel(dev):
+@pytest.mark.parametrize("wide", [1, 0])
+def test_chain_rows_sharing_memory_take_the_general_kernel(dev, wide):
     """rows of different row groups that share memory (op 1 reads x rows 128 floats apart, each 256 long: row m reads
-    op 0's output around its row m / 2, so rows 4-7 read rows 2-3) cannot run as row-group passes: the chain takes the
-    general kernel, one launch, and matches the oracle"""
+    op 0's output around its row m / 2, so rows 4-7 read rows 2-3) run in one pass of the wide kernel, which needs no
+    row independence; with it off (knob 12) they cannot run as row-group passes, and the chain takes the general
+    kernel, one launch; both match the oracle"""
     M, N0, K = 8, 256, 256
     w0, w1 = _w(N0, K, 81), _w(128, K, 82)
     x = O.randn(M * K, 83)
@@ -218,10 +225,14 @@ def test_chain_rows_sharing_memory_take_the_general_kernel(dev):
 
     for k in ("y0", "y1"):
         dv[k].fill_u32(NAN)
-    ch = capi.chain(enqueue)
+    old = capi.chain_tune(12, wide)
+    try:
+        ch = capi.chain(enqueue)
+    finally:
+        capi.chain_tune(12, old)
     info = ch.info()
     print("chain", info, flush=True)
-    assert info["passes"] == 1 and info["waves_per_workgroup"] == 8
+    assert info["passes"] == 1 and info["waves_per_workgroup"] == (12 if wide else 8)
     ch.run()
     assert not ch.status()
     g0 = dv["y0"].read(np.float32, M * N0)

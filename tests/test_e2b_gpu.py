@@ -241,10 +241,13 @@ def test_config_b_full_token_as_one_chain(dev):
         s.free()
 
 
-@pytest.mark.parametrize("M,data", [(8, "bounded"), (8, "large"), (16, "bounded")])
+@pytest.mark.parametrize("M,data", [(8, "bounded"), (8, "large"), (16, "bounded"), (16, "large"), (6, "bounded"),
+                                    (12, "large")])
 def test_config_c_verify_chain_m8_m16(dev, M, data):
-    """config C's M = 8 and 16 verify chains at the E2B shapes (two layers + the head, then argmaxM over the head's tile
-    maxima), each op against the oracle on the input it read"""
+    """config C's verify chains of 6 - 16 rows at the E2B shapes (two layers + the head, then argmaxM over the head's
+    tile maxima) in one pass of the wide kernel, each op against the oracle on the input it read; with large
+    activations the producer's 2^8 staging overflows from the second layer on and the waves stage x' with their own
+    scale"""
     s = E2B(M, seed=10 + M, bounded=data == "bounded")
     try:
         def token():
@@ -253,6 +256,7 @@ def test_config_c_verify_chain_m8_m16(dev, M, data):
         ch = capi.chain(token)
         info = ch.info()
         print("chain", info, flush=True)
+        assert info["passes"] == 1 and info["waves_per_workgroup"] == 12 and info["staged"] == 4 * s.L
         s.reset()
         s.dev["arg"].fill_u32(NAN)
         ch.run()
