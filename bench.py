@@ -46,7 +46,7 @@ def log(*a):
 class Step:
     """The decode step's weights and buffers (device), and its op sequence for M rows."""
 
-    def __init__(self, capi, seed=0):
+    def __init__(self, capi, seed=0, baseline_scales=False):
         self.c = capi
         c = capi
         self.layers = []
@@ -57,8 +57,12 @@ class Step:
         # layer by layer from O(1) towards 0 (a fixed slot cannot hold it at 1: that balance is unstable, and rounding
         # differences between paths would grow into inf). Values never reach inf or NaN, so an M > 1 verify pass keeps
         # its matrix-core path (it falls back to the VALU for |x'| >= 255) and every path runs what a model's step runs.
+        # baseline_scales: BASELINE's |N(0, 0.02)| scales for every layer instead (the activations then grow ~4x per op,
+        # and x' leaves the range of the matrix cores' fixed 2^8 staging from the second layer on)
         sigma = {"qkv": 1 / np.sqrt(21.5 * D), "o": 1 / np.sqrt(21.5 * D), "gu": 1 / np.sqrt(21.5 * D),
                  "down": 1.55 / np.sqrt(21.5 * MLP)}
+        if baseline_scales:
+            sigma = {k: 0.02 for k in sigma}
         for l in range(LAYERS):
             t = {}
             for name, (n, k) in (("qkv", (QKV, D)), ("o", (D, D)), ("gu", (2 * MLP, D)), ("down", (D, MLP))):
@@ -69,7 +73,8 @@ class Step:
         self.head = c.Buffer(VOCAB // 64 * D // 32 * 1280)
         c.fill_q4_sym(self.head, VOCAB, D, seed * 7919 + 999, 0.02)
         self.weight_bytes = sum(b.nbytes for t in self.layers for (b, n, k) in t.values()) + self.head.nbytes
-        self.nw = c.to_device((np.linspace(0.8, 1.2, D) * (1 - 2 * (np.arange(D) % 2))).astype(np.float32))
+        nw = np.linspace(0.8, 1.2, D) * (1 if baseline_scales else 1 - 2 * (np.arange(D) % 2))
+        self.nw = c.to_device(nw.astype(np.float32))
         self.M = 0
 
     def alloc(self, M):
@@ -96,6 +101,13 @@ class Step:
         self.rsrc = c.to_device(np.tile(np.array([0.0, 1.0], np.float32), M))
         self.arg = c.Buffer(max(16, 8 * M))
         self.stage = c.Buffer(max(16, 8 * M))
+
+    def free_weights(self):
+        for t in self.layers:
+            for (b, n, k) in t.values():
+                b.free()
+        self.head.free()
+        self.nw.free()
 
     def rms_off(self, j):
         """stat_off of rms op j (qkv of layer l: j = 2 l, gate_up: 2 l + 1)"""
@@ -359,8 +371,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="decode step only")
-    ap.add_argument("--verify-m", default="1,2,4,5,8,16",
+    ap.add_argument("--verify-m", default="1,2,4,5,8,12,16",
                     help="x rows of the verify passes timed (config C); empty: none")
+    ap.add_argument("--verify-m-baseline", default="5,8,16",
+                    help="x rows of the verify passes also timed on BASELINE's sigma 0.02 weight scales; empty: none")
     ap.add_argument("--no-config-a", action="store_true", help="skip the single-GEMV ring (config A)")
     ap.add_argument("--verify-chain-only", action="store_true",
                     help="time the verify passes as chains only (no recorded-graph timing)")
@@ -403,10 +417,13 @@ def main():
         if vm:
             extra["verify_sweep"] = bench_verify(c, step, vm, graph=not args.verify_chain_only)
             log("verify sweep", extra["verify_sweep"])
-    for t in step.layers:
-        for (b, n, k) in t.values():
-            b.free()
-    step.head.free()
+    step.free_weights()
+    vb = () if args.no_extra else tuple(int(v) for v in args.verify_m_baseline.split(",") if v.strip())
+    if vb:   # the same passes on BASELINE's weight scales (every layer |N(0, 0.02)|: activations grow ~4x per op)
+        step = Step(c, baseline_scales=True)
+        extra["verify_sweep_baseline_scales"] = bench_verify(c, step, vb, graph=False)
+        log("verify sweep, baseline scales", extra["verify_sweep_baseline_scales"])
+        step.free_weights()
     if args.calibrate:
         calibrate(c)
     if not args.no_gemm:

@@ -517,7 +517,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
       // workgroup, run the op in the reduction area and publish once their stores are acknowledged; the others publish
       // at once (their flag of op i says, as always, that they are done with every op up to i)
       if (aux_worker(p, b)) {
-        if (i > 0 && !wait_flags(mine + (size_t)(i - 1) * Gp, nullptr)) {
+        if (p.abefore >= 0 && !wait_flags(mine + (size_t)p.abefore * Gp, nullptr)) {
           abandon = true;
           break;
         }

@@ -18,10 +18,13 @@
 // Where the A operands come from:
 //  * the previous op's epilogue staged them (GemvP::stgIn, 2^8 x' split into hi and lo, and the 16-k sums, as in the
 //    pipelined kernel): each wave loads its 8 groups straight into registers, 2 x 16 bytes a lane per group;
-//  * otherwise, or when the staging marked a half too large for the fixed 2^8 scale (NaN), the wave stages its own
-//    8 groups from x (raw or rms prologue) with a scale of its own: 2^e with e chosen from the largest |x'| of the wave
-//    (that value x 2^e in [2^14, 2^15)), so the hi / lo pair keeps 22 bits of every value near the wave's largest and
-//    nothing overflows. The wave's D results are scaled back by 2^-e with the weight scale, one multiply it has anyway.
+//  * when the staging marked a half of the wave's groups too large for the fixed 2^8 scale (NaN), the wave takes the
+//    fp32 x' values the producer also wrote and splits them with a scale of its own: 2^e with e chosen from the largest
+//    |x'| of the wave (that value x 2^e in [2^14, 2^15)), so the hi / lo pair keeps 22 bits of every value near the
+//    wave's largest and nothing overflows. The wave's D results are scaled back by 2^-e with the weight scale, one
+//    multiply it has anyway;
+//  * an op whose x is not the previous op's output (the chain's first op) stages its x' from x (raw or rms prologue)
+//    with such a scale.
 //    There is no VALU fallback: any finite x' runs on the matrix cores.
 #include "chain_common.hpp"
 
@@ -85,60 +88,24 @@ __device__ __forceinline__ bool wide_load_staged(const GemvP& p, const Share& s,
   return __builtin_amdgcn_ballot_w64(!ok) == 0;
 }
 
-// A operands of the wave staged from x (raw or rms prologue, the prologue's own order x * rstd * nw) with the wave's
-// own scale 2^e (the largest |x'| of the wave x 2^e in [2^14, 2^15)); *deq = 2^-e. Odd k are pre-scaled 1/16 as the
-// B operand's odd codes are 16 q. sx as wide_load_staged.
-template <bool COH>
-__device__ __forceinline__ void wide_stage_x(const GemvP& p, const Share& s, int M, int c, int lane, half8_t (&ahi)[8],
-                                             half8_t (&alo)[8], f4_t (&sx)[8], float& deq) {
-  const int aw = lane >> 4, arow = min(lane & 15, M - 1);
-  const bool rms = p.pro == P0_PRO_RMS;
-  const bool vec = ((uintptr_t)(p.X + p.rowB) & 15) == 0 && (p.ldx & 3) == 0 &&
-                   (!rms || ((uintptr_t)(p.NW + p.nOff) & 15) == 0);
-  const float st = rms ? ldf<COH>(&p.ST[p.statOff + arow * p.statLd]) : 1.0f;
-  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)(p.X + p.rowB), (short)0, 0x7FFFFFFF,
-                                                                      0x00020000);
-  float xo[8][8];
+// The wave's A operands from its 8 groups' x' values v[gi][j] (k 8 (lane / 16) + j of group gi, row lane % 16 or
+// M - 1; zero for groups past the split), with the wave's own scale 2^e: the largest |x'| of the wave x 2^e in
+// [2^14, 2^15); *deq = 2^-e. Odd k are pre-scaled 1/16, as the B operand's odd codes are 16 q. sx as wide_load_staged.
+__device__ __forceinline__ void wide_scale_x(float (&v)[8][8], int lane, half8_t (&ahi)[8], half8_t (&alo)[8],
+                                             f4_t (&sx)[8], float& deq) {
+  const int aw = lane >> 4;
   float mx = 0.0f;
 #pragma unroll
   for (int gi = 0; gi < 8; ++gi) {
-    const int g = wide_group(c, gi);
-    const bool live = g < s.ngs;
-    const int k0 = (s.gA + min(g, s.ngs - 1)) * 32 + 8 * aw;   // in bounds also for groups past the split
-    float x[8], nw[8];
-    if (vec) {
-      const auto a = __builtin_amdgcn_raw_buffer_load_b128(xr, (arow * (int)p.ldx + k0) * 4, 0, COH ? 16 : 0);
-      const auto b = __builtin_amdgcn_raw_buffer_load_b128(xr, (arow * (int)p.ldx + k0 + 4) * 4, 0, COH ? 16 : 0);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        x[j] = __uint_as_float(a[j]);
-        x[4 + j] = __uint_as_float(b[j]);
-      }
-      if (rms) {
-        const float4 na = *(const float4*)&p.NW[p.nOff + k0], nb = *(const float4*)&p.NW[p.nOff + k0 + 4];
-        nw[0] = na.x; nw[1] = na.y; nw[2] = na.z; nw[3] = na.w;
-        nw[4] = nb.x; nw[5] = nb.y; nw[6] = nb.z; nw[7] = nb.w;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        x[j] = ldf<COH>(&p.X[arow * p.ldx + p.rowB + k0 + j]);
-        if (rms) nw[j] = ldf<COH>(&p.NW[p.nOff + k0 + j]);
-      }
-    }
-    float v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = live ? (rms ? x[j] * st * nw[j] : x[j]) : 0.0f;
-    const float s8 = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+    const float s8 = ((v[gi][0] + v[gi][1]) + (v[gi][2] + v[gi][3])) + ((v[gi][4] + v[gi][5]) + (v[gi][6] + v[gi][7]));
     float gsum = s8 + __shfl_xor(s8, 16, 64);
     gsum += __shfl_xor(gsum, 32, 64);
 #pragma unroll
     for (int i = 0; i < 4; ++i) sx[gi][i] = __shfl(gsum, 4 * aw + i, 64);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      xo[gi][j] = (j & 1) ? v[j] * 0.0625f : v[j];
-      mx = fmaxf(mx, __builtin_fabsf(xo[gi][j]));
-    }
+    for (int j = 1; j < 8; j += 2) v[gi][j] *= 0.0625f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mx = fmaxf(mx, __builtin_fabsf(v[gi][j]));
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
@@ -152,7 +119,7 @@ __device__ __forceinline__ void wide_stage_x(const GemvP& p, const Share& s, int
     _Float16 hi[8], lo[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float xs = xo[gi][j] * scale;
+      const float xs = v[gi][j] * scale;
       hi[j] = (_Float16)xs;
       lo[j] = (_Float16)(xs - (float)hi[j]);
     }
@@ -160,6 +127,84 @@ __device__ __forceinline__ void wide_stage_x(const GemvP& p, const Share& s, int
     ahi[gi] = half8_t{hi[0], hi[4], hi[1], hi[5], hi[2], hi[6], hi[3], hi[7]};
     alo[gi] = half8_t{lo[0], lo[4], lo[1], lo[5], lo[2], lo[6], lo[3], lo[7]};
   }
+}
+
+// the wave's x' from x (raw or rms prologue, the prologue's own order x * rstd * nw), every group's loads issued
+// before the first is used, then wide_scale_x
+template <bool COH>
+__device__ __forceinline__ void wide_stage_x(const GemvP& p, const Share& s, int M, int c, int lane, half8_t (&ahi)[8],
+                                             half8_t (&alo)[8], f4_t (&sx)[8], float& deq) {
+  const int aw = lane >> 4, arow = min(lane & 15, M - 1);
+  const bool rms = p.pro == P0_PRO_RMS;
+  const bool vec = ((uintptr_t)(p.X + p.rowB) & 15) == 0 && (p.ldx & 3) == 0 &&
+                   (!rms || ((uintptr_t)(p.NW + p.nOff) & 15) == 0);
+  const float st = rms ? ldf<COH>(&p.ST[p.statOff + arow * p.statLd]) : 1.0f;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)(p.X + p.rowB), (short)0, 0x7FFFFFFF,
+                                                                      0x00020000);
+  float v[8][8];
+#pragma unroll
+  for (int gi = 0; gi < 8; ++gi) {
+    const int k0 = (s.gA + min(wide_group(c, gi), s.ngs - 1)) * 32 + 8 * aw;   // in bounds also past the split
+    if (vec) {
+      const auto a = __builtin_amdgcn_raw_buffer_load_b128(xr, (arow * (int)p.ldx + k0) * 4, 0, COH ? 16 : 0);
+      const auto b = __builtin_amdgcn_raw_buffer_load_b128(xr, (arow * (int)p.ldx + k0 + 4) * 4, 0, COH ? 16 : 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[gi][j] = __uint_as_float(a[j]);
+        v[gi][4 + j] = __uint_as_float(b[j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[gi][j] = ldf<COH>(&p.X[arow * p.ldx + p.rowB + k0 + j]);
+    }
+  }
+#pragma unroll
+  for (int gi = 0; gi < 8; ++gi) {
+    const bool live = wide_group(c, gi) < s.ngs;
+    const int k0 = (s.gA + min(wide_group(c, gi), s.ngs - 1)) * 32 + 8 * aw;
+    float nw[8];
+    if (rms) {
+      if (vec) {
+        const float4 na = *(const float4*)&p.NW[p.nOff + k0], nb = *(const float4*)&p.NW[p.nOff + k0 + 4];
+        nw[0] = na.x; nw[1] = na.y; nw[2] = na.z; nw[3] = na.w;
+        nw[4] = nb.x; nw[5] = nb.y; nw[6] = nb.z; nw[7] = nb.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) nw[j] = ldf<COH>(&p.NW[p.nOff + k0 + j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[gi][j] = live ? (rms ? v[gi][j] * st * nw[j] : v[gi][j]) : 0.0f;
+  }
+  wide_scale_x(v, lane, ahi, alo, sx, deq);
+}
+
+// the wave's x' from the previous op's fp32 staging (stg_f32_at: the prologue's values as the producer computed them,
+// device-coherent loads, all in flight together), then wide_scale_x: for a wave whose staged halves overflowed the
+// fixed 2^8 scale
+__device__ __forceinline__ void wide_stage_f32(const GemvP& p, const Share& s, int M, int c, int lane, half8_t (&ahi)[8],
+                                               half8_t (&alo)[8], f4_t (&sx)[8], float& deq) {
+  const int aw = lane >> 4, arow = min(lane & 15, M - 1);
+  const __amdgpu_buffer_rsrc_t fr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.stgIn + stg_f32_at(M, p.K)), (short)0, 0x7FFFFFFF, 0x00020000);
+  float v[8][8];
+#pragma unroll
+  for (int gi = 0; gi < 8; ++gi) {
+    const int k0 = (s.gA + min(wide_group(c, gi), s.ngs - 1)) * 32 + 8 * aw;
+    const auto a = __builtin_amdgcn_raw_buffer_load_b128(fr, (arow * p.K + k0) * 4, 0, 16);
+    const auto b = __builtin_amdgcn_raw_buffer_load_b128(fr, (arow * p.K + k0 + 4) * 4, 0, 16);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[gi][j] = __uint_as_float(a[j]);
+      v[gi][4 + j] = __uint_as_float(b[j]);
+    }
+  }
+#pragma unroll
+  for (int gi = 0; gi < 8; ++gi)
+    if (wide_group(c, gi) >= s.ngs)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[gi][j] = 0.0f;
+  wide_scale_x(v, lane, ahi, alo, sx, deq);
 }
 
 template <int MW>
@@ -233,7 +278,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_wide_kernel(const GemvP* __
     const GemvP& p = op_at(ops, i);
     if (p.kind != kOpGemv) {   // copy / argmax / rowstats / normadd, as in the pipelined kernel
       if (aux_worker(p, b)) {
-        if (i > 0 && !wait_flags(mine + (size_t)(i - 1) * Gp)) {
+        if (p.abefore >= 0 && !wait_flags(mine + (size_t)p.abefore * Gp)) {
           abandon = true;
           break;
         }
@@ -256,10 +301,12 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_wide_kernel(const GemvP* __
       half8_t ahi[8], alo[8];
       f4_t sx[8];
       float deq = kMfDeq;
-      const bool staged = p.stgIn && wide_load_staged(p, s, M, c, lane, ahi, alo, sx);
-      if (!staged) {
-        if (p.coh & 1) wide_stage_x<true>(p, s, M, c, lane, ahi, alo, sx, deq);
-        else wide_stage_x<false>(p, s, M, c, lane, ahi, alo, sx, deq);
+      if (p.stgIn) {
+        if (!wide_load_staged(p, s, M, c, lane, ahi, alo, sx)) wide_stage_f32(p, s, M, c, lane, ahi, alo, sx, deq);
+      } else if (p.coh & 1) {
+        wide_stage_x<true>(p, s, M, c, lane, ahi, alo, sx, deq);
+      } else {
+        wide_stage_x<false>(p, s, M, c, lane, ahi, alo, sx, deq);
       }
       const bool stg_rms = p.stgOut && p.stgPro == P0_PRO_RMS;
       const int upr = max(1, kWideParts / (s.nrb * s.parts));   // units per round
@@ -348,6 +395,7 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_wide_kernel(const GemvP* __
               _Float16* const sh = (_Float16*)p.stgOut;
               *P0_GLOBAL(_Float16, sh + stg_half_at(M, k, m, 0)) = hi;
               *P0_GLOBAL(_Float16, sh + stg_half_at(M, k, m, 1)) = lo;
+              *P0_GLOBAL(float, (float*)p.stgOut + stg_f32_at(M, p.stgK) + (int64_t)m * p.stgK + k) = x;
               float g = __builtin_fabsf(xo) < kMfBig ? x : __builtin_nanf("");
               g += dpp_f<0xB1>(g);    // lane ^ 1
               g += dpp_f<0x4E>(g);    // lane ^ 2

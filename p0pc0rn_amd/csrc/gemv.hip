@@ -4,7 +4,7 @@
 // Replaces the WebGPU dispatch of gemv (engine/llm/lops.js:108-141) and gemvM (engine/llm/lops_spec.js:159-191) with
 // the same arguments, the same split semantics (nsplit partial rows Y[split * ldy + m * ldm + n]) and the same errors.
 // The kernels and their mapping onto MI355X are described in gemv_kernels.hpp.
-#include "gemv_kernels.hpp"
+#include "chain_aux.hpp"
 
 #include <algorithm>
 #include <map>
@@ -299,6 +299,46 @@ static size_t plan_mailboxes(std::vector<GemvP>& ops, std::vector<int64_t>& mb_o
       if (meet(wr[i], rd[j]) || meet(wr[i], wr[j])) c.wback = 2;
   }
   return words;
+}
+
+// The waits of a pipelined chain's copy / argmax / rowstats / normadd ops (GemvP::abefore). Their workers wait for the
+// completion flags of the latest earlier op that writes what the op reads or touches what it writes (on 128-byte
+// lines), not for op i - 1's: an op with no such predecessor (a copy of a chain input into a slot no earlier op
+// touches) starts at once. An op that workgroup 0 runs alone right after another op that workgroup 0 ran alone needs
+// nothing of that op (the workgroup ran it) and nothing the earlier op's own wait covered already (the argmax's result
+// copy after the argmax). Every other op still sees every earlier op complete before it writes (flags, or GemvP::wback).
+static void plan_aux_waits(std::vector<GemvP>& ops, int M) {
+  const size_t n = ops.size();
+  std::vector<std::vector<Span>> rd(n), wr(n);
+  for (size_t i = 0; i < n; ++i) op_spans(ops[i], M, rd[i], wr[i]);
+  auto meet = [](const std::vector<Span>& x, const std::vector<Span>& y) {
+    for (const Span& a : x)
+      for (const Span& b : y)
+        if (a.a < b.b && b.a < a.b) return true;
+    return false;
+  };
+  auto hazard = [&](size_t i, size_t j) { return meet(rd[i], wr[j]) || meet(wr[i], rd[j]) || meet(wr[i], wr[j]); };
+  auto last_hazard = [&](size_t i, size_t below) {   // the latest op j < below that op i conflicts with, or -1
+    for (size_t j = below; j-- > 0;)
+      if (hazard(i, j)) return (int)j;
+    return -1;
+  };
+  auto alone = [](const GemvP& p) {   // run by workgroup 0 alone (aux_worker)
+    return p.kind != kOpGemv && (p.kind == kOpCopy ? p.an <= kAuxCopyWords : p.arows <= 1);
+  };
+  std::vector<int> covered(n, -1);   // aux op i: every op up to covered[i] was complete everywhere when i ran
+  for (size_t i = 0; i < n; ++i) {
+    GemvP& p = ops[i];
+    if (p.kind == kOpGemv) continue;
+    int J = last_hazard(i, i);
+    const bool after_alone = i > 0 && alone(ops[i - 1]) && alone(p);
+    if (after_alone && J == (int)i - 1) {
+      const int J2 = last_hazard(i, i - 1);
+      J = J2 <= covered[i - 1] ? -1 : J2;
+    }
+    p.abefore = J;
+    covered[i] = std::max(J, after_alone ? covered[i - 1] : -1);
+  }
 }
 
 // Producer-staged x' of a pipelined M > 1 chain on the matrix cores. Op i takes its x' as op i - 1 wrote it (GemvP::stgIn,
@@ -954,9 +994,28 @@ static int build_exec(ChainBuild* cb, bool pipe_only, ChainExec** out) {
       grid = ctx().cu_count * pc;
     }
   }
-  // M <= pipe_max_m(): the pipelined kernel, one workgroup per CU, when every op can be planned for it
+  // 6 - 16 rows (2 - 16 with knob 12 = 2): the wide pipelined kernel, one workgroup per CU, when every op can be
+  // planned for it
   bool pipe = false;
-  if (cb->M <= pipe_max_m() && g_chain_stage && (cb->M == 1 || g_chain_pipe_m)) {
+  const int wide_min = g_chain_wide >= 2 ? 2 : pipe_max_m() + 1;
+  if (cb->M >= wide_min && cb->M <= wide_max_m() && g_chain_stage && g_chain_wide && !cb->q8) {
+    chain_kernel_t wk = wide_chain_kernel(cb->M);
+    const int wlds = wide_lds_bytes(cb->M);
+    P0_HIP(hipFuncSetAttribute((const void*)wk, hipFuncAttributeMaxDynamicSharedMemorySize, wlds), "p0_chain_end");
+    int pc = 0;
+    P0_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, (const void*)wk, 64 * pipe_waves(), wlds), "p0_chain_end");
+    std::vector<GemvP> planned = cb->ops;
+    if (pc >= 1 && plan_wide(planned, ctx().cu_count)) {
+      cb->ops = planned;
+      k = wk;
+      cb->W = pipe_waves();
+      grid = ctx().cu_count;
+      lds = wlds;
+      pipe = true;
+    }
+  }
+  // M <= pipe_max_m(): the pipelined kernel, one workgroup per CU, when every op can be planned for it
+  if (!pipe && cb->M <= pipe_max_m() && g_chain_stage && (cb->M == 1 || g_chain_pipe_m)) {
     chain_kernel_t pk = pipe_chain_kernel(cb->M, cb->q8);
     const int plds = pipe_lds_bytes(cb->M);
     P0_HIP(hipFuncSetAttribute((const void*)pk, hipFuncAttributeMaxDynamicSharedMemorySize, plds), "p0_chain_end");
@@ -973,23 +1032,6 @@ static int build_exec(ChainBuild* cb, bool pipe_only, ChainExec** out) {
       pipe = true;
     }
   }
-  // 6 - 16 rows: the wide pipelined kernel, one workgroup per CU, when every op can be planned for it
-  if (!pipe && cb->M > pipe_max_m() && cb->M <= wide_max_m() && g_chain_stage && g_chain_wide && !cb->q8) {
-    chain_kernel_t wk = wide_chain_kernel(cb->M);
-    const int wlds = wide_lds_bytes(cb->M);
-    P0_HIP(hipFuncSetAttribute((const void*)wk, hipFuncAttributeMaxDynamicSharedMemorySize, wlds), "p0_chain_end");
-    int pc = 0;
-    P0_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, (const void*)wk, 64 * pipe_waves(), wlds), "p0_chain_end");
-    std::vector<GemvP> planned = cb->ops;
-    if (pc >= 1 && plan_wide(planned, ctx().cu_count)) {
-      cb->ops = planned;
-      k = wk;
-      cb->W = pipe_waves();
-      grid = ctx().cu_count;
-      lds = wlds;
-      pipe = true;
-    }
-  }
   if (pipe_only && !pipe) return P0_OK;
   if (cb->aux && !pipe) {
     set_error("p0_chain_end: copy, argmax, rowstats and normadd ops join only pipelined chains (M <= 5 or rows that "
@@ -1002,6 +1044,7 @@ static int build_exec(ChainBuild* cb, bool pipe_only, ChainExec** out) {
     return P0_EINVAL;
   }
   mark_coherence(cb->ops, cb->M);
+  if (cb->aux) plan_aux_waits(cb->ops, cb->M);
   std::vector<int64_t> mb_out, mb_in;
   size_t mb_words = pipe && cb->M == 1 && g_chain_mbx ? plan_mailboxes(cb->ops, mb_out, mb_in) : 0;
   std::vector<int64_t> stg_out, stg_in;
@@ -1020,7 +1063,7 @@ static int build_exec(ChainBuild* cb, bool pipe_only, ChainExec** out) {
   ex->kernel = k;
   if (pipe) {
     ex->pipe_cfg[0] = g_pipe_loaders;
-    ex->pipe_cfg[1] = cb->M > pipe_max_m() ? g_wide_depth : cb->M > 1 ? g_pipe_depth_m : g_pipe_depth;
+    ex->pipe_cfg[1] = k == wide_chain_kernel(cb->M) ? g_wide_depth : cb->M > 1 ? g_pipe_depth_m : g_pipe_depth;
   }
   // chain state: last tag, timed out, the workgroups' lines and the completion counters (one 128-byte line each)
   const size_t mb_base = (chain_state_words((int)cb->ops.size(), grid) + 63) & ~(size_t)63;   // 256-byte aligned
@@ -1135,7 +1178,7 @@ extern "C" int p0_chain_free(void* chain) {
 extern "C" int p0_chain_tune(int knob, int value) {
   if (knob == 12) {
     const int old = g_chain_wide;
-    if (value >= 0) g_chain_wide = value ? 1 : 0;
+    if (value >= 0) g_chain_wide = value > 2 ? 2 : value;
     return old;
   }
   if (knob == 9) {

@@ -96,6 +96,7 @@ struct GemvP {
   //   normadd:  arows rows of acols floats: t = sum of the an partials asrc[j aldp + m acols + i], the residual adst
   //             updated (amode 0, norm weights aw + awOff) or replaced (amode 1), ast[astOff + m] = its rstd
   int kind;
+  int abefore;   // the op whose completion flags the workers wait for first (-1: none; set by p0_chain_end)
   const float* asrc; float* adst; float* ast; const float* aw;
   int64_t arows, acols, ald, ac0, an, aldp, astOff, awOff;
   float aeps, ascale;
@@ -111,7 +112,10 @@ __host__ __device__ inline int64_t stg_half_at(int M, int64_t k, int m, int lo) 
   const int w = (int)(k >> 3) & 3, j = (int)k & 7;
   return (((g * 4 + w) * 2 + lo) * M + m) * 8 + (((j & 3) << 1) | (j >> 2));
 }
-__host__ __device__ inline int64_t stg_words(int M, int64_t K) { return K * M + (K >> 5) * 2 * M; }
+// then the fp32 x' values themselves, [m][k], which the wide chain's producers also write (chain_wide.hip: a consumer
+// wave whose staged halves overflowed the 2^8 scale takes these instead, with a scale of its own)
+__host__ __device__ inline int64_t stg_f32_at(int M, int64_t K) { return K * M + (K >> 5) * 2 * M; }
+__host__ __device__ inline int64_t stg_words(int M, int64_t K) { return stg_f32_at(M, K) + K * M; }
 
 // Op i of a chain's op table, read through the constant address space. The table is read-only for the whole launch,
 // so every field read at a uniform op index becomes a scalar load. Through a global pointer the compiler has to
