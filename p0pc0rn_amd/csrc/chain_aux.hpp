@@ -52,7 +52,12 @@ typedef __attribute__((address_space(3))) float lds_f32;
 typedef __attribute__((address_space(3))) unsigned lds_u32;
 
 // the barrier of the chain kernel's compute waves: a monotonic LDS counter at ctr, every compute wave adds 1 per
-// barrier (gen: this wave's count of the barriers so far, times kAuxWaves)
+// barrier (gen: this wave's count of the barriers so far, times kAuxWaves). A wave that leaves the kernel after a
+// wait gave up adds kBarRelease first (every wave at most once: 8 x 2^26 < 2^32), which ends every barrier wait of
+// the workgroup at once: the go word it left on can turn 0 between two waves' reads of it after one barrier, and a
+// wave that read 1 must not wait at its next barrier for one that left (the run is void then and stores nothing
+// more once the others see the go word)
+constexpr unsigned kBarRelease = 1u << 26;
 __device__ __forceinline__ void aux_bar(lds_u32* ctr, unsigned& gen, int lane) {
   gen += kAuxWaves;
   __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's LDS writes are done

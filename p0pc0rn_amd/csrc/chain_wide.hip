@@ -416,7 +416,10 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_wide_kernel(const GemvP* __
     if (c == 0 && lane < kFlagCopies) st_coh(flags + ((size_t)lane * n_ops + i) * Gp + b, tag);
     q0 += s.nslot;
   }
-  if (abandon) return;
+  if (abandon) {
+    if (lane == 0) ctl_add(lctl + L::CtlBar, kBarRelease);   // no other compute wave waits for this one any more
+    return;
+  }
   // every workgroup has read this run's tag once all have published op 0: store it back for the next run
   if (b == 0 && wait_flags(flags + 0) && tc == 0) st_coh(st, tag);
 }
