@@ -264,7 +264,9 @@ int p0_chain_free(void* chain);
  * default), 0 = every op stages its own x' after its wait; knob 11: LDS slots each loader keeps in flight in chains of
  * M = 2-5 rows (1 or 2, default 1); knob 12: 1 = chains of 6-16 rows on the wide pipelined kernel, one pass (the
  * default), 0 = as row-group passes; knob 13: LDS slots each loader keeps in flight in the wide kernel (1 or 2, default
- * 2). Knobs 0-1 and 4-13 apply to chains begun afterwards, 2-3 to runs. value < 0 only queries (knobs 0-2 also ignore
+ * 2); knob 14: 1 = in the wide kernel a compute wave whose x' exceeded the producer's 2^8 fp16 staging in one op loads
+ * the fp32 x' at once in the next (the default; the results are the same bit for bit), 0 = it tries the staging
+ * first. Knobs 0-1 and 4-14 apply to chains begun afterwards, 2-3 to runs. value < 0 only queries (knobs 0-2 also ignore
  * 0); returns the previous value. */
 int p0_chain_tune(int knob, int value);
 

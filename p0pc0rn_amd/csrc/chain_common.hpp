@@ -11,7 +11,7 @@ constexpr int kPC = 8;                       // compute waves
 constexpr int kPW = kPL + kPC;
 constexpr int kSlotB = kStageRows * 32 * 20; // 10240: one slot
 // chain state words (in the first 128-byte line, after the tag) that the host sets from p0_chain_tune knob 5
-constexpr int kCfgLoaders = 4, kCfgDepth = 5;
+constexpr int kCfgLoaders = 4, kCfgDepth = 5, kCfgPredict = 6;
 
 // LDS words seen by the loader waves through inline assembly: the compiler tracks LDS-DMA loads as pending writes to
 // LDS and would otherwise wait for all of them (vmcnt(0)) before any LDS access in the loader code, which would

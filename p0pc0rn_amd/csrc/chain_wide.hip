@@ -91,15 +91,27 @@ __device__ __forceinline__ bool wide_load_staged(const GemvP& p, const Share& s,
 // The wave's A operands from its 8 groups' x' values v[gi][j] (k 8 (lane / 16) + j of group gi, row lane % 16 or
 // M - 1; zero for groups past the split), with the wave's own scale 2^e: the largest |x'| of the wave x 2^e in
 // [2^14, 2^15); *deq = 2^-e. Odd k are pre-scaled 1/16, as the B operand's odd codes are 16 q. sx as wide_load_staged.
-__device__ __forceinline__ void wide_scale_x(float (&v)[8][8], int lane, half8_t (&ahi)[8], half8_t (&alo)[8],
-                                             f4_t (&sx)[8], float& deq) {
+// fit8: where every |x'| of the wave is below kMfBig, the fixed 2^8 instead, so that the operands, group sums and deq
+// equal wide_load_staged's bit for bit (the producer's hi / lo split of 2^8 x', and its sums in the same tree).
+// Returns true if the wave's x' exceeds that range or holds a NaN (a half the producer marked, either way).
+// Lane exchanges: the two chunk-pair adds through the gfx950 row and half swaps (lane ^ 16, lane ^ 32: VALU moves, no
+// LDS round trip; each add takes the same two values as before, in either order), the wave's largest |x'| through
+// DPP and the same swaps (a maximum does not depend on the order).
+__device__ __forceinline__ bool wide_scale_x(float (&v)[8][8], int lane, half8_t (&ahi)[8], half8_t (&alo)[8],
+                                             f4_t (&sx)[8], float& deq, bool fit8) {
   const int aw = lane >> 4;
+  auto swap_add = [](float x, bool half) {
+    const auto r = half ? __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false)
+                        : __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  };
   float mx = 0.0f;
+  bool nan = false;
 #pragma unroll
   for (int gi = 0; gi < 8; ++gi) {
     const float s8 = ((v[gi][0] + v[gi][1]) + (v[gi][2] + v[gi][3])) + ((v[gi][4] + v[gi][5]) + (v[gi][6] + v[gi][7]));
-    float gsum = s8 + __shfl_xor(s8, 16, 64);
-    gsum += __shfl_xor(gsum, 32, 64);
+    const float gsum = swap_add(swap_add(s8, false), true);
+    nan = nan || gsum != gsum;
 #pragma unroll
     for (int i = 0; i < 4; ++i) sx[gi][i] = __shfl(gsum, 4 * aw + i, 64);
 #pragma unroll
@@ -107,11 +119,20 @@ __device__ __forceinline__ void wide_scale_x(float (&v)[8][8], int lane, half8_t
 #pragma unroll
     for (int j = 0; j < 8; ++j) mx = fmaxf(mx, __builtin_fabsf(v[gi][j]));
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  mx = fmaxf(mx, dpp_f<0xB1>(mx));    // lane ^ 1
+  mx = fmaxf(mx, dpp_f<0x4E>(mx));    // lane ^ 2
+  mx = fmaxf(mx, dpp_f<0x141>(mx));   // the other quad of the 8 lanes
+  mx = fmaxf(mx, dpp_f<0x140>(mx));   // the other 8 of the 16
+  {
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    mx = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    mx = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+  }
   int E = 15;
   if (mx > 0.0f && mx <= 3.4e38f) (void)__builtin_frexpf(mx, &E);   // mx in [2^(E-1), 2^E)
-  const int e = min(60, max(-60, 15 - E));
+  const bool big = !(mx < kMfBig) || __builtin_amdgcn_ballot_w64(nan) != 0;
+  const int e = fit8 && !big ? 8 : min(60, max(-60, 15 - E));
   const float scale = __builtin_ldexpf(1.0f, e);
   deq = __builtin_ldexpf(1.0f, -e);
 #pragma unroll
@@ -127,6 +148,7 @@ __device__ __forceinline__ void wide_scale_x(float (&v)[8][8], int lane, half8_t
     ahi[gi] = half8_t{hi[0], hi[4], hi[1], hi[5], hi[2], hi[6], hi[3], hi[7]};
     alo[gi] = half8_t{lo[0], lo[4], lo[1], lo[5], lo[2], lo[6], lo[3], lo[7]};
   }
+  return big;
 }
 
 // the wave's x' from x (raw or rms prologue, the prologue's own order x * rstd * nw), every group's loads issued
@@ -176,13 +198,13 @@ __device__ __forceinline__ void wide_stage_x(const GemvP& p, const Share& s, int
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[gi][j] = live ? (rms ? v[gi][j] * st * nw[j] : v[gi][j]) : 0.0f;
   }
-  wide_scale_x(v, lane, ahi, alo, sx, deq);
+  (void)wide_scale_x(v, lane, ahi, alo, sx, deq, false);
 }
 
 // the wave's x' from the previous op's fp32 staging (stg_f32_at: the prologue's values as the producer computed them,
-// device-coherent loads, all in flight together), then wide_scale_x: for a wave whose staged halves overflowed the
-// fixed 2^8 scale
-__device__ __forceinline__ void wide_stage_f32(const GemvP& p, const Share& s, int M, int c, int lane, half8_t (&ahi)[8],
+// device-coherent loads, all in flight together), then wide_scale_x with fit8: for a wave whose staged halves
+// overflowed the fixed 2^8 scale, or whose x' overflowed it in the op before (returns wide_scale_x's value)
+__device__ __forceinline__ bool wide_stage_f32(const GemvP& p, const Share& s, int M, int c, int lane, half8_t (&ahi)[8],
                                                half8_t (&alo)[8], f4_t (&sx)[8], float& deq) {
   const int aw = lane >> 4, arow = min(lane & 15, M - 1);
   const __amdgpu_buffer_rsrc_t fr = __builtin_amdgcn_make_buffer_rsrc(
@@ -204,7 +226,7 @@ __device__ __forceinline__ void wide_stage_f32(const GemvP& p, const Share& s, i
     if (wide_group(c, gi) >= s.ngs)
 #pragma unroll
       for (int j = 0; j < 8; ++j) v[gi][j] = 0.0f;
-  wide_scale_x(v, lane, ahi, alo, sx, deq);
+  return wide_scale_x(v, lane, ahi, alo, sx, deq, true);
 }
 
 template <int MW>
@@ -274,6 +296,11 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_wide_kernel(const GemvP* __
   const int aw = lane >> 4, n16 = lane & 15;
   int q0 = 0, buf = 0;
   bool abandon = false;
+  // this wave's x' exceeded the staging's 2^8 range in its last staged op: it takes the fp32 x' straight away (one
+  // round trip instead of two when the next op's x' exceeds it too; the operands are the same either way).
+  // st[kCfgPredict] = 0 (p0_chain_tune knob 14): every wave tries the staged halves first.
+  const bool predict = st[kCfgPredict] != 0u;
+  bool big = false;
   for (int i = 0; i < n_ops; ++i) {
     const GemvP& p = op_at(ops, i);
     if (p.kind != kOpGemv) {   // copy / argmax / rowstats / normadd, as in the pipelined kernel
@@ -302,7 +329,8 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_wide_kernel(const GemvP* __
       f4_t sx[8];
       float deq = kMfDeq;
       if (p.stgIn) {
-        if (!wide_load_staged(p, s, M, c, lane, ahi, alo, sx)) wide_stage_f32(p, s, M, c, lane, ahi, alo, sx, deq);
+        if (big || !wide_load_staged(p, s, M, c, lane, ahi, alo, sx))
+          big = wide_stage_f32(p, s, M, c, lane, ahi, alo, sx, deq) && predict;
       } else if (p.coh & 1) {
         wide_stage_x<true>(p, s, M, c, lane, ahi, alo, sx, deq);
       } else {

@@ -125,6 +125,7 @@ static int g_pipe_depth = 2;            // pipelined M = 1 chain: slots in fligh
 static int g_pipe_depth_m = 1;          // pipelined M > 1 chain: the same (measured: 1 is 1-2.5% faster at M = 2-5)
 static int g_chain_wide = 1;            // chains of 6-16 rows in one pass of the wide kernel (1) or as row groups (0)
 static int g_wide_depth = 2;            // wide chain: slots in flight per loader wave (measured: 2 is 2% faster at M >= 12)
+static int g_wide_predict = 1;          // wide chain: a wave whose x' overflowed the 2^8 staging takes fp32 x' next op
 static constexpr size_t kChainLds = 64 * 1024;
 static constexpr size_t kChainLdsMax = 160 * 1024 - 256;   // gfx950: LDS per CU, less the kernel's static LDS
 
@@ -137,7 +138,7 @@ struct ChainBuild {
   std::string error;   // the first failed append (reported again by p0_chain_end)
 };
 struct ChainExec {
-  int pipe_cfg[2];   // pipelined chains: loader waves, slots in flight per loader (0: another kernel)
+  int pipe_cfg[3];   // pipelined chains: loader waves, slots in flight per loader (0: another kernel), wide: predict
   GemvP* ops;
   unsigned* st;
   size_t st_words;
@@ -1064,6 +1065,7 @@ static int build_exec(ChainBuild* cb, bool pipe_only, ChainExec** out) {
   if (pipe) {
     ex->pipe_cfg[0] = g_pipe_loaders;
     ex->pipe_cfg[1] = k == wide_chain_kernel(cb->M) ? g_wide_depth : cb->M > 1 ? g_pipe_depth_m : g_pipe_depth;
+    ex->pipe_cfg[2] = g_wide_predict;
   }
   // chain state: last tag, timed out, the workgroups' lines and the completion counters (one 128-byte line each)
   const size_t mb_base = (chain_state_words((int)cb->ops.size(), grid) + 63) & ~(size_t)63;   // 256-byte aligned
@@ -1179,6 +1181,11 @@ extern "C" int p0_chain_tune(int knob, int value) {
   if (knob == 12) {
     const int old = g_chain_wide;
     if (value >= 0) g_chain_wide = value > 2 ? 2 : value;
+    return old;
+  }
+  if (knob == 14) {
+    const int old = g_wide_predict;
+    if (value >= 0) g_wide_predict = value ? 1 : 0;
     return old;
   }
   if (knob == 9) {

@@ -164,9 +164,10 @@ def test_chain_tune_knobs_round_trip():
     capi.chain_tune(0, old)
     assert capi.chain_tune(9, -1) == 3 and capi.chain_tune(9, 6) == 3 and capi.chain_tune(9, -1) == 6
     capi.chain_tune(9, 3)
-    assert capi.chain_tune(3, -1) == 0 and capi.chain_tune(14, 1) == -1
+    assert capi.chain_tune(3, -1) == 0 and capi.chain_tune(15, 1) == -1
     assert capi.chain_tune(12, -1) == 1 and capi.chain_tune(12, 0) == 1 and capi.chain_tune(12, 1) == 0
     assert capi.chain_tune(13, -1) == 2 and capi.chain_tune(13, 1) == 2 and capi.chain_tune(13, 2) == 1
+    assert capi.chain_tune(14, -1) == 1 and capi.chain_tune(14, 0) == 1 and capi.chain_tune(14, 1) == 0
     assert capi.chain_tune(10, -1) == 1 and capi.chain_tune(10, 0) == 1 and capi.chain_tune(10, -1) == 0
     assert capi.chain_tune(10, 1) == 0 and capi.chain_tune(10, -1) == 1
     assert capi.chain_tune(4, -1) == 1 and capi.chain_tune(4, 0) == 1 and capi.chain_tune(4, -1) == 0

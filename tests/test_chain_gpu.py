@@ -165,6 +165,40 @@ def test_chain_matches_oracle(dev, M, gemvM, pipe_m):
     s.free()
 
 
+@pytest.mark.parametrize("M", [8, 16])
+def test_wide_chain_fp32_staging_predicted(dev, M):
+    """the wide kernel: qkv's outputs lie far beyond the producer's 2^8 fp16 staging, o's back inside it, so o's waves
+    find their staged halves marked and take the fp32 x', and with knob 14 on gate_up's waves then load the fp32 x'
+    straight away: they must build the same operands as the staged halves (fixed 2^8 scale where it fits), so every
+    output equals the run with knob 14 off bit for bit, and each op matches the oracle"""
+    s = MiniStep(M=M, gemvM=True, seed=40 + M)
+    for name, rows, K, sd, sigma in (("w_qkv", s.QKV, s.D, 41, 400.0), ("w_o", s.D, s.D, 42, 4e-4)):
+        s.host[name] = O.pack_q4(O.randn(rows * K, sd, sigma), rows, K)[0]
+        s.dev[name].free()
+        s.dev[name] = capi.to_device(s.host[name])
+    outs = {}
+    for knob in (1, 0):
+        old = capi.chain_tune(14, knob)
+        try:
+            ch = s.make_chain()
+        finally:
+            capi.chain_tune(14, old)
+        info = ch.info()
+        print("chain", info, flush=True)
+        assert info["waves_per_workgroup"] == 12 and info["passes"] == 1 and info["staged"] >= 2
+        s.reset_outputs()
+        ch.run()
+        assert not ch.status()
+        outs[knob] = s.read()
+        ch.free()
+    qkv_q = outs[1]["qkv"].reshape(M, s.QKV)[:, :s.D]   # the rows o reads
+    assert np.max(np.abs(qkv_q)) > 255 * 16 and np.max(np.abs(outs[1]["o"])) < 200
+    for k in outs[1]:
+        assert np.array_equal(outs[1][k].view(np.uint32), outs[0][k].view(np.uint32)), k
+    s.check_against_oracle(outs[1], f"wide chain M={M}, fp32 staging predicted")
+    s.free()
+
+
 @pytest.mark.parametrize("M,wide", [(6, 0), (11, 0), (16, 0), (6, 1), (8, 1), (11, 1), (16, 1)])
 def test_chain_row_group_passes(dev, M, wide):
     """a gemvM chain of 6-16 rows runs in one launch of the wide pipelined kernel (p0_chain_tune knob 12 on, the
