@@ -1089,7 +1089,7 @@ static int build_exec(ChainBuild* cb, bool pipe_only, ChainExec** out) {
   if (e == hipSuccess && ex->pipe_cfg[0])
     e = hipMemcpy(ex->st + pipe_cfg_word(), ex->pipe_cfg, sizeof ex->pipe_cfg, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
-    hipFree(ex->ops);
+    (void)hipFree(ex->ops);   // (the first error is the one reported)
     state_free(ex->st);
     delete ex;
     return fail_hip(e, "p0_chain_end");
@@ -1098,7 +1098,7 @@ static int build_exec(ChainBuild* cb, bool pipe_only, ChainExec** out) {
     GemvP* ops_mem = ex->ops;
     unsigned* st_mem = ex->st;
     ex->dev = Keep(ops_mem, [st_mem](void* q) {
-      hipFree(q);
+      (void)hipFree(q);
       state_free(st_mem);
     });
   }
@@ -1165,7 +1165,7 @@ extern "C" int p0_chain_info(void* chain, p0_chain_info_t* out) {
 extern "C" int p0_chain_free(void* chain) {
   if (!chain) return P0_OK;
   auto* ex = (ChainExec*)chain;
-  if (ctx().device >= 0) hipStreamSynchronize(ctx().cur);
+  if (ctx().device >= 0) (void)hipStreamSynchronize(ctx().cur);   // (freeing proceeds whatever it reports)
   for (ChainExec* e : ex->parts) delete e;
   delete ex;   // the op table and state go once no recording that ran the chain holds them
   return P0_OK;
