@@ -154,6 +154,36 @@ def test_token_chain_ends_in_argmax_and_result_copy(dev, M):
     s.free_token()
 
 
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_token_chain_forced_give_up_reports_and_recovers(dev, M):
+    """every wait of a token chain forced to give up at once (knob 3; M = 1 and 3 on the pipelined kernel, 8 on the wide
+    one, with the copy, the argmax and the result copy in the chain): the launch ends, p0_chain_status reports the run
+    once, and the next run with normal waits is correct. The compute waves that leave early release their
+    workgroup's barrier, so none of the others waits for them."""
+    print("case forced give-up M", M, flush=True)
+    s = TokenStep(M=M)
+    ch = capi.chain(s.enqueue_token)
+    assert capi.chain_tune(3, 1) == 0
+    try:
+        s.reset_outputs()
+        ch.run()
+        assert ch.status(), "waits forced to give up must be reported"
+        assert not ch.status(), "the timed-out mark is cleared once read"
+    finally:
+        capi.chain_tune(3, 0)
+    s.reset_outputs()
+    for b in (s.arg, s.stage):
+        b.fill_u32(NAN)
+    ch.run()
+    assert ch.status() == 0
+    got = s.read()
+    s.check_against_oracle(got, f"token chain M={M} after a forced give-up")
+    want = np.asarray(O.argmaxM(got["mx"], s.NT, M), np.uint32).ravel()
+    assert np.array_equal(s.stage.read(np.uint32)[:2 * M], want), "the result copy"
+    ch.free()
+    s.free_token()
+
+
 @pytest.mark.parametrize("wide", [1, 0])
 def test_row_group_passes_end_in_argmaxM(dev, wide):
     """M = 8 verify rows in one pass of the wide kernel, and (knob 12 off) as row-group passes (rows that share no
