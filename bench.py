@@ -362,7 +362,19 @@ def cpu_baseline(min_seconds=10.0):
             "sample": "oracle lgemv_f32 (the reference lgemv's fp32 order) over one decoder layer's 4 GEMVs + "
                       "1/16 of the lm_head (16384x2048), %d repetitions in %.1f s; tokens/s = 1 / (30 x layer + "
                       "16 x head slice)" % (reps, time.time() - t0),
-            "ms_per_token": round(per_token * 1e3, 2)}
+            "ms_per_token": round(per_token * 1e3, 2), "cpu": cpu_model(), "nproc": os.cpu_count()}
+
+
+def cpu_model():
+    """the host CPU's model name (/proc/cpuinfo), or '?'"""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "?"
 
 
 def main():
