@@ -336,6 +336,26 @@ def calibrate(c, reps=3):
     log("calibration kernel: copy16_kernel reads and writes %d B" % CAL_COPY_BYTES)
 
 
+def measured_peaks(c):
+    """what this box sustains, reported beside the spec-sheet peaks the roofline uses: a 256 MiB device copy (bytes
+    read + written per second) and the dense fp16 matrix-core rate (p0_probe_mfma: back-to-back MFMAs, no memory)"""
+    a, b = c.Buffer(CAL_COPY_BYTES), c.Buffer(CAL_COPY_BYTES)
+    a.fill_u32(0x3F800000)
+    ms = time_runs(c, lambda: c.copy(a, 0, b, 0, CAL_COPY_BYTES), 2, 5)
+    a.free()
+    b.free()
+    sink = c.Buffer(4096)
+    fl = [0.0]
+
+    def probe():
+        fl[0] = c.probe_mfma(20000, sink)
+    mms = time_runs(c, probe, 1, 3)
+    sink.free()
+    return {"copy_GBps": round(2 * CAL_COPY_BYTES / (ms * 1e-3) / 1e9, 1), "copy_bytes": CAL_COPY_BYTES,
+            "mfma_f16_dense_TFLOPS": round(fl[0] / (mms * 1e-3) / 1e12, 1),
+            "spec_hbm_GBps": 8000.0, "spec_fp16_dense_TFLOPS": FP16_PEAK_TFLOPS}
+
+
 def cpu_baseline(min_seconds=10.0):
     """the oracle's fp32 port of lgemv (engine/llm/lops.js:60-88) over one layer + 1/16 of the head"""
     from oracle import oracle as O
@@ -440,6 +460,9 @@ def main():
         step.free_weights()
     if args.calibrate:
         calibrate(c)
+    if not args.no_extra:
+        extra["measured_peaks"] = measured_peaks(c)
+        log("measured peaks", extra["measured_peaks"])
     if not args.no_gemm:
         extra["gemm_flux2_klein_M4608"] = bench_gemm(
             c, 4608, [("qkv", 9216, 3072), ("out", 3072, 3072), ("mlp_up", 9216, 3072), ("mlp_down", 3072, 9216)])

@@ -319,6 +319,11 @@ int p0_upload_file(const char* path, int64_t offset, int64_t bytes, void* dst, i
 int p0_fill_q4_sym(void* w, int64_t w_off, int64_t N, int64_t K, uint32_t seed, float sigma);
 /* fp16 N(0,1)-shaped activations (hash-based Box-Muller), fp32 or fp16 output */
 int p0_fill_randn(void* dst, int64_t off_bytes, int64_t n, uint32_t seed, float sigma, int32_t as_f16);
+/* The dense fp16 matrix-core rate the chip sustains (no counterpart in the reference: a measurement probe for
+ * bench.py, which reports it beside the spec-sheet peak). Enqueues one workgroup of 8 waves per CU, each wave running
+ * `iters` rounds of 4 independent v_mfma_f32_32x32x16_f16 chains with no memory traffic; `sink` (one float per CU)
+ * is written only on a value the sums never take. *flops_out = the flops enqueued; time it with p0_timer_*. */
+int p0_probe_mfma(int64_t iters, float* sink, double* flops_out);
 
 #ifdef __cplusplus
 }

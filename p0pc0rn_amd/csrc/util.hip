@@ -100,6 +100,46 @@ extern "C" int p0_fill_q4_sym(void* w, int64_t w_off, int64_t N, int64_t K, uint
   return P0_OK;
 }
 
+// The dense fp16 matrix-core rate this chip sustains: every wave of one 8-wave workgroup per CU runs `iters` rounds of
+// 4 independent v_mfma_f32_32x32x16_f16 chains (no memory traffic; the sum goes to `sink` only on a value it never
+// takes, so the arithmetic stays live). The measured peak that bench.py reports beside the spec-sheet one.
+__global__ __launch_bounds__(512) void mfma_probe_kernel(int64_t iters, float* sink) {
+  typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  const int lane = threadIdx.x & 63;
+  half8 a, b;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    a[j] = (_Float16)(0.125f * (float)((lane + j) & 7));
+    b[j] = (_Float16)(0.0625f * (float)((lane * 3 + j) & 7));
+  }
+  f32x16 acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[c][e] = 0.0f;
+  for (int64_t i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[c], 0, 0, 0);
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s += acc[c][e];
+  if (s == -1.0f) sink[blockIdx.x] = s;
+}
+
+extern "C" int p0_probe_mfma(int64_t iters, float* sink, double* flops_out) {
+  if (iters <= 0 || !sink) { set_error("probe_mfma: iters > 0 and a sink buffer of one float per CU required"); return P0_EINVAL; }
+  if (int r = require_open("probe_mfma")) return r;
+  const int grid = ctx().cu_count > 0 ? ctx().cu_count : 1;
+  hipLaunchKernelGGL(mfma_probe_kernel, dim3(grid), dim3(512), 0, ctx().cur, iters, sink);
+  P0_LAUNCHED("probe_mfma");
+  if (flops_out) *flops_out = (double)grid * 8 * 4 * 32768.0 * (double)iters;
+  return P0_OK;
+}
+
 extern "C" int p0_fill_randn(void* dst, int64_t off_bytes, int64_t n, uint32_t seed, float sigma, int32_t as_f16) {
   if (!dst || n < 0 || off_bytes % (as_f16 ? 2 : 4)) { set_error("fill_randn: bad destination"); return P0_EINVAL; }
   if (int r = require_open("fill_randn")) return r;

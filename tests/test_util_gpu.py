@@ -77,3 +77,17 @@ def test_copy_errors(dev):
     with pytest.raises(capi.P0Error, match="overlap"):
         capi.copy(a, 0, a, 16, 64)
     a.free()
+
+
+def test_probe_mfma_counts_its_flops(dev):
+    """the matrix-core probe (p0_probe_mfma) enqueues 8 waves x 4 chains x iters 32x32x16 MFMAs per CU, reports that
+    many flops, and leaves its sink alone (its sums never take the sentinel value)"""
+    cus = capi.device_info()["cu_count"]
+    sink = capi.Buffer(4 * cus + 16).fill_u32(0x12345678)
+    fl = capi.probe_mfma(100, sink)
+    capi.done()
+    assert fl == cus * 8 * 4 * 32 * 32 * 16 * 2 * 100
+    assert np.all(sink.read(np.uint32) == 0x12345678)
+    with pytest.raises(capi.P0Error, match="probe_mfma"):
+        capi.probe_mfma(0, sink)
+    sink.free()
