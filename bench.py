@@ -280,6 +280,62 @@ def bench_config_a(c, reps=8):
     return {"us_per_launch": round(ms * 1e3, 2), "GBps": round(byts / (ms * 1e-3) / 1e9, 1), "bytes": int(byts)}
 
 
+# the 8-bit GEMV shapes of Gemma-4-E2B's balanced pack, as the reference's tuner lists them with their calls per token
+# (engine/tune/tunecore.js:17-21): prologue, epilogue, N, K, kPer, calls per token
+Q8_E2B = [("rms", "store", 2560, 1536, 0, 12), ("rms", "store", 5120, 1536, 0, 3), ("rms", "store", 2048, 1536, 0, 16),
+          ("rms", "store", 4096, 1536, 0, 4), ("raw", "store", 1536, 2048, 2048, 28),
+          ("raw", "store", 1536, 4096, 2048, 7), ("rms", "geglu", 6144, 1536, 0, 4),
+          ("raw", "store", 1536, 6144, 2048, 4), ("raw", "store", 256, 1536, 0, 35), ("pleg", "store", 1536, 256, 0, 35)]
+Q8_REC = 4224   # one q8g64s.t64 record: 64 rows x 64 k of byte codes, then 64 fp16 scales
+
+
+def q8_records(rows, K, seed):
+    """synthetic q8g64s.t64 weights: uniform byte codes (stored + 128) and fp16 scales |N(0, 0.02)| / 127"""
+    rng = np.random.default_rng(seed)
+    nrec = (rows // 64) * (K // 64)
+    rec = np.empty((nrec, Q8_REC), np.uint8)
+    rec[:, :4096] = rng.integers(0, 256, (nrec, 4096), dtype=np.uint8)
+    sc = (np.abs(rng.standard_normal((nrec, 64))) * 0.02 / 127).astype(np.float16)
+    rec[:, 4096:] = sc.view(np.uint8)
+    return rec.ravel()
+
+
+def bench_q8(c, reps=4):
+    """the q8g64s.t64 GEMV at the E2B balanced pack's 8-bit shapes, standalone launches replayed from a recording
+    over a ring of weight copies (256 MB or more where at most 256 copies reach it, so the weights come from HBM as in a
+    token): us per launch and GB/s of algorithmic bytes (records + x in + y out). Launch-bound like config A."""
+    res = {}
+    for pro, epi, N, K, kPer, calls in Q8_E2B:
+        rows = 2 * N if epi == "geglu" else N
+        wbytes = (rows // 64) * (K // 64) * Q8_REC
+        R = int(min(256, max(8, -(-(256 << 20) // wbytes))))
+        host = q8_records(rows, K, N + K)
+        ws = [c.to_device(host) for _ in range(R)]
+        x = c.Buffer(K * 4)
+        c.fill_randn(x, K, 0)
+        nw = c.to_device(np.linspace(0.9, 1.1, K).astype(np.float32))
+        ev = c.to_device(np.linspace(-0.5, 0.5, K).astype(np.float32))
+        st = c.to_device(np.array([0.0, 1.0, 0.0, 0.0], np.float32))
+        nsplit = -(-K // kPer) if kPer else 1
+        y = c.Buffer(nsplit * N * 4)
+        kw = dict(w_enc=2, w_rows=rows, w_cols=K, x=x, N=N, K=K, kPer=kPer, pro=c.PRO[pro], epi=c.EPI[epi], y=y)
+        if pro == "rms":
+            kw.update(norm=nw, stat=st, stat_off=1)
+        if pro == "pleg":
+            kw.update(src_n=1, src_ld=K, ev=ev)
+
+        def ops():
+            for b in ws:
+                c.q4_gemv(c.gemv_args(w=b, **kw))
+        ms = time_recording(c, ops, 1, reps) / R
+        byts = wbytes + K * 4 + nsplit * N * 4
+        res[f"{pro}.{epi}.{N}x{K}"] = {"us_per_launch": round(ms * 1e3, 2), "GBps": round(byts / (ms * 1e-3) / 1e9, 1),
+                                       "calls_per_token": calls, "ring_copies": R}
+        for b in ws + [x, nw, ev, st, y]:
+            b.free()
+    return res
+
+
 def bench_gemm(c, M, shapes, reps=5):
     """the dequant-GEMMs of one DiT block at M tokens: bf16 N(0,1) activations (converted to fp16 by a staging pass,
     exact for |x| >= 2^-17), fp16 output. The block figure times the block's GEMMs (each with its staging pass)
@@ -463,6 +519,8 @@ def main():
     if not args.no_extra:
         extra["measured_peaks"] = measured_peaks(c)
         log("measured peaks", extra["measured_peaks"])
+        extra["q8_gemv_e2b_shapes"] = bench_q8(c)
+        log("q8 GEMV", extra["q8_gemv_e2b_shapes"])
     if not args.no_gemm:
         extra["gemm_flux2_klein_M4608"] = bench_gemm(
             c, 4608, [("qkv", 9216, 3072), ("out", 3072, 3072), ("mlp_up", 9216, 3072), ("mlp_down", 3072, 9216)])

@@ -1037,6 +1037,8 @@ chain_kernel_t pick_chain_m(int W) {   // 16-wave chain workgroups for M = 1, 8-
 // the q8g64s.t64 GEMV (gemv_q8.hip): the kernel for M rows and its LDS bytes
 typedef void (*q8_kernel_t)(GemvP);
 q8_kernel_t q8_kernel(int M);
+q8_kernel_t q8_gemv1(bool geglu);   // M = 1, splits of at most 3072 k: 16 waves, the records in flight together
+size_t q8_gemv1_lds_bytes();
 size_t q8_lds_bytes(int M);
 
 // the pipelined chain (chain_pipe.hip) for M <= pipe_max_m() rows of x: its kernels and their shape

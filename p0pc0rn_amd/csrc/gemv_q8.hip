@@ -17,6 +17,8 @@
 namespace p0 {
 
 constexpr int kQ8Waves = 4, kQ8Threads = 64 * kQ8Waves, kQ8Chunk = 1024, kQ8CG = kQ8Chunk / 64;
+// the M = 1 kernel: 16 waves, 2 groups per wave and round, splits of at most 3072 k
+constexpr int kQ81Waves = 16, kQ81Threads = 64 * kQ81Waves, kQ81G = 2, kQ81MaxK = 3072;
 
 size_t q8_lds_bytes(int M) {   // x' chunk, group sums, and the cross-wave reduction [wave][tile][m][lane]
   return (size_t)M * (kQ8Chunk + kQ8CG) * sizeof(float) + (size_t)kQ8Waves * 2 * M * 64 * sizeof(float);
@@ -121,6 +123,90 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(GemvP p) {
   }
 }
 
+// M = 1 (gemv, the decode case): a workgroup of 16 waves per (64-row tile, split), every wave's record loads issued
+// before the input is staged. Wave w takes groups w and 16 + w of each round of 32 (a geglu, two tiles: group w of
+// each round of 16), so a split's records (at most 48 groups of 3072 k) are in flight in one to three rounds, the
+// first round's latency overlapping the x' staging; the kernel above, 4 waves that load their groups one after another, spends a memory round trip per group.
+// The group sums add the 64 x' of a group in k order; the waves' sums are added in wave order (deterministic).
+template <int T>   // 2: a geglu (the gate tile and its up tile), else 1
+__global__ __launch_bounds__(kQ81Threads) void q8_gemv1_kernel(GemvP p) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  float* xs = smem;                       // [kQ81MaxK] x' of the split
+  float* xsum = xs + kQ81MaxK;            // [kQ81MaxK / 64] its group sums
+  float* red = xsum + kQ81MaxK / 64;      // [wave][tile][64 rows]
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tile0 = blockIdx.x, split = blockIdx.y;
+  const int64_t tiles[2] = {tile0, tile0 + (T == 2 ? p.NT : 0)};
+  const int k0s = split * p.kPer, k1s = min(p.K, k0s + p.kPer), ng = (k1s - k0s) >> 6, g0 = k0s >> 6;
+  constexpr int GW = kQ81G / T;   // groups per wave and round (the registers of 2 tile-groups)
+  float acc[2] = {0.0f, 0.0f};
+  for (int r0 = 0; r0 < ng; r0 += kQ81Waves * GW) {
+    u32x4 q[GW][T][4];
+    uint32_t sw[GW][T];
+#pragma unroll
+    for (int b = 0; b < GW; ++b) {
+      const int gl = min(r0 + b * kQ81Waves + wv, ng - 1);   // past the split: its last group again (unused)
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const uint8_t* rec = p.w + (tiles[t] * p.wG + g0 + gl) * 4224;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[b][t][j] = *P0_GLOBAL(const u32x4, rec + lane * 64 + j * 16);
+        sw[b][t] = *P0_GLOBAL(const uint32_t, rec + 4096 + (lane & ~1) * 2);
+      }
+    }
+    if (r0 == 0) {   // x' of the split while the first round's records are in flight, then its group sums
+      for (int i = tid; i < k1s - k0s; i += kQ81Threads) xs[i] = prologue<false>(p, 0, k0s + i);
+      __syncthreads();
+      for (int gl = tid; gl < ng; gl += kQ81Threads) {
+        float s = 0.0f;
+        for (int j = 0; j < 64; ++j) s += xs[gl * 64 + j];
+        xsum[gl] = s;
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int b = 0; b < GW; ++b) {
+      const int gl = r0 + b * kQ81Waves + wv;
+      if (gl >= ng) break;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const float s = (lane & 1) ? h2f_hi(sw[b][t]) : h2f_lo(sw[b][t]);
+        float d = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t wd[4] = {q[b][t][j].x ^ 0x80808080u, q[b][t][j].y ^ 0x80808080u, q[b][t][j].z ^ 0x80808080u,
+                                  q[b][t][j].w ^ 0x80808080u};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float b0 = (float)(wd[e] & 0xFFu), b1 = (float)((wd[e] >> 8) & 0xFFu);
+            const float b2 = (float)((wd[e] >> 16) & 0xFFu), b3 = (float)(wd[e] >> 24);
+            const float4 x4 = *(const float4*)(xs + gl * 64 + j * 16 + e * 4);
+            d = __builtin_fmaf(b0, x4.x, __builtin_fmaf(b1, x4.y, __builtin_fmaf(b2, x4.z, __builtin_fmaf(b3, x4.w, d))));
+          }
+        }
+        acc[t] = __builtin_fmaf(s, d - 128.0f * xsum[gl], acc[t]);
+      }
+    }
+  }
+  // the waves' sums, added in wave order
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+    if (t < T) red[(wv * 2 + t) * 64 + lane] = acc[t];
+  __syncthreads();
+  if (wv != 0) return;
+  float tot[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (t >= T) break;
+    float v = red[t * 64 + lane];
+    for (int w = 1; w < kQ81Waves; ++w) v += red[(w * 2 + t) * 64 + lane];
+    tot[t] = v;
+  }
+  epilogue<false>(p, split, 0, tile0, lane, tot[0], tot[1]);
+}
+
 q8_kernel_t q8_kernel(int M) { return M == 1 ? q8_gemv_kernel<1> : q8_gemv_kernel<0>; }
+q8_kernel_t q8_gemv1(bool geglu) { return geglu ? q8_gemv1_kernel<2> : q8_gemv1_kernel<1>; }
+size_t q8_gemv1_lds_bytes() { return (kQ81MaxK + kQ81MaxK / 64 + kQ81Waves * 2 * 64) * sizeof(float); }
 
 }  // namespace p0
