@@ -497,8 +497,11 @@ __global__ __launch_bounds__(64 * kPW) void q4_chain_pipe_kernel(const GemvP* __
       xs[kl] = (kl & 1) ? v * odd : v;
       if ((lane & 31) == 0) xsum[kl >> 5] = gsum;
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the wave's x' is in LDS before it reads it back
+    // the wave reads its x' back right behind these writes: the LDS serves one wave's accesses in order, so no
+    // lgkmcnt wait; the wavefront fences keep the compiler from moving the reads above the other lanes' writes
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     return true;
   };
   // this op's rows, with their values as stored, into its mailbox (after the epilogue's own stores): the element of
