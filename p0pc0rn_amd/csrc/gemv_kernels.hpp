@@ -700,8 +700,10 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
   }
 
   // ---- several K-slices per split: partials -> workspace; the last workgroup of (split, tile block) to arrive
-  // reduces them in K-slice order. One thread fences for the workgroup (a device-scope release / acquire writes back
-  // / invalidates the whole L2 of the XCD, so it is done once, after the barrier that orders every wave's stores).
+  // reduces them in K-slice order. The workspace is uncached device memory: a partial is in memory once its store is
+  // acknowledged, and the last workgroup reads it from memory, so no fence (a device-scope release / acquire writes
+  // back / invalidates the whole L2 of the XCD) is needed: every wave waits for its own stores, then one thread counts
+  // the workgroup's arrival.
   const size_t sliceBase = (size_t)(split * p.nks) * M * p.rowsTot;
   if (owner) {
 #pragma unroll
@@ -713,15 +715,14 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
       }
     }
   }
+  __builtin_amdgcn_s_waitcnt(0);   // every wave: its partials (uncached memory) are written before the arrival count
   __syncthreads();
   if (tid == 0) {
-    __threadfence();   // release: the workgroup's partials reach memory before the arrival count
     auto* c = P0_GLOBAL(unsigned, p.cnt + (size_t)split * p.ntb + bx);
     const unsigned prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int last = prev == (unsigned)(p.nks - 1);
     if (last) {
       __hip_atomic_exchange(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // leave the counter at zero
-      __threadfence();     // acquire: every other workgroup's partials
     }
     *s_last = last;
   }

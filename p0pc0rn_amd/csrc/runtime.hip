@@ -82,9 +82,16 @@ __global__ void copy4_kernel(const uint32_t* __restrict__ src, uint32_t* __restr
 
 using namespace p0;
 
-// Split-K workspace held by the context: 64 MiB of partial sums and 1 Mi arrival counters.
+// Split-K workspace: 64 MiB of partial sums and 1 Mi arrival counters per device, in uncached device memory. The
+// partials then reach memory when their stores are acknowledged and are read from memory, so the arrival protocol
+// needs no L2 write-back or invalidate (a device-scope fence costs a write-back of the XCD's whole L2). Uncached memory
+// that a kernel has read is never freed while the process runs (allocations made after such a free have been seen
+// holding wrong values), so each device's workspace is allocated once and kept across p0_close / p0_open.
 static constexpr size_t kPartBytes = 64ull << 20;
 static constexpr size_t kCounters = 1ull << 20;
+static constexpr int kWsDevices = 64;
+static float* g_ws_part[kWsDevices] = {};
+static unsigned* g_ws_cnt[kWsDevices] = {};
 
 extern "C" {
 
@@ -113,8 +120,19 @@ int p0_open(int device) {
   P0_HIP(hipStreamCreate(&c.own), "p0_open");   // default priority
   P0_HIP(hipEventCreate(&c.ev0), "p0_open");
   P0_HIP(hipEventCreate(&c.ev1), "p0_open");
-  P0_HIP(hipMalloc((void**)&c.part, kPartBytes), "p0_open: workspace");
-  P0_HIP(hipMalloc((void**)&c.counters, kCounters * sizeof(unsigned)), "p0_open: workspace");
+  if (device >= kWsDevices) {
+    set_error("p0_open: device %d (this build keeps workspaces for devices 0 .. %d)", device, kWsDevices - 1);
+    return P0_ENODEV;
+  }
+  if (!g_ws_part[device]) {
+    P0_HIP(hipExtMallocWithFlags((void**)&g_ws_part[device], kPartBytes, hipDeviceMallocUncached), "p0_open: workspace");
+  }
+  if (!g_ws_cnt[device]) {
+    P0_HIP(hipExtMallocWithFlags((void**)&g_ws_cnt[device], kCounters * sizeof(unsigned), hipDeviceMallocUncached),
+           "p0_open: workspace");
+  }
+  c.part = g_ws_part[device];
+  c.counters = g_ws_cnt[device];
   P0_HIP(hipMemset(c.counters, 0, kCounters * sizeof(unsigned)), "p0_open: workspace");
   P0_HIP(hipDeviceSynchronize(), "p0_open");
   if (int r = gemm_init()) return r;
@@ -131,9 +149,7 @@ int p0_open(int device) {
 int p0_close(void) {
   Ctx& c = ctx();
   if (c.device < 0) return P0_OK;
-  hipStreamSynchronize(c.own);
-  hipFree(c.part);
-  hipFree(c.counters);
+  (void)hipStreamSynchronize(c.own);   // the split-K workspace stays allocated (see g_ws_part)
   c.xstage_keep.reset();   // freed unless a recording still holds it
   hipEventDestroy(c.ev0);
   hipEventDestroy(c.ev1);

@@ -180,6 +180,28 @@ def test_gemv_decompositions_agree(dev):
             capi.gemv_tune(k, v)
 
 
+def test_gemv_split_k_workspace_across_reopen(dev):
+    """K in many slices per workgroup (the uncached split-K workspace and its arrival counters), run after run, then
+    after closing and reopening the device (the workspace is kept, not freed): the same bits, the oracle's values"""
+    c = Case(1, 512, 4096, "rms", "store", kPer=2048, seed=23)
+    want = c.run_oracle()[0]
+    idx = c.rows_written()
+    old = [capi.gemv_tune(k) for k in range(4)]
+    try:
+        for k, v in enumerate((100000, 100000, 1, 2)):   # 2 waves per slot, 1 group per wave: 32 slices per split
+            capi.gemv_tune(k, v)
+        runs = [c.run_gpu()[0] for _ in range(3)]
+        capi.close_device()
+        capi.open_device(0)
+        runs.append(c.run_gpu()[0])
+    finally:
+        for k, v in enumerate(old):
+            capi.gemv_tune(k, v)
+    for r in runs:
+        assert np.array_equal(r.view(np.uint32), runs[0].view(np.uint32))
+    _check(runs[-1][idx], want[idx], "split-K after reopen")
+
+
 def test_gemv_head_shape_softcap(dev):
     """a head-like softcap GEMV: 65,536 rows x 2,048, per-tile max / argmax (engine/llm/gemma4.js:503-511)"""
     Case(1, 65536, 2048, "rms", "softcap", seed=21).check("head-like softcap 65536x2048")
