@@ -56,8 +56,10 @@ static Plan plan(int M, int NT, int epi, int nsplit, int kPer) {
   const int slots = pl.mode == 1 ? (NT + 1) / 2 : NT;
   pl.rowsTot = (epi == P0_EPI_GEGLU ? 2 : 1) * NT * 64;
   const int Gs = kPer / 32;
-  // K shares per slot and split: enough waves for the chip, but at least g_min_gpw groups each
-  int kws = (g_target_waves + slots * nsplit - 1) / (slots * nsplit);
+  // K shares per slot and split: enough waves for the chip, but at least g_min_gpw groups each (a geglu slot streams
+  // the gate and the up tile, so it counts twice)
+  const int work = pl.mode == 2 ? 2 * g_target_waves : g_target_waves;
+  int kws = (work + slots * nsplit - 1) / (slots * nsplit);
   const int kws_max = Gs / g_min_gpw > 1 ? Gs / g_min_gpw : 1;
   if (kws > kws_max) kws = kws_max;
   if (kws < 1) kws = 1;
