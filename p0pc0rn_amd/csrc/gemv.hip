@@ -66,6 +66,9 @@ static Plan plan(int M, int NT, int epi, int nsplit, int kPer) {
   const bool mf = M >= 2 && M >= g_mf_min_m;   // the MFMA kernel (512 threads)
   const int max_kw = M <= 2 && !mf ? g_max_kw : (g_max_kw < 8 ? g_max_kw : 8);   // the kernel's launch bound
   pl.kw = kws < max_kw ? kws : max_kw;
+  // one tile per slot whose K is split across workgroups anyway: at most 8 waves per slot, so that twice the
+  // workgroups (each with half the records to issue and dot) share it
+  if (pl.mode == 0 && kws > pl.kw && pl.kw > 8) pl.kw = 8;
   pl.tgw = pl.kw >= 4 ? 1 : 4 / pl.kw;                 // 4 waves per workgroup unless kw is larger
   if (pl.tgw > slots) pl.tgw = slots;
   pl.waves = pl.tgw * pl.kw;
