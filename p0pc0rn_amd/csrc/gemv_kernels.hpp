@@ -730,23 +730,45 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
   const bool last = *s_last != 0;
   if (!last || !owner) return last;
 
+  // the partials of SB K-slices (every x row and tile) are loaded together and then added in K-slice order: one
+  // memory round trip per SB slices, where a load per add took one per partial
+  constexpr int SB = M * T >= 16 ? 1 : 16 / (M * T);
+  float tot[T][M];
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-    float tot[T];
+  for (int t = 0; t < T; ++t)
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-      tot[t] = 0.0f;
-      const int row = (MODE == 2 && t == 1) ? p.N + tile[0] * 64 + lane : tile[t] * 64 + lane;
-      if (MODE != 1 || tile[t] < p.NT) {
-        for (int s = 0; s < p.nks; ++s) tot[t] += *P0_GLOBAL(const float, &p.part[sliceBase + ((size_t)s * M + m) * p.rowsTot + row]);
+    for (int m = 0; m < M; ++m) tot[t][m] = 0.0f;
+  for (int s0 = 0; s0 < p.nks; s0 += SB) {
+    float v[SB][T][M];
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      const int s = min(s0 + j, p.nks - 1);   // past the last slice: re-read it (in bounds, not added)
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int row = (MODE == 2 && t == 1) ? p.N + tile[0] * 64 + lane : tile[t] * 64 + lane;
+        const bool live = MODE != 1 || tile[t] < p.NT;
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+          v[j][t][m] = live ? *P0_GLOBAL(const float, &p.part[sliceBase + ((size_t)s * M + m) * p.rowsTot + row]) : 0.0f;
       }
     }
+#pragma unroll
+    for (int j = 0; j < SB; ++j)
+      if (s0 + j < p.nks) {
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+          for (int m = 0; m < M; ++m) tot[t][m] += v[j][t][m];
+      }
+  }
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
     if (MODE == 2) {
-      epi(split, m, tile[0], tot[0], tot[T - 1]);
+      epi(split, m, tile[0], tot[0][m], tot[T - 1][m]);
     } else {
 #pragma unroll
       for (int t = 0; t < T; ++t)
-        if (tile[t] < p.NT) epi(split, m, tile[t], tot[t], 0.0f);
+        if (tile[t] < p.NT) epi(split, m, tile[t], tot[t][m], 0.0f);
     }
   }
   return true;
