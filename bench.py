@@ -392,15 +392,23 @@ def calibrate(c, reps=3):
     log("calibration kernel: copy16_kernel reads and writes %d B" % CAL_COPY_BYTES)
 
 
+READ_PROBE_BYTES = 1 << 30
+
+
 def measured_peaks(c):
     """what this box sustains, reported beside the spec-sheet peaks the roofline uses: a 256 MiB device copy (bytes
-    read + written per second) and the dense fp16 matrix-core rate (p0_probe_mfma: back-to-back MFMAs, no memory)"""
+    read + written per second), a 1 GiB read-only stream (p0_probe_read: the access the GEMV weights make) and the
+    dense fp16 matrix-core rate (p0_probe_mfma: back-to-back MFMAs, no memory)"""
     a, b = c.Buffer(CAL_COPY_BYTES), c.Buffer(CAL_COPY_BYTES)
     a.fill_u32(0x3F800000)
     ms = time_runs(c, lambda: c.copy(a, 0, b, 0, CAL_COPY_BYTES), 2, 5)
     a.free()
     b.free()
     sink = c.Buffer(4096)
+    r = c.Buffer(READ_PROBE_BYTES)
+    r.fill_u32(0x3F800000)
+    rms = time_runs(c, lambda: c.probe_read(r, READ_PROBE_BYTES, sink), 2, 5)
+    r.free()
     fl = [0.0]
 
     def probe():
@@ -408,6 +416,7 @@ def measured_peaks(c):
     mms = time_runs(c, probe, 1, 3)
     sink.free()
     return {"copy_GBps": round(2 * CAL_COPY_BYTES / (ms * 1e-3) / 1e9, 1), "copy_bytes": CAL_COPY_BYTES,
+            "read_GBps": round(READ_PROBE_BYTES / (rms * 1e-3) / 1e9, 1), "read_bytes": READ_PROBE_BYTES,
             "mfma_f16_dense_TFLOPS": round(fl[0] / (mms * 1e-3) / 1e12, 1),
             "spec_hbm_GBps": 8000.0, "spec_fp16_dense_TFLOPS": FP16_PEAK_TFLOPS}
 

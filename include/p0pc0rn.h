@@ -324,6 +324,11 @@ int p0_fill_randn(void* dst, int64_t off_bytes, int64_t n, uint32_t seed, float 
  * `iters` rounds of 4 independent v_mfma_f32_32x32x16_f16 chains with no memory traffic; `sink` (one float per CU)
  * is written only on a value the sums never take. *flops_out = the flops enqueued; time it with p0_timer_*. */
 int p0_probe_mfma(int64_t iters, float* sink, double* flops_out);
+/* The HBM read rate the chip sustains (no counterpart in the reference: a measurement probe for bench.py, which reports
+ * it beside the spec-sheet peak). Enqueues one pass of 16-byte loads over `bytes` (a positive multiple of 16) at `buf`,
+ * 2048 workgroups of 256 threads in a grid-stride loop; `sink` (one word) is written only on a fold value the data
+ * does not give. Time it with p0_timer_*. */
+int p0_probe_read(const void* buf, int64_t bytes, uint32_t* sink);
 
 #ifdef __cplusplus
 }

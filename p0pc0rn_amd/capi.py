@@ -27,6 +27,7 @@ HEADER_SYMBOLS = [
     "p0_buffer", "p0_free", "p0_upload", "p0_read", "p0_fill", "p0_copy", "p0_done", "p0_timer_start", "p0_timer_stop",
     "p0_q4_gemv", "p0_q4_gemvM", "p0_q4_gemm", "p0_q4_gemm_noalloc", "p0_q4_dequant", "p0_fill_q4_sym", "p0_fill_randn", "p0_gemv_tune",
     "p0_probe_mfma",
+    "p0_probe_read",
     "p0_record_begin", "p0_record_end", "p0_replay", "p0_record_info", "p0_record_free",
     "p0_chain_begin", "p0_chain_end", "p0_chain_run", "p0_chain_status", "p0_chain_info", "p0_chain_free",
     "p0_chain_tune", "p0_rowstats", "p0_normadd", "p0_argmax", "p0_argmaxM", "p0_upload_file",
@@ -112,6 +113,7 @@ def lib():
             "p0_q4_dequant": [vp, i64, i64, i64, vp, vp], "p0_fill_q4_sym": [vp, i64, i64, i64, C.c_uint32, f32],
             "p0_fill_randn": [vp, i64, i64, C.c_uint32, f32, i32], "p0_gemv_tune": [C.c_int, C.c_int],
             "p0_probe_mfma": [i64, vp, C.POINTER(C.c_double)],
+            "p0_probe_read": [vp, i64, vp],
             "p0_record_begin": [], "p0_record_end": [C.POINTER(vp)], "p0_replay": [vp], "p0_record_free": [vp],
             "p0_record_info": [vp, C.POINTER(i32)],
             "p0_chain_begin": [], "p0_chain_end": [C.POINTER(vp)], "p0_chain_run": [vp],
@@ -255,6 +257,11 @@ def probe_mfma(iters, sink):
     fl = C.c_double()
     check(lib().p0_probe_mfma(iters, _ptr(sink), C.byref(fl)))
     return fl.value
+
+
+def probe_read(buf, nbytes, sink):
+    """enqueue one read pass over nbytes of buf (p0_probe_read)"""
+    check(lib().p0_probe_read(_ptr(buf), nbytes, _ptr(sink)))
 
 
 class Chain:

@@ -140,6 +140,30 @@ extern "C" int p0_probe_mfma(int64_t iters, float* sink, double* flops_out) {
   return P0_OK;
 }
 
+// the HBM read rate: a grid-stride stream of 16-byte loads over the buffer, XOR-folded per thread; the sink is written
+// only on a fold value the caller's data does not give (the loads cannot be dropped)
+__global__ __launch_bounds__(256) void read_probe_kernel(const uint4* __restrict__ p, int64_t n, uint32_t* sink) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  uint32_t acc = 0;
+  for (; i < n; i += stride) {
+    const uint4 v = p[i];
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+extern "C" int p0_probe_read(const void* buf, int64_t bytes, uint32_t* sink) {
+  if (!buf || !sink || bytes <= 0 || bytes % 16) {
+    set_error("probe_read: a buffer of a positive multiple of 16 bytes and a sink word required");
+    return P0_EINVAL;
+  }
+  if (int r = require_open("probe_read")) return r;
+  hipLaunchKernelGGL(read_probe_kernel, dim3(2048), dim3(256), 0, ctx().cur, (const uint4*)buf, bytes / 16, sink);
+  P0_LAUNCHED("probe_read");
+  return P0_OK;
+}
+
 extern "C" int p0_fill_randn(void* dst, int64_t off_bytes, int64_t n, uint32_t seed, float sigma, int32_t as_f16) {
   if (!dst || n < 0 || off_bytes % (as_f16 ? 2 : 4)) { set_error("fill_randn: bad destination"); return P0_EINVAL; }
   if (int r = require_open("fill_randn")) return r;

@@ -91,3 +91,23 @@ def test_probe_mfma_counts_its_flops(dev):
     with pytest.raises(capi.P0Error, match="probe_mfma"):
         capi.probe_mfma(0, sink)
     sink.free()
+
+
+def test_probe_read_reads_the_whole_buffer(dev):
+    """the read probe (p0_probe_read) folds every 16-byte piece it loads: a buffer whose only nonzero word sits in the
+    last piece (the grid-stride loop's last iterations) folds to the sentinel and writes the sink; a zero buffer
+    leaves it alone; sizes that are not multiples of 16 are refused"""
+    n = 64 << 20
+    buf = capi.Buffer(n).fill_u32(0)
+    sink = capi.Buffer(16).fill_u32(0x12345678)
+    capi.probe_read(buf, n, sink)
+    capi.done()
+    assert sink.read(np.uint32)[0] == 0x12345678
+    buf.upload(np.array([0x9E3779B9, 0, 0, 0], np.uint32), off=n - 16)
+    capi.probe_read(buf, n, sink)
+    capi.done()
+    assert sink.read(np.uint32)[0] == 0x9E3779B9
+    with pytest.raises(capi.P0Error, match="probe_read"):
+        capi.probe_read(buf, n - 8, sink)
+    buf.free()
+    sink.free()
