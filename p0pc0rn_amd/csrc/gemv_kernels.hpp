@@ -326,21 +326,33 @@ __device__ __forceinline__ bool stage_x_mf(const GemvP& p, int g0, int g1, int g
   return bad;
 }
 
-// one group's records of one 64-row tile in the MFMA B layout: lane l holds word l / 16 of rows 16 b + l % 16, and the
-// scale/min words of those rows
+// one group's records of one 64-row tile as loaded: lane = row, its four code words and its scale/min word (two loads
+// per lane; quarter_transpose turns them into the MFMA B layout)
 struct RecM {
-  uint32_t q[4];
-  uint32_t sm[4];
+  u32x4 q;
+  uint32_t sm;
 };
 __device__ __forceinline__ RecM load_rec_mf(const GemvP& p, int64_t tile, int g, int lane) {
   const uint8_t* rec = p.w + (int64_t)__builtin_amdgcn_readfirstlane((int)(tile * p.wG + g)) * 1280;
   RecM r;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    r.q[b] = *P0_GLOBAL(const uint32_t, rec + (16 * b + (lane & 15)) * 16 + (lane >> 4) * 4);
-    r.sm[b] = *P0_GLOBAL(const uint32_t, rec + 1024 + (16 * b + (lane & 15)) * 4);
-  }
+  r.q = *P0_GLOBAL(const u32x4, rec + lane * 16);
+  r.sm = *P0_GLOBAL(const uint32_t, rec + 1024 + lane * 4);
   return r;
+}
+// w[j] at lane 16 Q + i (Q the lane's 16-lane row) holds word j of weight row 16 Q + i; afterwards w[b] at lane 16 q + i
+// holds word q of weight row 16 b + i, the B layout of block b (lane l: word l / 16 of row 16 b + l % 16). A 4 x 4
+// transpose of (lane row, word) with the gfx950 lane swaps: permlane32_swap exchanges lanes 32-63 of its first operand
+// with lanes 0-31 of its second, permlane16_swap the odd 16-lane rows of its first operand with the even rows of its
+// second. Four copies of one word per lane come out as its row's word broadcast to the block's lanes.
+__device__ __forceinline__ void quarter_transpose(uint32_t (&w)[4]) {
+  const auto s02 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+  const auto s13 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+  const auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+  const auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+  w[0] = s01[0];
+  w[1] = s01[1];
+  w[2] = s23[0];
+  w[3] = s23[1];
 }
 // (v & mask) | e1024: with e1024 held in a vector register (its value hidden from the compiler) the and + or fold into
 // one v_and_or_b32 (VOP3, which takes no literal on gfx950: the mask goes to a scalar register); with both constants
@@ -535,16 +547,21 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
         const half8_t ahi = ap[0], alo = ap[M];
         const f4_t sx = *(const f4_t*)(xsum + gl * 16 + 4 * aw);
 #pragma unroll
-        for (int t = 0; t < T; ++t)
+        for (int t = 0; t < T; ++t) {
+          uint32_t qb[4] = {cur[t].q.x, cur[t].q.y, cur[t].q.z, cur[t].q.w};
+          uint32_t sb[4] = {cur[t].sm, cur[t].sm, cur[t].sm, cur[t].sm};
+          quarter_transpose(qb);
+          quarter_transpose(sb);
 #pragma unroll
           for (int b = 0; b < 4; ++b) {
-            const half8_t bq = codes_b(cur[t].q[b]);
+            const half8_t bq = codes_b(qb[b]);
             f4_t d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bq, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
             d = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bq, d, 0, 0, 0);
-            const float s8 = h2f_lo(cur[t].sm[b]) * kMfDeq, mn = h2f_hi(cur[t].sm[b]);
+            const float s8 = h2f_lo(sb[b]) * kMfDeq, mn = h2f_hi(sb[b]);
 #pragma unroll
             for (int i = 0; i < 4; ++i) am[t][b][i] = __builtin_fmaf(s8, d[i], __builtin_fmaf(mn, sx[i], am[t][b][i]));
           }
+        }
       };
       if (streams) {
 #pragma unroll
