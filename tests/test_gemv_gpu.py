@@ -202,6 +202,21 @@ def test_gemv_split_k_workspace_across_reopen(dev):
     _check(runs[-1][idx], want[idx], "split-K after reopen")
 
 
+@pytest.mark.parametrize("M,epi,K,kPer", [(3, "store", 4096, 2048), (5, "geglu", 2048, 0), (16, "store", 4096, 2048)])
+def test_gemvM_many_k_slices(dev, M, epi, K, kPer):
+    """gemvM (matrix cores) with K in many slices: the last workgroup to arrive loads the slices' partials of every x
+    row in batches (fewer slices per batch as M grows) and adds them in slice order; the oracle's values"""
+    c = Case(M, 256, K, "rms", epi, kPer=kPer, seed=29 + M, gemvM=True)
+    old = [capi.gemv_tune(k) for k in range(4)]
+    try:
+        for k, v in enumerate((100000, 100000, 1, 2)):
+            capi.gemv_tune(k, v)
+        c.check(f"gemvM M={M} {epi}, many K slices")
+    finally:
+        for k, v in enumerate(old):
+            capi.gemv_tune(k, v)
+
+
 def test_gemv_head_shape_softcap(dev):
     """a head-like softcap GEMV: 65,536 rows x 2,048, per-tile max / argmax (engine/llm/gemma4.js:503-511)"""
     Case(1, 65536, 2048, "rms", "softcap", seed=21).check("head-like softcap 65536x2048")
