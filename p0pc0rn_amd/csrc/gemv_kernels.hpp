@@ -717,10 +717,11 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
   }
 
   // ---- several K-slices per split: partials -> workspace; the last workgroup of (split, tile block) to arrive
-  // reduces them in K-slice order. The workspace is uncached device memory: a partial is in memory once its store is
-  // acknowledged, and the last workgroup reads it from memory, so no fence (a device-scope release / acquire writes
-  // back / invalidates the whole L2 of the XCD) is needed: every wave waits for its own stores, then one thread counts
-  // the workgroup's arrival.
+  // reduces them in K-slice order. The workspace is uncached device memory, written and read with device-scope
+  // accesses (no cache of any level serves a stale line, also to a persistent chain workgroup that reduced the same
+  // slots for an earlier op): a partial is in memory once its store is acknowledged, so no fence (a device-scope
+  // release / acquire writes back / invalidates the whole L2 of the XCD) is needed: every wave waits for its own
+  // stores, then one thread counts the workgroup's arrival.
   const size_t sliceBase = (size_t)(split * p.nks) * M * p.rowsTot;
   if (owner) {
 #pragma unroll
@@ -728,7 +729,7 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
       const int row = (MODE == 2 && t == 1) ? p.N + tile[0] * 64 + lane : tile[t] * 64 + lane;
       if (MODE != 1 || tile[t] < p.NT) {
 #pragma unroll
-        for (int m = 0; m < M; ++m) *P0_GLOBAL(float, &p.part[sliceBase + ((size_t)ks * M + m) * p.rowsTot + row]) = acc[t][m];
+        for (int m = 0; m < M; ++m) stf<true>(&p.part[sliceBase + ((size_t)ks * M + m) * p.rowsTot + row], acc[t][m]);
       }
     }
   }
@@ -766,7 +767,7 @@ __device__ __forceinline__ bool gemv_item(const GemvP& p, int bx, int by, float*
         const bool live = MODE != 1 || tile[t] < p.NT;
 #pragma unroll
         for (int m = 0; m < M; ++m)
-          v[j][t][m] = live ? *P0_GLOBAL(const float, &p.part[sliceBase + ((size_t)s * M + m) * p.rowsTot + row]) : 0.0f;
+          v[j][t][m] = live ? ldf<true>(&p.part[sliceBase + ((size_t)s * M + m) * p.rowsTot + row]) : 0.0f;
       }
     }
 #pragma unroll

@@ -111,6 +111,10 @@ int p0_open(int device) {
     set_error("p0_open: no HIP device %d (%d visible)", device, e == hipSuccess ? n : 0);
     return P0_ENODEV;
   }
+  if (device >= kWsDevices) {
+    set_error("p0_open: device %d (this build keeps workspaces for devices 0 .. %d)", device, kWsDevices - 1);
+    return P0_ENODEV;
+  }
   P0_HIP(hipSetDevice(device), "p0_open");
   P0_HIP(hipGetDeviceProperties(&c.prop, device), "p0_open");
   if (std::strncmp(c.prop.gcnArchName, "gfx950", 6) != 0) {
@@ -120,10 +124,6 @@ int p0_open(int device) {
   P0_HIP(hipStreamCreate(&c.own), "p0_open");   // default priority
   P0_HIP(hipEventCreate(&c.ev0), "p0_open");
   P0_HIP(hipEventCreate(&c.ev1), "p0_open");
-  if (device >= kWsDevices) {
-    set_error("p0_open: device %d (this build keeps workspaces for devices 0 .. %d)", device, kWsDevices - 1);
-    return P0_ENODEV;
-  }
   if (!g_ws_part[device]) {
     P0_HIP(hipExtMallocWithFlags((void**)&g_ws_part[device], kPartBytes, hipDeviceMallocUncached), "p0_open: workspace");
   }
