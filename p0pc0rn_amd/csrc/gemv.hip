@@ -56,9 +56,10 @@ static Plan plan(int M, int NT, int epi, int nsplit, int kPer) {
   const int slots = pl.mode == 1 ? (NT + 1) / 2 : NT;
   pl.rowsTot = (epi == P0_EPI_GEGLU ? 2 : 1) * NT * 64;
   const int Gs = kPer / 32;
-  // K shares per slot and split: enough waves for the chip, but at least g_min_gpw groups each (a geglu slot streams
-  // the gate and the up tile, so it counts twice)
-  const int work = pl.mode == 2 ? 2 * g_target_waves : g_target_waves;
+  // K shares per slot and split: enough waves for the chip, but at least g_min_gpw groups each. A geglu slot streams
+  // the gate and the up tile and counts twice at M = 1 and from M = 12 on; at M = 2-8 the extra K-slices' partials cost
+  // more than the parallelism gains (measured on the E2B gate_up: 14-20 us per launch against 20-26)
+  const int work = pl.mode == 2 && (M == 1 || M >= 12) ? 2 * g_target_waves : g_target_waves;
   int kws = (work + slots * nsplit - 1) / (slots * nsplit);
   const int kws_max = Gs / g_min_gpw > 1 ? Gs / g_min_gpw : 1;
   if (kws > kws_max) kws = kws_max;
