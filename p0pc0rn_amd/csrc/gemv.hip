@@ -61,6 +61,10 @@ static Plan plan(int M, int NT, int epi, int nsplit, int kPer) {
   // more than the parallelism gains (measured on the E2B gate_up: 14-20 us per launch against 20-26)
   const int work = pl.mode == 2 && (M == 1 || M >= 12) ? 2 * g_target_waves : g_target_waves;
   int kws = (work + slots * nsplit - 1) / (slots * nsplit);
+  // 12-16 x rows over several kPer splits (the E2B down projection): the splits already give the chip its workgroups,
+  // and K-slices would multiply the partials of every row; two waves per slot, K in one workgroup per split
+  // (measured at M = 12 / 16: 25-26 us per launch against 31-32)
+  if (M >= 12 && nsplit >= 4 && kws > 2) kws = 2;
   const int kws_max = Gs / g_min_gpw > 1 ? Gs / g_min_gpw : 1;
   if (kws > kws_max) kws = kws_max;
   if (kws < 1) kws = 1;
