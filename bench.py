@@ -10,7 +10,7 @@ lm_head 262144x2048 rms+softcap (tile max/argmax), the argmax over the 4096 tile
 words into the staging buffer = 121 GEMV ops + 3 others. Run per token both ways the library offers (the
 DecodeRunner analogue): planned once into a chain that runs as ONE persistent launch, and recorded as a graph of 124
 launches; the faster is the headline and both are reported (also the 121 GEMVs alone).
-Attention, norms and the PLE projections are not part of the step.
+Attention, norms and the PLE projections are not part of the step (config B counts the linears only).
 
 Also reported: the step's weight-streaming GB/s, config A (one 8192x2048 GEMV, weight ring of 32 copies), the
 verify pass at M = 5 and the M sweep {1, 2, 4, 8, 16} (config C), and the FLUX.2-klein (M=4608, config D) and
@@ -484,8 +484,8 @@ def main():
                          "counters")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py: this build measures one GPU; --gpus %d is not supported (the hot path runs on one MI355X, "
-              "see DESIGN.md for how it would shard)" % args.gpus, file=sys.stderr)
+        print("bench.py: this build measures one GPU; --gpus %d is not supported (the hot path runs on one MI355X; "
+              "sharding across GPUs is a design, not part of this build)" % args.gpus, file=sys.stderr)
         sys.exit(2)
 
     from p0pc0rn_amd import capi as c
