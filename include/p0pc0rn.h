@@ -214,7 +214,10 @@ int p0_q4_dequant(const void* w, int64_t w_off, int64_t N, int64_t K, float* out
  * knob 3: most waves sharing one tile slot's K range inside a workgroup (default 16, at most 16; 8 when M > 2);
  * knob 4: fewest x rows M from which a gemvM call outside a chain runs on the matrix cores (default 2, i.e. every
  *         M > 1; 17: never, the fp32 VALU kernel).
- * value <= 0 only queries. Returns the previous value, or -1 for an unknown knob. */
+ * knob 5: K-slices per split of a q8g64s.t64 gemv (M = 1, splits of 1024-3072 k) across workgroups (default 0: planned,
+ *         up to ~192 workgroups with at least 8 groups of 64 k a slice; a negative value restores the plan).
+ * value <= 0 only queries (knob 5: value < 0 restores its plan). Returns the previous value, or -1 for an unknown
+ * knob. */
 int p0_gemv_tune(int knob, int value);
 
 /* ---- GEMV chains: a decode step's GEMVs in ONE persistent launch (engine/llm/drunner.js:1-8, 83-101) ------------- */

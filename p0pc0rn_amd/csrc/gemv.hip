@@ -42,6 +42,7 @@ static int g_two_tiles_min_nt = 1024;   // output tiles from which a wave stream
 static int g_min_gpw = 2;               // fewest q4 groups a wave streams when K is split
 static int g_max_kw = 16;               // most waves that share one tile slot's K-slice inside a workgroup
 static int g_mf_min_m = 2;              // fewest x rows a standalone GEMV-M runs on MFMA (17: never)
+static int g_q8_slices = 0;             // q8g64s.t64 GEMV at M = 1: K-slices per split across workgroups (0: planned)
 static int g_pipe_mf_min_m = 3;         // fewest x rows a pipelined chain does its slot arithmetic on MFMA (6: never)
 
 struct Plan {
@@ -536,8 +537,25 @@ static int launch_q8(GemvP& p, int M, const char* op) {
   // q8_gemv1_kernel: 16 waves per (tile, split), for splits of 1024-3072 k (16-48 groups; a split of 4 groups, the
   // E2B pleg projection's 256 k, runs faster on the 4-wave kernel: 3.9 against 4.9 us)
   if (M == 1 && p.kPer >= 1024 && p.kPer <= 3072) {
-    hipLaunchKernelGGL(q8_gemv1(p.epi == P0_EPI_GEGLU), dim3((unsigned)p.NT, (unsigned)p.nsplit), dim3(1024), q8_gemv1_lds_bytes(), ctx().cur,
-                       p);
+    // K-slices across workgroups (p.nks) when the tiles and splits leave most CUs idle: up to ~192 workgroups, at
+    // least 8 groups (512 k) a slice (measured at the E2B 8-bit shapes: 6.2-9.3 us per launch against 6.9-10.9 with
+    // one workgroup per split; p0_gemv_tune knob 5 sets the count)
+    const int gsplit = p.kPer / 64;
+    const int wgs = p.NT * p.nsplit;
+    int nks = g_q8_slices > 0 ? g_q8_slices : std::min(std::max(gsplit / 8, 1), (192 + wgs - 1) / wgs);
+    if (nks > gsplit) nks = gsplit;
+    p.gps = (gsplit + nks - 1) / nks;
+    p.nks = (gsplit + p.gps - 1) / p.gps;   // every slice holds at least one group
+    p.rowsTot = (p.epi == P0_EPI_GEGLU ? 2 : 1) * p.NT * 64;
+    p.part = ctx().part;
+    p.cnt = ctx().counters;
+    if (p.nks > 1 && ((size_t)p.nsplit * p.nks * p.rowsTot > ctx().part_floats ||
+                      (size_t)p.nsplit * p.NT > ctx().n_counters)) {
+      p.nks = 1;
+      p.gps = gsplit;
+    }
+    hipLaunchKernelGGL(q8_gemv1(p.epi == P0_EPI_GEGLU), dim3((unsigned)p.NT, (unsigned)(p.nsplit * p.nks)), dim3(1024),
+                       q8_gemv1_lds_bytes(), ctx().cur, p);
     P0_LAUNCHED(op);
     return P0_OK;
   }
@@ -788,10 +806,11 @@ extern "C" int p0_q4_gemvM(const p0_gemvm_args_t* a, int32_t* nsplit_out) {
 // tiles, 2 = fewest groups per wave, 3 = most waves per tile slot in a workgroup. Returns the previous value.
 extern "C" int p0_gemv_tune(int knob, int value) {
   int* t = knob == 0 ? &g_target_waves : knob == 1 ? &g_two_tiles_min_nt : knob == 2 ? &g_min_gpw
-         : knob == 3 ? &g_max_kw : knob == 4 ? &g_mf_min_m : nullptr;
+         : knob == 3 ? &g_max_kw : knob == 4 ? &g_mf_min_m : knob == 5 ? &g_q8_slices : nullptr;
   if (!t) return -1;
   const int old = *t;
   if (value > 0) *t = knob == 3 && value > 16 ? 16 : value;
+  else if (knob == 5 && value < 0) *t = 0;   // the planned slice count again
   return old;
 }
 

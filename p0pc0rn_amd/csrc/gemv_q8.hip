@@ -128,6 +128,10 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(GemvP p) {
 // each round of 16), so a split's records (at most 48 groups of 3072 k) are in flight in one to three rounds, the
 // first round's latency overlapping the x' staging; the kernel above, 4 waves that load their groups one after another, spends a memory round trip per group.
 // The group sums add the 64 x' of a group in k order; the waves' sums are added in wave order (deterministic).
+// With p.nks > 1 a split's groups are cut into p.nks slices of consecutive groups, one workgroup each (blockIdx.y =
+// split * nks + slice); wave 0 writes the slice's row sums to the uncached split-K workspace with device-scope stores
+// and counts the arrival, and the last workgroup of the (split, tile) adds the slices' partials in slice order and
+// runs the epilogue (the GEMV's split-K protocol, gemv_item).
 template <int T>   // 2: a geglu (the gate tile and its up tile), else 1
 __global__ __launch_bounds__(kQ81Threads) void q8_gemv1_kernel(GemvP p) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
@@ -135,9 +139,12 @@ __global__ __launch_bounds__(kQ81Threads) void q8_gemv1_kernel(GemvP p) {
   float* xsum = xs + kQ81MaxK;            // [kQ81MaxK / 64] its group sums
   float* red = xsum + kQ81MaxK / 64;      // [wave][tile][64 rows]
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int tile0 = blockIdx.x, split = blockIdx.y;
+  const int tile0 = blockIdx.x, split = (int)blockIdx.y / p.nks, ks = (int)blockIdx.y - split * p.nks;
   const int64_t tiles[2] = {tile0, tile0 + (T == 2 ? p.NT : 0)};
-  const int k0s = split * p.kPer, k1s = min(p.K, k0s + p.kPer), ng = (k1s - k0s) >> 6, g0 = k0s >> 6;
+  // this workgroup's slice of the split: groups [gs0, gs0 + ng) (p.gps groups of 64 k a slice)
+  const int sk0 = split * p.kPer, sk1 = min(p.K, sk0 + p.kPer);
+  const int gs0 = (sk0 >> 6) + ks * p.gps, gs1 = min(sk1 >> 6, gs0 + p.gps);
+  const int k0s = gs0 * 64, k1s = gs1 * 64, ng = gs1 - gs0, g0 = gs0;
   constexpr int GW = kQ81G / T;   // groups per wave and round (the registers of 2 tile-groups)
   float acc[2] = {0.0f, 0.0f};
   for (int r0 = 0; r0 < ng; r0 += kQ81Waves * GW) {
@@ -201,6 +208,40 @@ __global__ __launch_bounds__(kQ81Threads) void q8_gemv1_kernel(GemvP p) {
     float v = red[t * 64 + lane];
     for (int w = 1; w < kQ81Waves; ++w) v += red[(w * 2 + t) * 64 + lane];
     tot[t] = v;
+  }
+  if (p.nks > 1) {
+    // rows of the (split, slice) partials: the tile's 64 rows, and for a geglu its up rows at N + ...
+    const size_t base = (size_t)blockIdx.y * p.rowsTot;
+#pragma unroll
+    for (int t = 0; t < T; ++t) stf<true>(&p.part[base + (t ? p.N : 0) + tile0 * 64 + lane], tot[t]);
+    __builtin_amdgcn_s_waitcnt(0);   // the partials (uncached memory) are written before the arrival count
+    unsigned last = 0;
+    if (lane == 0) {
+      auto* c = P0_GLOBAL(unsigned, p.cnt + (size_t)split * p.NT + tile0);
+      last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(p.nks - 1);
+      if (last) __hip_atomic_exchange(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // leave it at zero
+    }
+    if (!__builtin_amdgcn_readfirstlane(last)) return;
+    // the slices' partials, loaded 8 slices at a time and added in slice order
+    const size_t sbase = (size_t)split * p.nks * p.rowsTot;
+    float sum[2] = {0.0f, 0.0f};
+    for (int s0 = 0; s0 < p.nks; s0 += 8) {
+      float v[8][2];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int sl = min(s0 + j, p.nks - 1);   // past the last slice: re-read it (in bounds, not added)
+#pragma unroll
+        for (int t = 0; t < T; ++t) v[j][t] = ldf<true>(&p.part[sbase + (size_t)sl * p.rowsTot + (t ? p.N : 0) + tile0 * 64 + lane]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < p.nks) {
+#pragma unroll
+          for (int t = 0; t < T; ++t) sum[t] += v[j][t];
+        }
+    }
+    tot[0] = sum[0];
+    tot[1] = sum[1];
   }
   epilogue<false>(p, split, 0, tile0, lane, tot[0], tot[1]);
 }

@@ -186,3 +186,15 @@ def test_chain_tune_knobs_round_trip():
     assert capi.chain_tune(7, 1) == 0 and capi.chain_tune(7, -1) == 1
     assert capi.chain_tune(8, -1) == 1 and capi.chain_tune(8, 0) == 1 and capi.chain_tune(8, -1) == 0
     assert capi.chain_tune(8, 1) == 0 and capi.chain_tune(8, -1) == 1
+
+
+def test_gemv_tune_q8_slices_knob():
+    """knob 5 (q8 K-slices) answers without a device: 0 = planned, a positive count sets it, a negative value restores
+    the plan; knob 6 does not exist"""
+    old = capi.gemv_tune(5)
+    assert old >= 0
+    assert capi.gemv_tune(5, 3) == old and capi.gemv_tune(5) == 3
+    assert capi.gemv_tune(5, -1) == 3 and capi.gemv_tune(5) == 0
+    if old > 0:
+        capi.gemv_tune(5, old)
+    assert capi.gemv_tune(6, 1) == -1

@@ -61,6 +61,20 @@ def test_q8_kshipped_shapes(dev, pro, epi, K, kPer):
         v.free()
 
 
+
+@pytest.mark.parametrize("slices", [1, 2, 5, 24])
+@pytest.mark.parametrize("pro,epi,K,kPer", [("rms", "geglu", 1536, 0), ("raw", "store", 6144, 2048)])
+def test_q8_k_slices_across_workgroups(dev, slices, pro, epi, K, kPer):
+    """the 16-wave q8 GEMV with each split's K cut into slices across workgroups (p0_gemv_tune knob 5: one workgroup
+    per split, two, five uneven slices, one group a slice), the last arriving workgroup adding the slices' partials
+    through the uncached workspace: the same checks as the shipped shapes"""
+    old = capi.gemv_tune(5, slices)
+    try:
+        test_q8_kshipped_shapes(dev, pro, epi, K, kPer)
+    finally:
+        capi.gemv_tune(5, old if old > 0 else -1)
+
+
 @pytest.mark.parametrize("M,epi", [(5, "store"), (16, "store"), (3, "softcap")])
 def test_q8_gemvM_matches_oracle(dev, M, epi):
     N, K = 256, 2048
