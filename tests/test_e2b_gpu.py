@@ -31,9 +31,26 @@ def _check(got, want, what):
     assert r <= 1e-3 and r <= 2e-5, (what, r)
 
 
+def _device_fill(b, host, what):
+    """the weights the GPU holds, read back, after checking them against the oracle's fill of the same seed: the code
+    words bit for bit; the fp16 scales equal or one fp16 step apart, in a small fraction of the groups (the device's
+    float64 log / cos and libm's may round a scale's last bit differently), and every min exactly -8 x its scale. The
+    oracle then runs on the exact bytes the GPU reads."""
+    dev = b.read(np.uint8, host.size)
+    d, h = dev.reshape(-1, 1280), host.reshape(-1, 1280)
+    assert np.array_equal(d[:, :1024], h[:, :1024]), what + ": code words differ from the oracle's fill"
+    ds, hs = d[:, 1024:].view(np.uint16)[:, 0::2], h[:, 1024:].view(np.uint16)[:, 0::2]
+    diff = np.abs(ds.astype(np.int32) - hs.astype(np.int32))   # positive fp16: adjacent values, adjacent bit patterns
+    assert diff.max() <= 1 and np.mean(diff != 0) < 1e-3, (what, int(diff.max()), float(np.mean(diff != 0)))
+    mins = d[:, 1024:].view(np.uint16)[:, 1::2]
+    want = (np.float32(-8) * ds.view(np.float16).astype(np.float32)).astype(np.float16).view(np.uint16)
+    assert np.array_equal(mins, want), what + ": min != -8 x scale"
+    return dev
+
+
 class E2B:
-    """two decode layers + the head at bench.py's shapes, M rows; symmetric BASELINE weights filled on the device and,
-    bit-identically, on the host by the oracle's copy of the same counter hash. bounded: bench.py's weight scales and
+    """two decode layers + the head at bench.py's shapes, M rows; symmetric BASELINE weights filled on the device and
+    on the host by the oracle's copy of the same counter hash (the oracle then runs on the device's bytes read back). bounded: bench.py's weight scales and
     sign-alternating norm weights, which keep every activation O(1) (|x'| < 255: an M > 1 chain then runs every op on
     the matrix cores); else sigma 0.02 everywhere, whose activations grow ~4x per op (later M > 1 ops take the VALU
     fallback)."""
@@ -47,13 +64,13 @@ class E2B:
             for i, (k, (n, kk)) in enumerate(shapes.items()):
                 s = seed * 101 + l * 16 + i
                 sig = float(gain[k] / np.sqrt(21.5 * kk)) if bounded else 0.02
-                self.w_host[(l, k)] = O.fill_q4_sym(n, kk, s, sig)
                 b = capi.Buffer(n // 64 * kk // 32 * 1280)
                 capi.fill_q4_sym(b, n, kk, s, sig)
                 self.w_dev[(l, k)] = b
-        self.w_host["head"] = O.fill_q4_sym(V, D, seed * 101 + 99, 0.02)
+                self.w_host[(l, k)] = _device_fill(b, O.fill_q4_sym(n, kk, s, sig), f"weights {l} {k}")
         self.w_dev["head"] = capi.Buffer(V // 64 * D // 32 * 1280)
         capi.fill_q4_sym(self.w_dev["head"], V, D, seed * 101 + 99, 0.02)
+        self.w_host["head"] = _device_fill(self.w_dev["head"], O.fill_q4_sym(V, D, seed * 101 + 99, 0.02), "head")
         self.x = O.fill_randn(M * D, seed)[0]
         self.nw = np.linspace(0.8, 1.2, D).astype(np.float32)
         if bounded:
