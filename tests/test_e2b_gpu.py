@@ -10,7 +10,8 @@ standalone launches; config C at M = 5 (the verify pass) both ways, and the M sw
 calls at the qkv and gate_up shapes. Each op is checked against the oracle run on the input that op read on the GPU
 (its predecessor's output, read back), after every output was NaN-filled; the head's 4096 tile maxima are checked
 against the oracle and its argmax indices by their defining property over the GPU's own logits.
-Tolerance: relative L2 <= 1e-3 (BASELINE) and this build's fp32 bar of 2e-5.
+Tolerance: relative L2 <= 1e-3 (BASELINE) and 2e-6 here, tighter than this build's general fp32 bar of 2e-5 since the
+oracle runs on the exact weight bytes the GPU holds (read back); the largest seen is 5e-7.
 """
 import numpy as np
 import pytest
@@ -28,7 +29,7 @@ def _check(got, want, what):
     r = rel_l2(got, want)
     print(f"{what}: rel_l2 {r:.3e} (rms {float(np.sqrt(np.mean(np.square(want, dtype=np.float64)))):.3g})", flush=True)
     assert np.all(np.isfinite(got)), what + ": non-finite output"
-    assert r <= 1e-3 and r <= 2e-5, (what, r)
+    assert r <= 1e-3 and r <= 2e-6, (what, r)
 
 
 def _device_fill(b, host, what):
