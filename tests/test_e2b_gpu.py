@@ -113,8 +113,9 @@ class E2B:
         """sets every rms op's rstd slots, the head's included, to 1 / sqrt(mean(x^2) + 1e-6) over each row that op
         reads on the GPU, as the model's RMSNorm computes them, so that activations stay O(1) through every layer
         (with fixed slots the geglu's square makes the magnitude an unstable balance: it collapses towards 0 within a
-        few layers). One slot per run of the chain ch: its arithmetic is fixed, so a run reproduces every op before
-        the slot just set bit for bit, and the next slot is computed from that run's output."""
+        few layers). One slot per run of ch (a chain, or a recording: anything with run / replay): its arithmetic is
+        fixed, so a run reproduces every op before the slot just set bit for bit, and the next slot is computed from
+        that run's output."""
         M = self.M
 
         def rstd(x):
@@ -124,8 +125,11 @@ class E2B:
         self.st[self.rms_off(0)::2][:M] = rstd(self.x)
         self.dev["st"].upload(self.st)
         for j in range(1, 2 * self.L + 1):
-            ch.run()
-            assert not ch.status()
+            if hasattr(ch, "replay"):
+                ch.replay()
+            else:
+                ch.run()
+                assert not ch.status()
             src = ("o", (j - 1) // 2) if j % 2 else ("dn", j // 2 - 1)   # gate_up reads o, qkv / head a down partial
             r = rstd(self.out[src].read(np.float32, M * D))
             assert np.all((r > 0.01) & (r < 100)), (j, r)   # every op's input stays O(1)
@@ -214,31 +218,40 @@ class E2B:
         assert np.array_equal(want[0::2], np.argmax(lg, axis=1).astype(np.uint32)), what + ": argmax of the logits"
         print(what, "argmax", want[0::2].tolist(), flush=True)
 
-    def check(self, what):
+    def check(self, what, layers=None, head_rows=None):
+        """every op (or those of `layers` and the head) against the oracle on the input it read on the GPU; head_rows:
+        the head's first head_rows rows only (a multiple of 64: its logits and tile maxima; rows are independent)"""
         got = {k: self.out[k].read(np.float32, n) for k, n in self.out_len.items()}
         gmx = self.dev["mx"].read(np.float32, self.mx_len)
         M = self.M
         hostbuf = {"x": self.x, "st": self.st, "nw": self.nw}
+        NT, HR = V // 64, head_rows or V
         for name, wk, xk, f in self.fields({k: 0 for k in list(self.out_len) + ["x", "st", "nw", "mx"]}, self.w_host):
+            if layers is not None and name != "head" and name[1] not in layers:
+                continue
             xin = np.ascontiguousarray(hostbuf["x"] if xk == "x" else got[xk], np.float32)
             y = np.full(self.out_len[name], np.nan, np.float32)
-            mx = self.mx.copy()
             f = dict(f, w=self.w_host[wk].ctypes.data, x=xin.ctypes.data, y=y.ctypes.data, norm=self.nw.ctypes.data)
             if name == "head":
-                f.update(stat=mx.ctypes.data, mx=mx.ctypes.data)
+                # the rstd slots past the tile pairs (a softcap GEMV at M = 1 reads them from mx, as the reference's
+                # gemv does); the oracle writes the first HR rows' tile pairs at the front, as M rows of HR / 64
+                mx = self.mx.copy()
+                f.update(w_rows=HR, N=HR, stat=mx.ctypes.data, mx=mx.ctypes.data)
             else:
                 f["stat"] = self.st.ctypes.data if "stat" in f else None
             (O.q4_gemv if M == 1 else O.q4_gemvM)((capi.gemv_args if M == 1 else capi.gemvm_args)(**f))
-            _check(got[name], y, f"{what} {name}")
+            if name == "head":
+                _check(got[name].reshape(M, V)[:, :HR], y.reshape(M, V)[:, :HR], f"{what} head rows < {HR}")
+            else:
+                _check(got[name], y, f"{what} {name}")
         # the head's per-tile (max, argmax): maxima against the oracle, indices by their defining property over the
         # GPU's own logits (the first row of the tile holding the tile's largest value)
-        NT = V // 64
         lg = got["head"].reshape(M, NT, 64)
         gm = gmx[:2 * NT * M:2].reshape(M, NT)
         gi = gmx[1:2 * NT * M:2].view(np.uint32).reshape(M, NT)
-        wm = mx[:2 * NT * M:2].reshape(M, NT)
-        _check(gm, wm, what + " tile maxima")   # the maxima are logits: the logits' bar
-        print(what, "tile maxima: largest |diff|", float(np.max(np.abs(gm - wm))), flush=True)
+        wm = mx[:2 * M * (HR // 64):2].reshape(M, HR // 64)
+        _check(gm[:, :HR // 64], wm, what + " tile maxima")   # the maxima are logits: the logits' bar
+        print(what, "tile maxima: largest |diff|", float(np.max(np.abs(gm[:, :HR // 64] - wm))), flush=True)
         want_i = (np.argmax(lg, axis=2) + np.arange(NT)[None, :] * 64).astype(np.uint32)
         assert np.array_equal(gi, want_i), what + ": tile argmax"
         assert np.array_equal(gm, np.take_along_axis(lg, (gi % 64).astype(np.int64)[:, :, None], 2)[:, :, 0])
@@ -360,6 +373,36 @@ def test_config_c_verify_chain_m8_m16(dev, M, data):
         gmx = s.dev["mx"].read(np.float32, s.mx_len)
         want = np.asarray(O.argmaxM(gmx, V // 64, M), np.uint32).ravel()
         assert np.array_equal(s.dev["arg"].read(np.uint32, 2 * M), want)
+    finally:
+        s.free()
+
+
+@pytest.mark.parametrize("M,way", [(5, "chain"), (5, "graph"), (16, "chain")])
+def test_config_c_full_depth(dev, M, way):
+    """config C at full depth, as bench.py times the verify pass: 30 layers + the head (M rows), with the token's tail
+    (the rstd copies, argmaxM, the result copy), as one chain launch (the pipelined kernel at M = 5, the wide kernel at
+    M = 16) or as a recording of standalone launches. The rstd slots are calibrated from the path's own activations
+    first, so every layer computes on O(1) data and every M > 1 op runs on the matrix cores. Checked against the
+    oracle on the inputs they read: every op of the 30 layers, the head (at M = 16 its first 65536 rows and their tile
+    maxima: the oracle's cost grows with M) and the whole tail"""
+    s = E2B(M, layers=30, seed=20 + M, bounded=True)
+    try:
+        run = (capi.chain if way == "chain" else capi.record)(lambda: s.enqueue(tail=True))
+        if way == "chain":
+            info = run.info()
+            print("chain", info, flush=True)
+            assert info["n_ops"] == 4 * 30 + M + 3 and info["passes"] == 1
+        s.calibrate(run)
+        print("head rstd", s.rstd_head.tolist(), flush=True)
+        s.reset(tail=True)
+        if way == "chain":
+            run.run()
+            assert not run.status()
+        else:
+            run.replay()
+        s.check(f"config C full depth M={M} {way}", head_rows=65536 if M > 8 else None)
+        s.check_tail(f"config C full depth M={M} {way}")
+        run.free()
     finally:
         s.free()
 
