@@ -63,11 +63,13 @@ def test_q8_kshipped_shapes(dev, pro, epi, K, kPer):
 
 
 @pytest.mark.parametrize("slices", [1, 2, 5, 24])
-@pytest.mark.parametrize("pro,epi,K,kPer", [("rms", "geglu", 1536, 0), ("raw", "store", 6144, 2048)])
+@pytest.mark.parametrize("pro,epi,K,kPer", [("rms", "geglu", 1536, 0), ("raw", "store", 6144, 2048),
+                                            ("raw", "store", 5120, 2048)])
 def test_q8_k_slices_across_workgroups(dev, slices, pro, epi, K, kPer):
     """the 16-wave q8 GEMV with each split's K cut into slices across workgroups (p0_gemv_tune knob 5: one workgroup
-    per split, two, five uneven slices, one group a slice), the last arriving workgroup adding the slices' partials
-    through the uncached workspace: the same checks as the shipped shapes"""
+    per split, two, five uneven slices, two groups a slice), the last arriving workgroup adding the slices' partials
+    through the uncached workspace: the same checks as the shipped shapes. K = 5120 in splits of 2048 leaves a last
+    split of 16 groups, whose trailing slices hold no group (they add zeros and still count their arrival)"""
     old = capi.gemv_tune(5, slices)
     try:
         test_q8_kshipped_shapes(dev, pro, epi, K, kPer)
