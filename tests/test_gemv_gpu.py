@@ -202,11 +202,14 @@ def test_gemv_split_k_workspace_across_reopen(dev):
     _check(runs[-1][idx], want[idx], "split-K after reopen")
 
 
-@pytest.mark.parametrize("M,epi,K,kPer", [(3, "store", 4096, 2048), (5, "geglu", 2048, 0), (16, "store", 4096, 2048)])
+@pytest.mark.parametrize("M,epi,K,kPer", [(3, "store", 4096, 2048), (5, "geglu", 2048, 0), (16, "store", 4096, 2048),
+                                          (4, "store", 3168, 1024), (1, "store", 3168, 1024)])
 def test_gemvM_many_k_slices(dev, M, epi, K, kPer):
     """gemvM (matrix cores) with K in many slices: the last workgroup to arrive loads the slices' partials of every x
-    row in batches (fewer slices per batch as M grows) and adds them in slice order; the oracle's values"""
-    c = Case(M, 256, K, "rms", epi, kPer=kPer, seed=29 + M, gemvM=True)
+    row in batches (fewer slices per batch as M grows) and adds them in slice order; the oracle's values. K = 3168 in
+    splits of 1024 leaves a last split of 3 groups, whose later slices hold no group (they store zeros and still count
+    their arrival); at M = 1 the same through gemv"""
+    c = Case(M, 256, K, "rms", epi, kPer=kPer, seed=29 + M, gemvM=M > 1)
     old = [capi.gemv_tune(k) for k in range(4)]
     try:
         for k, v in enumerate((100000, 100000, 1, 2)):
