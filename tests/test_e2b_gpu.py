@@ -377,6 +377,37 @@ def test_config_c_verify_chain_m8_m16(dev, M, data):
         s.free()
 
 
+@pytest.mark.parametrize("M", [8, 16])
+def test_config_c_row_group_passes(dev, M):
+    """config C's verify chain at 8 and 16 rows (two layers + the head, argmaxM) with the wide kernel off
+    (p0_chain_tune knob 12 = 0): pipelined passes over row groups of at most 5 rows, each pass's staged x', 4-split down
+    projection and softcap tile maxima at their row group's offsets, every op against the oracle"""
+    s = E2B(M, seed=40 + M, bounded=True)
+    old = capi.chain_tune(12, 0)
+    try:
+        def token():
+            s.enqueue()
+            capi.argmaxM(s.dev["mx"], V // 64, M, s.dev["arg"])
+        ch = capi.chain(token)
+    finally:
+        capi.chain_tune(12, old)
+    try:
+        info = ch.info()
+        print("chain", info, flush=True)
+        assert info["passes"] == -(-M // 5) and info["passes"] > 1
+        s.reset()
+        s.dev["arg"].fill_u32(NAN)
+        ch.run()
+        assert not ch.status()
+        s.check(f"config C M={M} row-group passes")
+        gmx = s.dev["mx"].read(np.float32, s.mx_len)
+        want = np.asarray(O.argmaxM(gmx, V // 64, M), np.uint32).ravel()
+        assert np.array_equal(s.dev["arg"].read(np.uint32, 2 * M), want)
+    finally:
+        ch.free()
+        s.free()
+
+
 @pytest.mark.parametrize("M,way", [(5, "chain"), (5, "graph"), (16, "chain")])
 def test_config_c_full_depth(dev, M, way):
     """config C at full depth, as bench.py times the verify pass: 30 layers + the head (M rows), with the token's tail
