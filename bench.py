@@ -15,7 +15,9 @@ Attention, norms and the PLE projections are not part of the step (config B coun
 Also reported: the step's weight-streaming GB/s, config A (one 8192x2048 GEMV, weight ring of 32 copies), the
 verify pass at M = 5 and the M sweep {1, 2, 4, 8, 16} (config C), and the FLUX.2-klein (M=4608, config D) and
 SANA-Video (M=32760, config E) dequant-GEMM TFLOP/s. All weights are synthetic symmetric int4 (codes uniform,
-scale |N(0, 0.02)| fp16, min = -8 scale) filled on the device; activations fp16-valued N(0, 1).
+scale |N(0, 0.02)| fp16, min = -8 scale) filled on the device; activations fp16-valued N(0, 1). The decode and verify
+layers take weight scales that keep each op's output at its input's magnitude, and each timed path runs on rstd slots
+calibrated from its own activations (Step.calibrate), so every layer computes on O(1) values.
 
 Timing: HIP events on the library's stream around back-to-back replays, inputs already resident in HBM.
 CPU baseline: the oracle's fp32 port of the reference's lgemv kernel (engine/llm/lops.js:60-88) on the host cores,
@@ -53,10 +55,11 @@ class Step:
         # Bounded activations. The weight scales keep each op's output at its input's magnitude (codes q - 8 have mean
         # square 21.5; the down projection makes up for the geglu's ~0.65), and the norm weights alternate in sign, so
         # that the codes' mean of -0.5 s does not pile up a common-mode component op after op. The rstd slots are
-        # fixed inputs (the model's RMSNorm sits outside the step), so the geglu's square makes the magnitude shrink
-        # layer by layer from O(1) towards 0 (a fixed slot cannot hold it at 1: that balance is unstable, and rounding
-        # differences between paths would grow into inf). Values never reach inf or NaN, so an M > 1 verify pass keeps
-        # its matrix-core path (it falls back to the VALU for |x'| >= 255) and every path runs what a model's step runs.
+        # inputs of the step (the model's RMSNorm sits outside it); calibrate() sets them before each timed path from
+        # that path's own activations, as the norm would, so every layer and the head compute on O(1) values (with
+        # fixed slots the geglu's square makes the magnitude collapse towards 0 within a few layers, and the later
+        # layers would compute on zeros). An M > 1 verify pass keeps its matrix-core path (it falls back to the VALU
+        # for |x'| >= 255) and every path runs what a model's step runs.
         # baseline_scales: BASELINE's |N(0, 0.02)| scales for every layer instead (the activations then grow ~4x per op,
         # and x' leaves the range of the matrix cores' fixed 2^8 staging from the second layer on)
         sigma = {"qkv": 1 / np.sqrt(21.5 * D), "o": 1 / np.sqrt(21.5 * D), "gu": 1 / np.sqrt(21.5 * D),
@@ -86,15 +89,23 @@ class Step:
         # rstd slots: a (pad, rstd) pair per row for each of the 2 per layer rms ops (qkv, gate_up), all 1 / sqrt(1 + eps)
         st = np.zeros(2 * M * 2 * LAYERS + 4, np.float32)
         st[1::2] = 1.0 / np.sqrt(1.0 + 1e-6)
+        self.st_host = st
         self.st = c.to_device(st)
+        # the activations, one set shared by every layer (as the model's step reuses its buffers), and per-layer twins
+        # that calibrate() runs the same ops on
         self.qkvp = c.Buffer(M * QKV * 4)
         self.obuf = c.Buffer(M * D * 4)
         self.mbuf = c.Buffer(M * MLP * 4)
         self.dpart = c.Buffer(4 * M * D * 4)
+        self.shared = {"qkvp": self.qkvp, "obuf": self.obuf, "mbuf": self.mbuf, "dpart": self.dpart}
+        self.twin = [{"qkvp": c.Buffer(M * QKV * 4), "obuf": c.Buffer(M * D * 4), "mbuf": c.Buffer(M * MLP * 4),
+                      "dpart": c.Buffer(4 * M * D * 4)} for _ in range(LAYERS)]
         self.logits = c.Buffer(M * VOCAB * 4)
         mx = np.zeros(M * (VOCAB // 64) * 2 + 2 * M + 4, np.float32)
         mx[M * (VOCAB // 64) * 2 + 1::2] = 1.0
+        self.mx_host = mx
         self.mx = c.to_device(mx)
+        self.rstd_head = np.ones(M, np.float32)
         self.mx_stat_off = M * (VOCAB // 64) * 2 + 1
         # the token's tail: the final norm's rstd per row (what the token copies into the head's stat slot), the
         # argmax words and the staging buffer the result is copied to
@@ -113,10 +124,60 @@ class Step:
         """stat_off of rms op j (qkv of layer l: j = 2 l, gate_up: 2 l + 1)"""
         return 2 * self.M * j + 1
 
+    def calibrate(self, graph=False, token=False):
+        """sets every rms op's rstd slots, the head's included (in the mx buffer and in the token's rsrc), to
+        1 / sqrt(mean(x^2) + 1e-6) over each row that op reads, as the model's RMSNorm computes them. They are computed
+        on a twin of the path about to be timed (a chain, or a recording if graph; with the token's tail if token)
+        whose ops write per-layer buffers, so that every op's input can be read after a run; the arithmetic does not
+        depend on the buffers' addresses, so the twin computes the timed path's values bit for bit. One slot per run
+        of the twin: a run reproduces every op before the slot just set, and the next slot is computed from its
+        output. Returns the rstd values set."""
+        c, M = self.c, self.M
+
+        def rstd(buf):
+            x = buf.read(np.float32, M * D).reshape(M, D).astype(np.float64)
+            return (1.0 / np.sqrt(np.mean(x * x, axis=1) + 1e-6)).astype(np.float32)
+
+        got = [rstd(self.x)]
+        self.st_host[self.rms_off(0)::2][:M] = got[0]
+        self.st.upload(self.st_host)
+        tw = (c.record if graph else c.chain)(lambda: self.ops(token=token, twin=True))
+        try:
+            for j in range(1, 2 * LAYERS + 1):
+                if graph:
+                    tw.replay()
+                else:
+                    tw.run()
+                    if tw.status():
+                        raise RuntimeError("a chain wait gave up during the rstd calibration")
+                # gate_up reads o's output; the next qkv, and the head, the first K-split partial of down
+                got.append(rstd(self.twin[(j - 1) // 2]["obuf"] if j % 2 else self.twin[j // 2 - 1]["dpart"]))
+                if j < 2 * LAYERS:
+                    self.st_host[self.rms_off(j)::2][:M] = got[-1]
+                    self.st.upload(self.st_host)
+        finally:
+            tw.free()
+        self.rstd_head = got[-1]
+        self.mx_host[self.mx_stat_off::2][:M] = got[-1]
+        self.mx.upload(self.mx_host)
+        r = np.zeros(2 * M, np.float32)
+        r[1::2] = got[-1]
+        self.rsrc.upload(r)
+        return np.concatenate(got)
+
+    def head_input_norm(self):
+        """per row, the rms of the head's input (the last layer's first down partial, in the shared buffer) times its
+        rstd slot after a timed path's runs: ~1 when the calibration carried over to the path"""
+        x = self.dpart.read(np.float32, self.M * D).reshape(self.M, D).astype(np.float64)
+        return [round(float(v), 4) for v in np.sqrt(np.mean(x * x, axis=1)) * self.rstd_head]
+
     def free_acts(self):
         for b in (self.x, self.st, self.qkvp, self.obuf, self.mbuf, self.dpart, self.logits, self.mx, self.rsrc,
                   self.arg, self.stage):
             b.free()
+        for t in self.twin:
+            for b in t.values():
+                b.free()
 
     # one projection, M = 1 through gemv, M > 1 through gemvM (the reference's decode / verify call pairs)
     def proj(self, w, n, k, x, y, pro="raw", epi="store", kPer=0, stat=None, stat_off=0, mx=None, ldx=0):
@@ -130,22 +191,24 @@ class Step:
                          epi=c.EPI[epi], y=y, stat=stat, stat_off=stat_off, stat_ld=2, norm=self.nw, mx=mx)
         return c.q4_gemvM(a)
 
-    def ops(self, only=None, token=False):
+    def ops(self, only=None, token=False, twin=False):
         """enqueue the step (or only one projection kind over all layers). Every op reads its predecessor's output:
         o the q rows of qkv, gate_up o's output, down gate_up's, the next layer's qkv (and the head) the first K-split
         partial of down. In the model a norm sits between some of them (normadd / rowstats, not part of the step);
-        their rstd slots are fixed inputs here. token: the whole token, with the tail of engine/llm/gemma4.js:503-511
-        (the rstd copy into the head's stat slot before the head, the argmax after it) and DecodeRunner.end's copy of
-        the result words (engine/llm/drunner.js:82-90)."""
+        their rstd slots are inputs here (calibrate). token: the whole token, with the tail of
+        engine/llm/gemma4.js:503-511 (the rstd copy into the head's stat slot before the head, the argmax after it) and
+        DecodeRunner.end's copy of the result words (engine/llm/drunner.js:82-90). twin: the layers write their own
+        buffers instead of the shared ones."""
         c, M = self.c, self.M
         for li in range(LAYERS):
-            self.ops_layer(li, ("qkv", "o", "gu", "down") if only is None else (only,))
+            self.ops_layer(li, ("qkv", "o", "gu", "down") if only is None else (only,), twin)
         if only in (None, "head"):
             if token:
                 for m in range(M):
                     c.copy(self.rsrc, (2 * m + 1) * 4, self.mx, (self.mx_stat_off + 2 * m) * 4, 4)
             # the head's rms slot lives in the mx buffer past the tile maxima (engine/llm/gemma4.js:505-508)
-            self.proj(self.head, VOCAB, D, self.dpart, self.logits, "rms", "softcap", stat=self.mx,
+            self.proj(self.head, VOCAB, D, (self.twin[-1] if twin else self.shared)["dpart"], self.logits, "rms",
+                      "softcap", stat=self.mx,
                       stat_off=self.mx_stat_off, mx=self.mx)
             if token:
                 if M == 1:
@@ -154,22 +217,23 @@ class Step:
                     c.argmaxM(self.mx, VOCAB // 64, M, self.arg)
                 c.copy(self.arg, 0, self.stage, 0, 8 * M)
 
-    def ops_layer(self, li, kinds):
-        """enqueue the projections `kinds` of layer li"""
+    def ops_layer(self, li, kinds, twin=False):
+        """enqueue the projections `kinds` of layer li (twin: on the layer's own buffers)"""
         t = self.layers[li]
+        a = self.twin[li] if twin else self.shared
+        xin = self.x if li == 0 else (self.twin[li - 1] if twin else self.shared)["dpart"]
         if "qkv" in kinds:
             b, n, k = t["qkv"]
-            self.proj(b, n, k, self.x if li == 0 else self.dpart, self.qkvp, "rms", stat=self.st,
-                      stat_off=self.rms_off(2 * li))
+            self.proj(b, n, k, xin, a["qkvp"], "rms", stat=self.st, stat_off=self.rms_off(2 * li))
         if "o" in kinds:
             b, n, k = t["o"]
-            self.proj(b, n, k, self.qkvp, self.obuf, "raw", kPer=2048, ldx=QKV)
+            self.proj(b, n, k, a["qkvp"], a["obuf"], "raw", kPer=2048, ldx=QKV)
         if "gu" in kinds:
             b, n, k = t["gu"]
-            self.proj(b, n, k, self.obuf, self.mbuf, "rms", "geglu", stat=self.st, stat_off=self.rms_off(2 * li + 1))
+            self.proj(b, n, k, a["obuf"], a["mbuf"], "rms", "geglu", stat=self.st, stat_off=self.rms_off(2 * li + 1))
         if "down" in kinds:
             b, n, k = t["down"]
-            self.proj(b, n, k, self.mbuf, self.dpart, "raw", kPer=2048)
+            self.proj(b, n, k, a["mbuf"], a["dpart"], "raw", kPer=2048)
 
     def step_bytes(self, only=None, token=False):
         M = self.M
@@ -224,6 +288,10 @@ def bench_decode(c, step, steps, warmup, breakdown=True):
     the chain's first dispatches after the weight fill run slower (the clock and the address translation caches settle
     over ~50 dispatches), and the headline is the steady state."""
     step.alloc(1)
+    # O(1) values in every shared buffer before the one-kind chains below read them: the token chain calibrated and
+    # run once
+    step.calibrate(token=True)
+    time_chain(c, lambda: step.ops(token=True), 1, 1)
     by_kind = {}
     for kind in ("qkv", "o", "gu", "down", "head") if breakdown else ():
         kms, _ = time_chain(c, lambda: step.ops(kind), 3, 20)
@@ -233,26 +301,52 @@ def bench_decode(c, step, steps, warmup, breakdown=True):
                          "us_per_launch": round(kms_graph * 1e3 / launches, 2),
                          "GBps_chain": round(step.step_bytes(kind) / (kms * 1e-3) / 1e9, 1),
                          "GBps": round(step.step_bytes(kind) / (kms_graph * 1e-3) / 1e9, 1)}
+    # each timed path on its own calibrated rstd slots (calibrate); after it, the head's input rows times their rstd
+    # (~1: the calibration carried over to the timed path)
+    step.calibrate(graph=True, token=True)
     ms_graph = time_recording(c, lambda: step.ops(token=True), warmup, steps)
+    norm = {"graph": step.head_input_norm()}
+    step.calibrate()
     ms_gemv, _ = time_chain(c, step.ops, warmup, steps)   # the 121 GEMVs alone, as one chain
+    norm["gemv_chain"] = step.head_input_norm()
+    r = step.calibrate(token=True)
     ms_chain, info = time_chain(c, lambda: step.ops(token=True), warmup, steps)
+    norm["chain"] = step.head_input_norm()
+    log("rstd slots of the token chain: %.3g - %.3g; head input x rstd after each timed path: %s"
+        % (r.min(), r.max(), norm))
     mode = "chain" if ms_chain <= ms_graph else "graph"
     out = {"ms": min(ms_chain, ms_graph), "mode": mode, "ms_chain": ms_chain, "ms_graph": ms_graph,
-           "ms_gemv_chain": ms_gemv, "bytes": step.step_bytes(token=True), "by_kind": by_kind, "chain": info}
+           "ms_gemv_chain": ms_gemv, "bytes": step.step_bytes(token=True), "by_kind": by_kind, "chain": info,
+           "rstd_range": [round(float(r.min()), 4), round(float(r.max()), 4)], "head_input_x_rstd": norm}
     step.free_acts()
     return out
 
 
-def bench_verify(c, step, Ms=(1, 2, 4, 5, 8, 16), graph=True):
+def bench_verify(c, step, Ms=(1, 2, 4, 5, 8, 16), graph=True, calibrate=True):
+    """a verify pass of M rows per M, as one chain launch and as a recording; calibrate: each path on rstd slots set
+    from its own activations (Step.calibrate), else on the fixed 1 / sqrt(1 + eps)"""
     res = {}
     for M in Ms:
         step.alloc(M)
+        norm = {}
+        if calibrate:
+            step.calibrate()
         ms_chain, _ = time_chain(c, step.ops, 3, 10)
-        ms_graph = time_recording(c, step.ops, 3, 10) if graph else float("inf")
+        if calibrate:
+            norm["chain"] = step.head_input_norm()
+        ms_graph = float("inf")
+        if graph:
+            if calibrate:
+                step.calibrate(graph=True)
+            ms_graph = time_recording(c, step.ops, 3, 10)
+            if calibrate:
+                norm["graph"] = step.head_input_norm()
         ms = min(ms_chain, ms_graph)
         res[str(M)] = {"ms_per_pass": round(ms, 4), "tok_per_s": round(M / (ms * 1e-3), 1),
                        "GBps": round(step.step_bytes() / (ms * 1e-3) / 1e9, 1),
                        "ms_chain": round(ms_chain, 4), "ms_graph": round(ms_graph, 4) if graph else None}
+        if calibrate:
+            res[str(M)]["head_input_x_rstd"] = norm
         step.free_acts()
     return res
 
@@ -507,7 +601,8 @@ def main():
                              "GBps": round(step_gbps, 1), "frac_hbm_peak": round(step_gbps / HBM_PEAK_GBPS, 4),
                              "mode": dec["mode"], "ms_chain": round(dec["ms_chain"], 4),
                              "ms_graph": round(dec["ms_graph"], 4), "ms_gemv_chain": round(dec["ms_gemv_chain"], 4),
-                             "chain": dec["chain"], "by_projection": dec["by_kind"]}}
+                             "chain": dec["chain"], "by_projection": dec["by_kind"],
+                             "rstd_slots_range": dec["rstd_range"], "head_input_x_rstd": dec["head_input_x_rstd"]}}
     if not args.no_extra:
         if not args.no_config_a:
             extra["config_a_gemv"] = bench_config_a(c)
@@ -520,7 +615,7 @@ def main():
     vb = () if args.no_extra else tuple(int(v) for v in args.verify_m_baseline.split(",") if v.strip())
     if vb:   # the same passes on BASELINE's weight scales (every layer |N(0, 0.02)|: activations grow ~4x per op)
         step = Step(c, baseline_scales=True)
-        extra["verify_sweep_baseline_scales"] = bench_verify(c, step, vb, graph=False)
+        extra["verify_sweep_baseline_scales"] = bench_verify(c, step, vb, graph=False, calibrate=False)
         log("verify sweep, baseline scales", extra["verify_sweep_baseline_scales"])
         step.free_weights()
     if args.calibrate:
@@ -582,6 +677,9 @@ def main():
                                "262144x2048 rms+softcap, argmax over 4096 tile maxima, result copy; q4g32a.t64 int4 "
                                "weights (0.625 B/weight), fp32 accumulate",
                    "weights_GB": round(step.weight_bytes / 1e9, 3),
+                   "activations": "fp16-valued N(0,1) input rows; every rms op's rstd slot calibrated per timed path "
+                                  "from that path's own activations, so all 30 layers and the head compute on O(1) "
+                                  "values",
                    "launches_per_step": 1 if dec["mode"] == "chain" else 124, "gemv_ops_per_step": 121,
                    "ops_per_token": 124,
                    "decode_path": dec["mode"],
