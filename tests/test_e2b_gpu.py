@@ -377,6 +377,36 @@ def test_config_c_verify_chain_m8_m16(dev, M, data):
         s.free()
 
 
+@pytest.mark.parametrize("M", [5, 16])
+def test_config_c_full_depth_many_runs(dev, M):
+    """the full-depth verify chain (30 layers + the head + the tail; the pipelined kernel at M = 5, the wide kernel at
+    M = 16) run 500 times back to back with no reset: no wait gives up, and the last run's logits, tile pairs, argmax
+    words and result copy equal the first run's bit for bit; rstd slots calibrated as in the full-depth test"""
+    s = E2B(M, layers=30, seed=60 + M, bounded=True)
+    try:
+        ch = capi.chain(lambda: s.enqueue(tail=True))
+        s.calibrate(ch)
+        s.reset(tail=True)
+        ch.run()
+        assert not ch.status()
+        V_ = s.out_len["head"]
+        first = (s.out["head"].read(np.uint32, V_).copy(), s.dev["mx"].read(np.uint32, s.mx_len).copy(),
+                 s.dev["arg"].read(np.uint32, 2 * M).copy(), s.dev["stage"].read(np.uint32, 2 * M).copy())
+        for block in range(5):
+            for _ in range(100):
+                ch.run()
+            assert not ch.status(), f"a wait gave up within runs {100 * block + 2}-{100 * block + 101}"
+            print(f"M={M}: runs up to {100 * block + 101}: no wait gave up", flush=True)
+        last = (s.out["head"].read(np.uint32, V_), s.dev["mx"].read(np.uint32, s.mx_len),
+                s.dev["arg"].read(np.uint32, 2 * M), s.dev["stage"].read(np.uint32, 2 * M))
+        for what, a, b in zip(("logits", "tile pairs", "argmax", "result copy"), first, last):
+            assert np.array_equal(a, b), what
+        s.check_tail(f"config C M={M} run 501")
+        ch.free()
+    finally:
+        s.free()
+
+
 @pytest.mark.parametrize("M", [8, 16])
 def test_config_c_row_group_passes(dev, M):
     """config C's verify chain at 8 and 16 rows (two layers + the head, argmaxM) with the wide kernel off
