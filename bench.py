@@ -563,6 +563,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--no-q8", action="store_true", help="leave out the q8g64s.t64 GEMV section")
     ap.add_argument("--no-extra", action="store_true", help="decode step only")
     ap.add_argument("--verify-m", default="1,2,4,5,8,12,16",
                     help="x rows of the verify passes timed (config C); empty: none")
@@ -623,8 +624,9 @@ def main():
     if not args.no_extra:
         extra["measured_peaks"] = measured_peaks(c)
         log("measured peaks", extra["measured_peaks"])
-        extra["q8_gemv_e2b_shapes"] = bench_q8(c)
-        log("q8 GEMV", extra["q8_gemv_e2b_shapes"])
+        if not args.no_q8:
+            extra["q8_gemv_e2b_shapes"] = bench_q8(c)
+            log("q8 GEMV", extra["q8_gemv_e2b_shapes"])
     if not args.no_gemm:
         extra["gemm_flux2_klein_M4608"] = bench_gemm(
             c, 4608, [("qkv", 9216, 3072), ("out", 3072, 3072), ("mlp_up", 9216, 3072), ("mlp_down", 3072, 9216)])
